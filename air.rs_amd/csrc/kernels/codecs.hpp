@@ -1,0 +1,82 @@
+// Device-side scalar codecs, bit-exact with the reference's CPU arithmetic.
+//
+// The library is compiled without fast-math: f32 division is correctly
+// rounded and f32 denormals are kept, which the quantizers below rely on.
+// Floating-point contraction is switched off inside every codec so each f32
+// operation rounds exactly once, as Rust's does.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace airkv {
+
+// f32 -> bf16 bits, round to nearest even; NaN keeps its high half with the
+// quiet bit set (half 2.7.1 bf16::from_f32, the conversion candle and the
+// reference use, src/pd_disagg.rs:66-69).
+__device__ __forceinline__ uint16_t bf16_rne(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    uint32_t lsb = (u >> 16) & 1u;
+    return (uint16_t)((u + 0x7FFFu + lsb) >> 16);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// F8E4M3::from_f32 (src/fp8.rs:54-91): -0.0 -> 0x00 (sign is x < 0), |x| >= 448
+// and exponent field 15 saturate to 0x7E, the mantissa rounds half-up and is
+// capped at 7 (no carry), subnormal results flush to signed zero, NaN -> 0x7F.
+__device__ __forceinline__ uint8_t fp8_encode(float x) {
+    if (x != x) return 0x7F;
+    uint32_t sign = x < 0.0f ? 0x80u : 0u;
+    uint32_t bits = __float_as_uint(x) & 0x7FFFFFFFu;
+    float a = __uint_as_float(bits);
+    if (a == 0.0f) return (uint8_t)sign;
+    if (a >= 448.0f) return (uint8_t)(sign | 0x7Eu);
+    int exp8 = (int)(bits >> 23) - 120;
+    if (exp8 <= 0) return (uint8_t)sign;
+    if (exp8 >= 15) return (uint8_t)(sign | 0x7Eu);
+    uint32_t mant3 = ((bits & 0x007FFFFFu) + (1u << 19)) >> 20;
+    mant3 = mant3 > 7u ? 7u : mant3;
+    return (uint8_t)(sign | ((uint32_t)exp8 << 3) | mant3);
+}
+
+// F8E4M3::to_f32 (src/fp8.rs:94-112): 0x7F is NaN, exponent field 0 decodes to
+// +0.0 whatever the sign, 0xFF decodes to -480.  Every value is an exact f32.
+__device__ __forceinline__ float fp8_decode(uint32_t b) {
+    b &= 0xFFu;
+    uint32_t e = (b >> 3) & 0xFu;
+    uint32_t bits = ((b & 0x80u) << 24) | (((b & 0x7Fu) << 20) + (120u << 23));
+    float v = __uint_as_float(bits);
+    v = e == 0u ? 0.0f : v;
+    return b == 0x7Fu ? __uint_as_float(0x7FC00000u) : v;
+}
+
+// Rust `f32::round` then saturating `as i8` after a clamp to +-127
+// (src/kv_cache.rs:69): NaN -> 0.
+__device__ __forceinline__ int8_t q8_code(float x, float inv) {
+#pragma clang fp contract(off)
+    float r = roundf(x * inv);
+    if (r != r) return 0;
+    r = r < -127.0f ? -127.0f : (r > 127.0f ? 127.0f : r);
+    return (int8_t)(int)r;
+}
+
+// Q8_0 scale from the group's absmax (src/kv_cache.rs:60-62).
+__device__ __forceinline__ float q8_scale(float max_abs) {
+#pragma clang fp contract(off)
+    return max_abs == 0.0f ? 1.0f : max_abs / 127.0f;
+}
+
+// FP8 group scale (Fp8Layer rule, src/fp8.rs:230-234).
+__device__ __forceinline__ float fp8_scale(float max_abs) {
+#pragma clang fp contract(off)
+    return max_abs < 1e-8f ? 1.0f : max_abs / 448.0f;
+}
+
+__device__ __forceinline__ uint8_t fp8_code(float x, float scale) {
+#pragma clang fp contract(off)
+    return fp8_encode(x / scale);
+}
+
+}  // namespace airkv

@@ -1,0 +1,154 @@
+// Reshape-and-cache: scatter new K/V rows into their pages, converting or
+// quantizing on the way (the paged replacement of the Tensor::cat append at
+// src/model.rs:569 and of save_layer's Q8 quantize, src/kv_cache.rs:307-315).
+//
+// One thread owns 8 consecutive head_dim elements of one (token, kv head) row
+// and handles both K and V: two 32-byte f32 loads each, one 32/16/8-byte store
+// each.  Consecutive threads cover a row, then the next head of the same
+// token, so the f32 source streams fully coalesced.  For INT8/FP8 the
+// scale_group/8 lanes of one scale group reduce their absmax with butterfly
+// shuffles; the group's first lane stores the f32 scale.
+#include <hip/hip_runtime.h>
+
+#include "../pool.hpp"
+#include "codecs.hpp"
+
+namespace airkv {
+namespace {
+
+constexpr int kThreads = 256;
+
+struct AppendArgs {
+    const float *k, *v;
+    const int64_t *slots;
+    int64_t n_rows;          // n_tokens * n_kv_heads
+    int64_t num_slots;       // num_blocks * block_size
+    int32_t n_kv_heads, head_dim, block_size, scale_group;
+    void *k_pages, *v_pages;
+    float *k_scales, *v_scales;
+    unsigned long long *errors;
+};
+
+template <int DT>
+__device__ __forceinline__ void store_row_chunk(const float (&x)[8], void *pages, float *scales,
+                                                int64_t elem, int64_t scale_idx, bool lead,
+                                                int lanes_per_group, bool valid) {
+    if constexpr (DT == AIR_KV_F32) {
+        if (valid) {
+            float4 *o = reinterpret_cast<float4 *>((float *)pages + elem);
+            o[0] = make_float4(x[0], x[1], x[2], x[3]);
+            o[1] = make_float4(x[4], x[5], x[6], x[7]);
+        }
+    } else if constexpr (DT == AIR_KV_BF16) {
+        if (valid) {
+            uint4 w;
+            w.x = (uint32_t)bf16_rne(x[0]) | ((uint32_t)bf16_rne(x[1]) << 16);
+            w.y = (uint32_t)bf16_rne(x[2]) | ((uint32_t)bf16_rne(x[3]) << 16);
+            w.z = (uint32_t)bf16_rne(x[4]) | ((uint32_t)bf16_rne(x[5]) << 16);
+            w.w = (uint32_t)bf16_rne(x[6]) | ((uint32_t)bf16_rne(x[7]) << 16);
+            *reinterpret_cast<uint4 *>((uint16_t *)pages + elem) = w;
+        }
+    } else {
+        // absmax fold from 0.0 with a NaN-ignoring max (src/kv_cache.rs:60,
+        // src/fp8.rs:228-232); max is order independent, so the lane-parallel
+        // reduction equals the reference's sequential fold.
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(x[j]));
+        for (int mask = 1; mask < lanes_per_group; mask <<= 1) m = fmaxf(m, __shfl_xor(m, mask));
+        uint32_t lo = 0, hi = 0;
+        float scale;
+        if constexpr (DT == AIR_KV_INT8) {
+            scale = q8_scale(m);
+            float inv;
+            {
+#pragma clang fp contract(off)
+                inv = 1.0f / scale;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) lo |= (uint32_t)(uint8_t)q8_code(x[j], inv) << (8 * j);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) hi |= (uint32_t)(uint8_t)q8_code(x[4 + j], inv) << (8 * j);
+        } else {
+            scale = fp8_scale(m);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) lo |= (uint32_t)fp8_code(x[j], scale) << (8 * j);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) hi |= (uint32_t)fp8_code(x[4 + j], scale) << (8 * j);
+        }
+        if (valid) {
+            *reinterpret_cast<uint2 *>((uint8_t *)pages + elem) = make_uint2(lo, hi);
+            if (lead) scales[scale_idx] = scale;
+        }
+    }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void kv_append_kernel(AppendArgs a) {
+    const int chunks = a.head_dim >> 3;
+    const int64_t gid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t row = gid / chunks;
+    const int c = (int)(gid - row * chunks);
+    const bool active = row < a.n_rows;
+    const int64_t t = active ? row / a.n_kv_heads : 0;
+    const int h = active ? (int)(row - t * a.n_kv_heads) : 0;
+    const int64_t slot = active ? a.slots[t] : -1;
+    const bool valid = slot >= 0 && slot < a.num_slots;
+    if (active && slot >= a.num_slots && c == 0 && h == 0) atomicAdd(a.errors, 1ull);
+
+    float kx[8], vx[8];
+    if (valid) {
+        const float4 *ks = reinterpret_cast<const float4 *>(a.k + row * a.head_dim + c * 8);
+        const float4 *vs = reinterpret_cast<const float4 *>(a.v + row * a.head_dim + c * 8);
+        float4 k0 = ks[0], k1 = ks[1], v0 = vs[0], v1 = vs[1];
+        kx[0] = k0.x; kx[1] = k0.y; kx[2] = k0.z; kx[3] = k0.w;
+        kx[4] = k1.x; kx[5] = k1.y; kx[6] = k1.z; kx[7] = k1.w;
+        vx[0] = v0.x; vx[1] = v0.y; vx[2] = v0.z; vx[3] = v0.w;
+        vx[4] = v1.x; vx[5] = v1.y; vx[6] = v1.z; vx[7] = v1.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) kx[j] = vx[j] = 0.0f;
+    }
+    const int64_t blk = valid ? slot / a.block_size : 0;
+    const int64_t off = valid ? slot - blk * a.block_size : 0;
+    const int64_t dst_row = (blk * a.n_kv_heads + h) * a.block_size + off;
+    const int64_t elem = dst_row * a.head_dim + c * 8;
+    int lanes_per_group = 1;
+    int64_t scale_idx = 0;
+    bool lead = false;
+    if constexpr (DT == AIR_KV_INT8 || DT == AIR_KV_FP8) {
+        lanes_per_group = a.scale_group >> 3;
+        scale_idx = dst_row * (a.head_dim / a.scale_group) + (c * 8) / a.scale_group;
+        lead = (c % lanes_per_group) == 0;
+    }
+    store_row_chunk<DT>(kx, a.k_pages, a.k_scales, elem, scale_idx, lead, lanes_per_group, valid);
+    store_row_chunk<DT>(vx, a.v_pages, a.v_scales, elem, scale_idx, lead, lanes_per_group, valid);
+}
+
+}  // namespace
+
+hipError_t launch_append(const air_kv_pool &p, hipStream_t s, const float *k, const float *v,
+                         const int64_t *slots, int32_t n_tokens) {
+    AppendArgs a;
+    a.k = k; a.v = v; a.slots = slots;
+    a.n_rows = (int64_t)n_tokens * p.desc.n_kv_heads;
+    a.num_slots = p.desc.num_blocks * p.desc.block_size;
+    a.n_kv_heads = p.desc.n_kv_heads; a.head_dim = p.desc.head_dim;
+    a.block_size = p.desc.block_size; a.scale_group = p.desc.scale_group;
+    a.k_pages = p.k_pages; a.v_pages = p.v_pages;
+    a.k_scales = p.k_scales; a.v_scales = p.v_scales;
+    a.errors = p.errors;
+    const int64_t threads = a.n_rows * (p.desc.head_dim / 8);
+    const int64_t blocks = (threads + kThreads - 1) / kThreads;
+    if (blocks > INT32_MAX) return hipErrorInvalidValue;
+    dim3 grid((unsigned)blocks);
+    switch (p.desc.dtype) {
+    case AIR_KV_F32: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_F32>, grid, dim3(kThreads), 0, s, a); break;
+    case AIR_KV_BF16: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_BF16>, grid, dim3(kThreads), 0, s, a); break;
+    case AIR_KV_INT8: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_INT8>, grid, dim3(kThreads), 0, s, a); break;
+    default: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_FP8>, grid, dim3(kThreads), 0, s, a); break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace airkv

@@ -1,0 +1,220 @@
+// Gather: pages -> one contiguous view per sequence (dequantizing INT8/FP8).
+//
+// Work is the flat list of (sequence, page, kv head) tiles of every live
+// sequence, so variable lengths cost nothing: each workgroup builds the
+// exclusive prefix sum of pages-per-sequence in LDS once, then walks the tile
+// list with a grid stride, finding a tile's sequence by binary search.  A
+// tile is block_size rows of head_dim elements of K and of V; each thread
+// moves 8 elements (a 16-byte bf16 load) per tensor per step, so a bf16
+// tile of 16 x 128 is exactly one pass of 256 threads.
+#include <hip/hip_runtime.h>
+
+#include "../pool.hpp"
+#include "codecs.hpp"
+
+namespace airkv {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxSeqsPerLaunch = 4096;   // LDS prefix: 16 KB
+
+struct GatherArgs {
+    const int32_t *tables, *lens;
+    const int64_t *out_offsets;
+    int32_t batch, max_blocks;
+    int32_t n_kv_heads, head_dim, block_size, scale_group;
+    int64_t num_blocks;
+    const void *k_pages, *v_pages;
+    const float *k_scales, *v_scales;
+    void *out_k, *out_v;
+    int32_t layout;
+    unsigned long long *errors;
+};
+
+template <int DT>
+__device__ __forceinline__ void load8(const void *pages, const float *scales, int64_t elem,
+                                      int64_t scale_idx, float (&x)[8], uint4 *raw) {
+    if constexpr (DT == AIR_KV_F32) {
+        const float4 *p = reinterpret_cast<const float4 *>((const float *)pages + elem);
+        float4 a = p[0], b = p[1];
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    } else if constexpr (DT == AIR_KV_BF16) {
+        uint4 w = *reinterpret_cast<const uint4 *>((const uint16_t *)pages + elem);
+        *raw = w;
+        uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            x[2 * j] = __uint_as_float(u[j] << 16);
+            x[2 * j + 1] = __uint_as_float(u[j] & 0xFFFF0000u);
+        }
+    } else {
+        uint2 w = *reinterpret_cast<const uint2 *>((const uint8_t *)pages + elem);
+        const float s = scales[scale_idx];
+        uint32_t u[2] = {w.x, w.y};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t byte = (u[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+            float val;
+            if constexpr (DT == AIR_KV_INT8) val = (float)(int32_t)(int8_t)byte;
+            else val = fp8_decode(byte);
+            {
+#pragma clang fp contract(off)
+                x[j] = val * s;   // q as f32 * scale (src/kv_cache.rs:88, src/fp8.rs:263-264)
+            }
+        }
+    }
+}
+
+template <int DT, int OUT>
+__device__ __forceinline__ void store8(void *out, int64_t elem, const float (&x)[8], uint4 raw) {
+    if constexpr (OUT == AIR_KV_F32) {
+        float4 *o = reinterpret_cast<float4 *>((float *)out + elem);
+        o[0] = make_float4(x[0], x[1], x[2], x[3]);
+        o[1] = make_float4(x[4], x[5], x[6], x[7]);
+    } else if constexpr (DT == AIR_KV_BF16) {
+        *reinterpret_cast<uint4 *>((uint16_t *)out + elem) = raw;   // raw bits, no re-rounding
+    } else {
+        uint4 w;
+        w.x = (uint32_t)bf16_rne(x[0]) | ((uint32_t)bf16_rne(x[1]) << 16);
+        w.y = (uint32_t)bf16_rne(x[2]) | ((uint32_t)bf16_rne(x[3]) << 16);
+        w.z = (uint32_t)bf16_rne(x[4]) | ((uint32_t)bf16_rne(x[5]) << 16);
+        w.w = (uint32_t)bf16_rne(x[6]) | ((uint32_t)bf16_rne(x[7]) << 16);
+        *reinterpret_cast<uint4 *>((uint16_t *)out + elem) = w;
+    }
+}
+
+template <int DT, int OUT>
+__global__ __launch_bounds__(kThreads) void kv_gather_kernel(GatherArgs a) {
+    __shared__ int32_t s_prefix[kMaxSeqsPerLaunch + 1];
+    __shared__ int32_t s_wave_tot[kThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t max_len = (int64_t)a.max_blocks * a.block_size;
+
+    // exclusive prefix of pages per sequence, kThreads sequences per round
+    int32_t carry = 0;
+    for (int base = 0; base < a.batch; base += kThreads) {
+        const int b = base + tid;
+        int32_t pages = 0;
+        if (b < a.batch) {
+            int64_t len = a.lens[b];
+            len = len < 0 ? 0 : (len > max_len ? max_len : len);
+            pages = (int32_t)((len + a.block_size - 1) / a.block_size);
+        }
+        int32_t incl = pages;
+        for (int off = 1; off < 64; off <<= 1) {
+            int32_t y = __shfl_up(incl, off);
+            if (lane >= off) incl += y;
+        }
+        if (lane == 63) s_wave_tot[wave] = incl;
+        __syncthreads();
+        int32_t before = carry;
+        for (int w = 0; w < wave; ++w) before += s_wave_tot[w];
+        if (b < a.batch) s_prefix[b] = before + incl - pages;
+        int32_t round_total = 0;
+        for (int w = 0; w < kThreads / 64; ++w) round_total += s_wave_tot[w];
+        carry += round_total;
+        __syncthreads();
+    }
+    if (tid == 0) s_prefix[a.batch] = carry;
+    __syncthreads();
+    // count malformed lengths once
+    if (blockIdx.x == 0) {
+        for (int b = tid; b < a.batch; b += kThreads) {
+            int32_t len = a.lens[b];
+            if (len < 0 || len > max_len) atomicAdd(a.errors, 1ull);
+        }
+    }
+
+    const int64_t total_tiles = (int64_t)carry * a.n_kv_heads;
+    const int rows = a.block_size, d = a.head_dim;
+    const int tile_elems = rows * d;
+    const int ng = DT == AIR_KV_INT8 || DT == AIR_KV_FP8 ? d / a.scale_group : 1;
+    for (int64_t tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
+        const int32_t page_g = (int32_t)(tile / a.n_kv_heads);
+        const int h = (int)(tile - (int64_t)page_g * a.n_kv_heads);
+        // sequence owning global page index page_g: last b with prefix[b] <= page_g
+        int lo = 0, hi = a.batch - 1;
+        while (lo < hi) {
+            int mid = (lo + hi + 1) >> 1;
+            if (s_prefix[mid] <= page_g) lo = mid; else hi = mid - 1;
+        }
+        const int b = lo;
+        const int32_t p = page_g - s_prefix[b];
+        int64_t len = a.lens[b];
+        len = len > max_len ? max_len : len;
+        const int32_t blk = a.tables[(int64_t)b * a.max_blocks + p];
+        if (blk < 0 || blk >= a.num_blocks) {
+            if (tid == 0) atomicAdd(a.errors, 1ull);
+            continue;
+        }
+        const int64_t out_base = a.out_offsets[b];
+        for (int e = tid * 8; e < tile_elems; e += kThreads * 8) {
+            const int r = e / d, col = e - r * d;
+            const int64_t t = (int64_t)p * rows + r;
+            if (t >= len) continue;
+            const int64_t src_row = ((int64_t)blk * a.n_kv_heads + h) * rows + r;
+            const int64_t src = src_row * d + col;
+            const int64_t sidx = src_row * ng + col / (a.scale_group > 0 ? a.scale_group : 1);
+            const int64_t dst = out_base + (a.layout == AIR_KV_LAYOUT_HEAD_MAJOR
+                                                ? ((int64_t)h * len + t) * d + col
+                                                : (t * a.n_kv_heads + h) * d + col);
+            float xk[8], xv[8];
+            uint4 rk = make_uint4(0, 0, 0, 0), rv = rk;
+            load8<DT>(a.k_pages, a.k_scales, src, sidx, xk, &rk);
+            load8<DT>(a.v_pages, a.v_scales, src, sidx, xv, &rv);
+            store8<DT, OUT>(a.out_k, dst, xk, rk);
+            store8<DT, OUT>(a.out_v, dst, xv, rv);
+        }
+    }
+}
+
+template <int DT>
+void dispatch_out(int out_dtype, dim3 grid, hipStream_t s, const GatherArgs &a) {
+    if (out_dtype == AIR_KV_F32)
+        hipLaunchKernelGGL((kv_gather_kernel<DT, AIR_KV_F32>), grid, dim3(kThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL((kv_gather_kernel<DT, AIR_KV_BF16>), grid, dim3(kThreads), 0, s, a);
+}
+
+}  // namespace
+
+hipError_t launch_gather(const air_kv_pool &p, hipStream_t s, const int32_t *tables,
+                         const int32_t *lens, const int64_t *out_offsets, int32_t batch,
+                         int32_t max_blocks, void *out_k, void *out_v, int32_t out_dtype,
+                         int32_t out_layout) {
+    int cus = 256;
+    {
+        int dev = 0;
+        if (hipGetDevice(&dev) == hipSuccess)
+            (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    }
+    for (int32_t b0 = 0; b0 < batch; b0 += kMaxSeqsPerLaunch) {
+        const int32_t nb = batch - b0 < kMaxSeqsPerLaunch ? batch - b0 : kMaxSeqsPerLaunch;
+        GatherArgs a;
+        a.tables = tables + (int64_t)b0 * max_blocks;
+        a.lens = lens + b0;
+        a.out_offsets = out_offsets + b0;
+        a.batch = nb;
+        a.max_blocks = max_blocks;
+        a.n_kv_heads = p.desc.n_kv_heads; a.head_dim = p.desc.head_dim;
+        a.block_size = p.desc.block_size; a.scale_group = p.desc.scale_group;
+        a.num_blocks = p.desc.num_blocks;
+        a.k_pages = p.k_pages; a.v_pages = p.v_pages;
+        a.k_scales = p.k_scales; a.v_scales = p.v_scales;
+        a.out_k = out_k; a.out_v = out_v;
+        a.layout = out_layout;
+        a.errors = p.errors;
+        dim3 grid((unsigned)(cus * 8));
+        switch (p.desc.dtype) {
+        case AIR_KV_F32: dispatch_out<AIR_KV_F32>(out_dtype, grid, s, a); break;
+        case AIR_KV_BF16: dispatch_out<AIR_KV_BF16>(out_dtype, grid, s, a); break;
+        case AIR_KV_INT8: dispatch_out<AIR_KV_INT8>(out_dtype, grid, s, a); break;
+        default: dispatch_out<AIR_KV_FP8>(out_dtype, grid, s, a); break;
+        }
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace airkv

@@ -1,0 +1,268 @@
+// extern "C" entry points for the device pool (air_kv.h, "Device side").
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "host/status.hpp"
+#include "pool.hpp"
+
+using airkv::fail;
+
+namespace {
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(AIR_KV_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int air_kv_pool_create(const air_kv_pool_desc *desc, air_kv_pool **out) {
+    if (!desc || !out) return fail(AIR_KV_E_INVALID_ARG, "desc or out is NULL");
+    const air_kv_pool_desc d = *desc;
+    if (d.num_blocks <= 0 || d.num_blocks > (int64_t)INT32_MAX)
+        return fail(AIR_KV_E_INVALID_ARG, "num_blocks %lld out of range", (long long)d.num_blocks);
+    if (d.block_size != 16 && d.block_size != 32)
+        return fail(AIR_KV_E_INVALID_ARG, "block_size must be 16 or 32 (got %d)", d.block_size);
+    if (d.n_kv_heads <= 0 || d.n_kv_heads > 256)
+        return fail(AIR_KV_E_INVALID_ARG, "n_kv_heads %d out of range", d.n_kv_heads);
+    if (d.head_dim <= 0 || d.head_dim % 32 || d.head_dim > 256)
+        return fail(AIR_KV_E_INVALID_ARG, "head_dim must be a multiple of 32 up to 256 (got %d)", d.head_dim);
+    if (d.dtype < AIR_KV_F32 || d.dtype > AIR_KV_FP8)
+        return fail(AIR_KV_E_INVALID_ARG, "unknown dtype %d", d.dtype);
+    if (airkv::dtype_quantized(d.dtype) &&
+        (!pow2(d.scale_group) || d.scale_group < 8 || d.head_dim % d.scale_group))
+        return fail(AIR_KV_E_INVALID_ARG,
+                    "scale_group must be a power of two >= 8 dividing head_dim (got %d)", d.scale_group);
+
+    auto *p = new (std::nothrow) air_kv_pool();
+    if (!p) return fail(AIR_KV_E_OOM, "host allocation failed");
+    p->desc = d;
+    if (!airkv::dtype_quantized(d.dtype)) p->desc.scale_group = 0;
+    p->elem_bytes = airkv::dtype_bytes(d.dtype);
+    const size_t rows = (size_t)d.n_kv_heads * d.block_size;
+    p->page_slab_bytes = rows * d.head_dim * p->elem_bytes;
+    p->scale_slab_bytes = airkv::dtype_quantized(d.dtype) ? rows * (d.head_dim / d.scale_group) * 4 : 0;
+    p->block_bytes = 2 * (p->page_slab_bytes + p->scale_slab_bytes);
+
+    hipError_t e = hipGetDevice(&p->device);
+    if (e != hipSuccess) { delete p; return hip_fail(e, "hipGetDevice"); }
+    const size_t pages = p->page_slab_bytes * (size_t)d.num_blocks;
+    const size_t scales = p->scale_slab_bytes * (size_t)d.num_blocks;
+    auto cleanup = [&](hipError_t err, const char *what) {
+        (void)hipFree(p->k_pages); (void)hipFree(p->v_pages);
+        (void)hipFree(p->k_scales); (void)hipFree(p->v_scales);
+        (void)hipFree(p->errors);
+        delete p;
+        return err == hipErrorOutOfMemory ? fail(AIR_KV_E_OOM, "%s: out of device memory", what)
+                                          : hip_fail(err, what);
+    };
+    if ((e = hipMalloc(&p->k_pages, pages)) != hipSuccess) return cleanup(e, "hipMalloc(k_pages)");
+    if ((e = hipMalloc(&p->v_pages, pages)) != hipSuccess) return cleanup(e, "hipMalloc(v_pages)");
+    if (scales) {
+        if ((e = hipMalloc((void **)&p->k_scales, scales)) != hipSuccess) return cleanup(e, "hipMalloc(k_scales)");
+        if ((e = hipMalloc((void **)&p->v_scales, scales)) != hipSuccess) return cleanup(e, "hipMalloc(v_scales)");
+    }
+    if ((e = hipMalloc((void **)&p->errors, sizeof(unsigned long long))) != hipSuccess)
+        return cleanup(e, "hipMalloc(errors)");
+    if ((e = hipMemset(p->k_pages, 0, pages)) != hipSuccess) return cleanup(e, "hipMemset");
+    if ((e = hipMemset(p->v_pages, 0, pages)) != hipSuccess) return cleanup(e, "hipMemset");
+    if (scales) {
+        if ((e = hipMemset(p->k_scales, 0, scales)) != hipSuccess) return cleanup(e, "hipMemset");
+        if ((e = hipMemset(p->v_scales, 0, scales)) != hipSuccess) return cleanup(e, "hipMemset");
+    }
+    if ((e = hipMemset(p->errors, 0, sizeof(unsigned long long))) != hipSuccess) return cleanup(e, "hipMemset");
+    if ((e = hipDeviceSynchronize()) != hipSuccess) return cleanup(e, "hipDeviceSynchronize");
+    *out = p;
+    return AIR_KV_OK;
+}
+
+int air_kv_pool_destroy(air_kv_pool *p) {
+    if (!p) return AIR_KV_OK;
+    int dev_prev = 0;
+    (void)hipGetDevice(&dev_prev);
+    (void)hipSetDevice(p->device);
+    (void)hipFree(p->k_pages); (void)hipFree(p->v_pages);
+    (void)hipFree(p->k_scales); (void)hipFree(p->v_scales);
+    (void)hipFree(p->errors);
+    (void)hipSetDevice(dev_prev);
+    delete p;
+    return AIR_KV_OK;
+}
+
+int air_kv_pool_info(const air_kv_pool *p, air_kv_pool_desc *desc, void **k_pages, void **v_pages,
+                     void **k_scales, void **v_scales, size_t *block_bytes) {
+    if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
+    if (desc) *desc = p->desc;
+    if (k_pages) *k_pages = p->k_pages;
+    if (v_pages) *v_pages = p->v_pages;
+    if (k_scales) *k_scales = p->k_scales;
+    if (v_scales) *v_scales = p->v_scales;
+    if (block_bytes) *block_bytes = p->block_bytes;
+    return AIR_KV_OK;
+}
+
+int air_kv_append(air_kv_pool *p, void *stream, const float *k, const float *v,
+                  const int64_t *slot_mapping, int32_t n_tokens) {
+    if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
+    if (n_tokens < 0) return fail(AIR_KV_E_INVALID_ARG, "n_tokens < 0");
+    if (n_tokens == 0) return AIR_KV_OK;
+    if (!k || !v || !slot_mapping) return fail(AIR_KV_E_INVALID_ARG, "k, v or slot_mapping is NULL");
+    hipError_t e = airkv::launch_append(*p, (hipStream_t)stream, k, v, slot_mapping, n_tokens);
+    return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "air_kv_append launch");
+}
+
+int air_kv_gather(air_kv_pool *p, void *stream, const int32_t *block_tables, const int32_t *seq_lens,
+                  const int64_t *out_offsets, int32_t batch, int32_t max_blocks, void *out_k,
+                  void *out_v, int32_t out_dtype, int32_t out_layout) {
+    if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
+    if (batch < 0 || max_blocks <= 0) return fail(AIR_KV_E_INVALID_ARG, "bad batch / max_blocks");
+    if (batch == 0) return AIR_KV_OK;
+    if (!block_tables || !seq_lens || !out_offsets || !out_k || !out_v)
+        return fail(AIR_KV_E_INVALID_ARG, "NULL gather buffer");
+    if (out_dtype != AIR_KV_F32 && out_dtype != AIR_KV_BF16)
+        return fail(AIR_KV_E_INVALID_ARG, "gather out_dtype must be F32 or BF16");
+    if (out_dtype == AIR_KV_BF16 && p->desc.dtype == AIR_KV_F32)
+        return fail(AIR_KV_E_INVALID_ARG, "an F32 pool gathers to F32 only");
+    if (out_layout != AIR_KV_LAYOUT_HEAD_MAJOR && out_layout != AIR_KV_LAYOUT_TOKEN_MAJOR)
+        return fail(AIR_KV_E_INVALID_ARG, "unknown out_layout %d", out_layout);
+    hipError_t e = airkv::launch_gather(*p, (hipStream_t)stream, block_tables, seq_lens, out_offsets,
+                                        batch, max_blocks, out_k, out_v, out_dtype, out_layout);
+    return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "air_kv_gather launch");
+}
+
+int air_paged_decode_workspace_size(const air_kv_pool *p, int32_t n_q_heads, int32_t batch,
+                                    int32_t max_blocks, int32_t max_splits, size_t *bytes) {
+    if (!p || !bytes) return fail(AIR_KV_E_INVALID_ARG, "pool or bytes is NULL");
+    airkv::DecodePlan plan;
+    if (int rc = airkv::plan_decode(*p, n_q_heads, batch, max_blocks, max_splits, &plan)) return rc;
+    *bytes = plan.ws_bytes;
+    return AIR_KV_OK;
+}
+
+int air_paged_decode(air_kv_pool *p, void *stream, const void *q, int32_t q_dtype, int32_t n_q_heads,
+                     const int32_t *block_tables, const int32_t *seq_lens, int32_t batch,
+                     int32_t max_blocks, float scale, int32_t max_splits, void *workspace,
+                     size_t ws_bytes, void *out, int32_t out_dtype) {
+    if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
+    airkv::DecodePlan plan;
+    if (int rc = airkv::plan_decode(*p, n_q_heads, batch, max_blocks, max_splits, &plan)) return rc;
+    if (batch == 0) return AIR_KV_OK;
+    if (!q || !block_tables || !seq_lens || !out || !workspace)
+        return fail(AIR_KV_E_INVALID_ARG, "NULL decode buffer");
+    if (ws_bytes < plan.ws_bytes)
+        return fail(AIR_KV_E_INVALID_ARG, "workspace %zu bytes < %zu needed", ws_bytes, plan.ws_bytes);
+    if (q_dtype != AIR_KV_F32 && q_dtype != AIR_KV_BF16)
+        return fail(AIR_KV_E_INVALID_ARG, "q_dtype must be F32 or BF16");
+    if (out_dtype != AIR_KV_F32 && out_dtype != AIR_KV_BF16)
+        return fail(AIR_KV_E_INVALID_ARG, "out_dtype must be F32 or BF16");
+    if (!(scale == scale)) return fail(AIR_KV_E_INVALID_ARG, "scale is NaN");
+    hipError_t e = airkv::launch_decode(*p, (hipStream_t)stream, plan, q, q_dtype, n_q_heads,
+                                        block_tables, seq_lens, batch, max_blocks, scale, workspace,
+                                        out, out_dtype);
+    return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "air_paged_decode launch");
+}
+
+int air_kv_copy_blocks(air_kv_pool *p, void *stream, const int32_t *src, const int32_t *dst, int32_t n) {
+    if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
+    if (n < 0) return fail(AIR_KV_E_INVALID_ARG, "n < 0");
+    if (n == 0) return AIR_KV_OK;
+    if (!src || !dst) return fail(AIR_KV_E_INVALID_ARG, "NULL block list");
+    hipError_t e = airkv::launch_copy_blocks(*p, (hipStream_t)stream, src, dst, n);
+    return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "air_kv_copy_blocks launch");
+}
+
+static int check_ids(const air_kv_pool *p, const int32_t *ids, int32_t n) {
+    for (int32_t i = 0; i < n; ++i)
+        if (ids[i] < 0 || ids[i] >= p->desc.num_blocks)
+            return fail(AIR_KV_E_INVALID_ARG, "block id %d outside the pool", ids[i]);
+    return AIR_KV_OK;
+}
+
+int air_kv_read_blocks(air_kv_pool *p, void *stream, const int32_t *ids, int32_t n, void *host_dst) {
+    if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
+    if (n < 0 || (n > 0 && (!ids || !host_dst))) return fail(AIR_KV_E_INVALID_ARG, "bad block list");
+    if (int rc = check_ids(p, ids, n)) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    uint8_t *dst = (uint8_t *)host_dst;
+    for (int32_t i = 0; i < n; ++i) {
+        const size_t b = (size_t)ids[i];
+        uint8_t *o = dst + (size_t)i * p->block_bytes;
+        const void *srcs[4] = {(const uint8_t *)p->k_pages + b * p->page_slab_bytes,
+                               (const uint8_t *)p->v_pages + b * p->page_slab_bytes,
+                               p->k_scales ? (const uint8_t *)p->k_scales + b * p->scale_slab_bytes : nullptr,
+                               p->v_scales ? (const uint8_t *)p->v_scales + b * p->scale_slab_bytes : nullptr};
+        const size_t sizes[4] = {p->page_slab_bytes, p->page_slab_bytes, p->scale_slab_bytes,
+                                 p->scale_slab_bytes};
+        for (int j = 0; j < 4; ++j) {
+            if (!sizes[j]) continue;
+            hipError_t e = hipMemcpyAsync(o, srcs[j], sizes[j], hipMemcpyDeviceToHost, s);
+            if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(D2H)");
+            o += sizes[j];
+        }
+    }
+    hipError_t e = hipStreamSynchronize(s);
+    return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+int air_kv_write_blocks(air_kv_pool *p, void *stream, const int32_t *ids, int32_t n, const void *host_src) {
+    if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
+    if (n < 0 || (n > 0 && (!ids || !host_src))) return fail(AIR_KV_E_INVALID_ARG, "bad block list");
+    if (int rc = check_ids(p, ids, n)) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    const uint8_t *src = (const uint8_t *)host_src;
+    for (int32_t i = 0; i < n; ++i) {
+        const size_t b = (size_t)ids[i];
+        const uint8_t *in = src + (size_t)i * p->block_bytes;
+        void *dsts[4] = {(uint8_t *)p->k_pages + b * p->page_slab_bytes,
+                         (uint8_t *)p->v_pages + b * p->page_slab_bytes,
+                         p->k_scales ? (uint8_t *)p->k_scales + b * p->scale_slab_bytes : nullptr,
+                         p->v_scales ? (uint8_t *)p->v_scales + b * p->scale_slab_bytes : nullptr};
+        const size_t sizes[4] = {p->page_slab_bytes, p->page_slab_bytes, p->scale_slab_bytes,
+                                 p->scale_slab_bytes};
+        for (int j = 0; j < 4; ++j) {
+            if (!sizes[j]) continue;
+            hipError_t e = hipMemcpyAsync(dsts[j], in, sizes[j], hipMemcpyHostToDevice, s);
+            if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(H2D)");
+            in += sizes[j];
+        }
+    }
+    hipError_t e = hipStreamSynchronize(s);
+    return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+void air_kv_pool_read_cb(void *ctx, uint32_t block, uint8_t *dst, size_t bytes) {
+    air_kv_pool *p = (air_kv_pool *)ctx;
+    if (!p || bytes != p->block_bytes) return;
+    int32_t id = (int32_t)block;
+    air_kv_read_blocks(p, nullptr, &id, 1, dst);
+}
+
+void air_kv_pool_write_cb(void *ctx, uint32_t block, const uint8_t *src, size_t bytes) {
+    air_kv_pool *p = (air_kv_pool *)ctx;
+    if (!p || bytes != p->block_bytes) return;
+    int32_t id = (int32_t)block;
+    air_kv_write_blocks(p, nullptr, &id, 1, src);
+}
+
+int air_kv_pool_error_count(air_kv_pool *p, void *stream, int64_t *count, int32_t reset) {
+    if (!p || !count) return fail(AIR_KV_E_INVALID_ARG, "pool or count is NULL");
+    hipStream_t s = (hipStream_t)stream;
+    unsigned long long v = 0;
+    hipError_t e = hipMemcpyAsync(&v, p->errors, sizeof(v), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e == hipSuccess && reset) {
+        e = hipMemsetAsync(p->errors, 0, sizeof(v), s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+    }
+    if (e != hipSuccess) return hip_fail(e, "error counter read");
+    *count = (int64_t)v;
+    return AIR_KV_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,52 @@
+// Internal definition of the device pool and the kernel launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "air_kv.h"
+
+struct air_kv_pool {
+    air_kv_pool_desc desc;
+    int device = 0;
+    void *k_pages = nullptr;     // [num_blocks][n_kv_heads][block_size][head_dim]
+    void *v_pages = nullptr;
+    float *k_scales = nullptr;   // [num_blocks][n_kv_heads][block_size][head_dim/scale_group]
+    float *v_scales = nullptr;
+    unsigned long long *errors = nullptr;   // device counter of skipped bad slots / entries
+    size_t elem_bytes = 0;
+    size_t page_slab_bytes = 0;  // one block of K (or of V)
+    size_t scale_slab_bytes = 0; // one block of K scales (or of V scales)
+    size_t block_bytes = 0;      // K + V + scales of one block
+};
+
+namespace airkv {
+
+inline size_t dtype_bytes(int dt) { return dt == AIR_KV_F32 ? 4 : dt == AIR_KV_BF16 ? 2 : 1; }
+inline bool dtype_quantized(int dt) { return dt == AIR_KV_INT8 || dt == AIR_KV_FP8; }
+
+// Partitioning of one decode launch (shared by the workspace query).
+struct DecodePlan {
+    int32_t group;        // q heads per kv head
+    int32_t part_tokens;  // tokens per split-K partition (multiple of block_size)
+    int32_t num_parts;    // partitions per sequence
+    size_t ws_bytes;      // partial outputs + (max, sum) per (seq, q head, part)
+};
+int plan_decode(const air_kv_pool &pool, int32_t n_q_heads, int32_t batch, int32_t max_blocks,
+                int32_t max_splits, DecodePlan *plan);
+
+hipError_t launch_append(const air_kv_pool &pool, hipStream_t s, const float *k, const float *v,
+                         const int64_t *slots, int32_t n_tokens);
+hipError_t launch_gather(const air_kv_pool &pool, hipStream_t s, const int32_t *tables,
+                         const int32_t *lens, const int64_t *out_offsets, int32_t batch,
+                         int32_t max_blocks, void *out_k, void *out_v, int32_t out_dtype,
+                         int32_t out_layout);
+hipError_t launch_decode(const air_kv_pool &pool, hipStream_t s, const DecodePlan &plan,
+                         const void *q, int32_t q_dtype, int32_t n_q_heads, const int32_t *tables,
+                         const int32_t *lens, int32_t batch, int32_t max_blocks, float scale,
+                         void *workspace, void *out, int32_t out_dtype);
+hipError_t launch_copy_blocks(const air_kv_pool &pool, hipStream_t s, const int32_t *src,
+                              const int32_t *dst, int32_t n);
+
+}  // namespace airkv

@@ -1,0 +1,263 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged KV-cache hot path on one MI355X.
+
+Workload: Llama-3-8B decode shape, bf16 KV pages,
+32 q / 8 kv heads, head_dim 128, block_size 16, batch 64, contexts
+U[512, 4096], block tables over a shuffled pool of 1.25x the tokens.  One
+step = append one new token per sequence (reshape-and-cache of f32 K/V) then
+split-K paged decode attention over every cached token.  All inputs are
+resident in HBM before timing starts.
+
+Prints one JSON line: whole-step HBM throughput (`value`, GB/s of
+algorithmic bytes), the decode kernel's roofline fraction (HIP events on the
+launch stream), gather / large-append bandwidths, and the CPU oracle timed
+on a bounded sample of the same workload on this host.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "air.rs_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_HBM_GBPS = 8000.0   # MI355X HBM3E spec
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--max-splits", type=int, default=64)
+    ap.add_argument("--kernel-iters", type=int, default=50)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only-decode", action="store_true",
+                    help="skip the gather / append bandwidth legs (for profiling runs)")
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def timed_loop(torch, fn, iters, lead_sleep=True):
+    """Average GPU time per launch of fn() over `iters` back-to-back launches,
+    measured with events on the current stream; a sleep kernel first lets the
+    host queue every launch before the first one starts."""
+    torch.cuda.synchronize()
+    if lead_sleep:
+        torch.cuda._sleep(20_000_000)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters   # ms
+
+
+def cpu_baseline(pool, w, tables, lens, q_f32, budget_s):
+    """Oracle paged decode (gather + flash_decode, chunk 64, one thread) on
+    whole sequences of the same workload until ~budget_s of CPU time."""
+    import numpy as np
+
+    import oracle
+    cfg = w.cfg
+    bytes_per_tok = cfg.n_kv_heads * cfg.head_dim * 2 * 2
+    done_bytes, done_tok, spent, nseq = 0, 0, 0.0, 0
+    order = list(range(len(lens)))
+    for b in order:
+        L = int(lens[b])
+        nblk = -(-L // cfg.block_size)
+        ids = tables[b, :nblk].astype(np.int32)
+        raw = pool.read_blocks(ids)
+        k, v, _, _ = pool.split_blocks(raw)
+        host = oracle.HostPool(nblk, cfg.block_size, cfg.n_kv_heads, cfg.head_dim, oracle.BF16)
+        host.k[:], host.v[:] = k, v
+        tab = np.arange(nblk, dtype=np.int32).reshape(1, nblk)
+        t0 = time.perf_counter()
+        host.paged_decode(q_f32[b:b + 1], tab, np.array([L], np.int32), chunk=64)
+        spent += time.perf_counter() - t0
+        done_bytes += L * bytes_per_tok + 4 * nblk + cfg.n_q_heads * cfg.head_dim * (2 + 4)
+        done_tok += 1
+        nseq += 1
+        if spent >= budget_s:
+            break
+    return {"value": done_bytes / spent / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{nseq} of {len(lens)} sequences of the same workload (all 32 q heads, "
+                      f"{sum(int(lens[b]) for b in order[:nseq])} cached tokens), oracle "
+                      f"gather + flash_decode chunk 64, {spent:.1f} s",
+            "seq_per_s": nseq / spent}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the paged KV path runs on one "
+                                   "MI355X and no multi-GPU figure is produced (--gpus 1)"}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import airkv
+    from airkv import workloads
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    dev = "cuda"
+    cfg = workloads.CONFIGS["c2"]
+    n_steps = args.warmup + args.steps
+    lens0 = workloads.c2_lengths(cfg.batch, 512, 4096, seed=2)
+    t_setup = time.perf_counter()
+    w = workloads.build_prefill_decode(cfg, lens0, seed=2, decode_steps=n_steps)
+    pool = airkv.KvPool(w.num_blocks, cfg.block_size, cfg.n_kv_heads, cfg.head_dim, cfg.dtype)
+    log(f"pool {w.num_blocks} blocks, {sum(lens0)} prefill tokens, {n_steps} steps")
+
+    # prefill (untimed): stream f32 K/V through the append kernel
+    n_prefill = len(lens0)
+    gen = workloads.kv_rows(10 ** 12, cfg.n_kv_heads, cfg.head_dim, seed=5, device=dev,
+                            chunk_rows=8192)
+    for slots in w.batches[:n_prefill]:
+        done = 0
+        while done < len(slots):
+            k, v = next(gen)
+            n = min(len(slots) - done, k.shape[0])
+            pool.append(k[:n].contiguous(), v[:n].contiguous(),
+                        torch.from_numpy(slots[done:done + n]).to(dev))
+            done += n
+    # per-step inputs, resident before timing
+    step_slots = [torch.from_numpy(s).to(dev) for s in w.batches[n_prefill:]]
+    step_k = [torch.randn(cfg.batch, cfg.n_kv_heads, cfg.head_dim, device=dev) for _ in range(n_steps)]
+    step_v = [torch.randn(cfg.batch, cfg.n_kv_heads, cfg.head_dim, device=dev) for _ in range(n_steps)]
+    step_q = [torch.randn(cfg.batch, cfg.n_q_heads, cfg.head_dim, device=dev).to(torch.bfloat16)
+              for _ in range(n_steps)]
+    tables_np, lens_final = w.tables()
+    max_blocks = tables_np.shape[1]
+    tables = torch.from_numpy(tables_np).to(dev)
+    step_lens = [torch.from_numpy((np.array(lens0) + i + 1).astype(np.int32)).to(dev)
+                 for i in range(n_steps)]
+    out = torch.empty(cfg.batch, cfg.n_q_heads, cfg.head_dim, device=dev, dtype=torch.bfloat16)
+    ws = pool.new_workspace(cfg.n_q_heads, cfg.batch, max_blocks, args.max_splits)
+    appends = [pool.bind_append(step_k[i], step_v[i], step_slots[i]) for i in range(n_steps)]
+    decodes = [pool.bind_decode(step_q[i], tables, step_lens[i], out, ws, max_splits=args.max_splits)
+               for i in range(n_steps)]
+    torch.cuda.synchronize()
+    log(f"setup {time.perf_counter() - t_setup:.1f} s")
+
+    # ---- timed steps: append + decode ------------------------------------
+    for i in range(args.warmup):
+        appends[i]()
+        decodes[i]()
+    torch.cuda.synchronize()
+    torch.cuda._sleep(20_000_000)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(args.warmup, n_steps):
+        appends[i]()
+        decodes[i]()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_step = e0.elapsed_time(e1) / args.steps
+    assert pool.error_count() == 0
+
+    kv_b = cfg.n_kv_heads * cfg.head_dim * 2 * 2           # K+V bytes per cached token (bf16)
+    bs = cfg.block_size
+    lens_t = np.array(lens0) + args.warmup + 1 + np.arange(args.steps)[:, None]   # [steps][batch]
+
+    def decode_bytes(lens):
+        tok = int(np.sum(lens))
+        pages = int(np.sum((lens + bs - 1) // bs))
+        qo = cfg.batch * cfg.n_q_heads * cfg.head_dim * (2 + 2)
+        return tok * kv_b + 4 * pages + qo
+
+    append_bytes_step = cfg.batch * cfg.n_kv_heads * cfg.head_dim * 2 * (4 + 2) + 8 * cfg.batch
+    step_bytes = sum(decode_bytes(l) for l in lens_t) / args.steps + append_bytes_step
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    log(f"step {ms_step * 1e3:.1f} us, {value:.0f} GB/s")
+
+    # ---- decode kernel alone, final state ---------------------------------
+    last = decodes[-1]
+    ms_dec = timed_loop(torch, last, args.kernel_iters)
+    dec_bytes = decode_bytes(np.array(lens0) + n_steps)
+    dec_gbps = dec_bytes / (ms_dec * 1e-3) / 1e9
+    log(f"decode {ms_dec * 1e3:.1f} us, {dec_gbps:.0f} GB/s ({dec_gbps / PEAK_HBM_GBPS:.1%} of peak)")
+
+    extra = {}
+    if not args.only_decode:
+        # gather of every sequence to contiguous bf16 [head][len][dim]
+        lens_f = np.array(lens0) + n_steps
+        per = lens_f.astype(np.int64) * cfg.n_kv_heads * cfg.head_dim
+        offs = torch.from_numpy(np.concatenate([[0], np.cumsum(per)[:-1]]).astype(np.int64)).to(dev)
+        gk = torch.empty(int(per.sum()), dtype=torch.bfloat16, device=dev)
+        gv = torch.empty_like(gk)
+        gather = pool.bind_gather(tables, step_lens[-1], offs, gk, gv)
+        ms_g = timed_loop(torch, gather, 20)
+        g_bytes = int(per.sum()) * 2 * 2 * 2 + 4 * int(np.sum((lens_f + bs - 1) // bs))
+        extra["gather_gbps"] = round(g_bytes / (ms_g * 1e-3) / 1e9, 1)
+        extra["gather_us"] = round(ms_g * 1e3, 1)
+        del gk, gv
+        # large append: 32768 prefill-like tokens (rewrites existing slots)
+        big = np.concatenate(w.batches[:n_prefill])[:32768]
+        bk = torch.randn(len(big), cfg.n_kv_heads, cfg.head_dim, device=dev)
+        bv = torch.randn_like(bk)
+        big_app = pool.bind_append(bk, bv, torch.from_numpy(big).to(dev))
+        ms_a = timed_loop(torch, big_app, 20)
+        a_bytes = len(big) * cfg.n_kv_heads * cfg.head_dim * 2 * (4 + 2) + 8 * len(big)
+        extra["append_gbps"] = round(a_bytes / (ms_a * 1e-3) / 1e9, 1)
+        extra["append_us"] = round(ms_a * 1e3, 1)
+        extra["append_tokens"] = int(len(big))
+        # the per-step 64-token append alone
+        ms_sa = timed_loop(torch, appends[-1], 50)
+        extra["step_append_us"] = round(ms_sa * 1e3, 2)
+        log(f"gather {extra['gather_gbps']} GB/s, append {extra['append_gbps']} GB/s")
+
+    cpu = None
+    if not args.no_cpu:
+        q_last = step_q[-1].float().cpu().numpy()
+        cpu = cpu_baseline(pool, w, tables_np, np.array(lens0) + n_steps, q_last, args.cpu_seconds)
+        log(f"cpu oracle {cpu['value']:.3f} GB/s over {cpu['sample']}")
+
+    result = {
+        "metric": "paged decode attn HBM GB/s (% of peak); KV append+gather GB/s, 1 MI355X",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) K/V/Q, seeded U[512,4096] contexts, shuffled pool)",
+        "config": {
+            "workload": "c2: append 1 token/seq + split-K paged decode, Llama-3-8B shape",
+            "batch": cfg.batch, "n_q_heads": cfg.n_q_heads, "n_kv_heads": cfg.n_kv_heads,
+            "head_dim": cfg.head_dim, "block_size": cfg.block_size, "kv_dtype": "bf16",
+            "q_dtype": "bf16", "out_dtype": "bf16", "ctx": "U[512,4096] seed 2",
+            "pool_blocks": w.num_blocks, "max_splits": args.max_splits,
+            "cached_tokens_final": int(np.sum(np.array(lens0) + n_steps)),
+        },
+        "pct_of_peak": round(100.0 * value / PEAK_HBM_GBPS, 2),
+        "decode_gbps": round(dec_gbps, 1),
+        "decode_us": round(ms_dec * 1e3, 2),
+        "tokens_per_s": round(cfg.batch / (ms_step * 1e-3), 1),
+        "roofline": {"bound": "hbm", "achieved": round(dec_gbps, 1), "peak": PEAK_HBM_GBPS,
+                     "unit": "GB/s", "frac": round(dec_gbps / PEAK_HBM_GBPS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    result.update(extra)
+    print(json.dumps(result), flush=True)
+    pool.close()
+
+
+if __name__ == "__main__":
+    main()

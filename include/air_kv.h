@@ -1,0 +1,261 @@
+/*
+ * air_kv.h -- C ABI of the MI355X-native paged KV-cache path.
+ *
+ * The reference (SunayHegde2006/Air.rs) has no FFI for this path; its seams
+ * are Rust types and traits.  Each entry point below names the reference
+ * interface it replaces.  A Rust caller binds these with `extern "C"` (see
+ * the binding in the integration notes); this build's tests bind them with
+ * ctypes.
+ *
+ * Conventions
+ *  - Every function returns an int status: AIR_KV_OK (0) or a negative
+ *    AIR_KV_E_* code.  The message of the last failure on the calling thread
+ *    is available from air_kv_last_error().  The library never aborts.
+ *  - Device-side entry points take raw device pointers, plain sizes and a
+ *    `void *stream` (a hipStream_t; NULL = the default stream).  They only
+ *    enqueue work and return; nothing synchronises unless documented.
+ *  - A pool owns all of its device memory (pages and scales).  The caller
+ *    owns every buffer it passes in.
+ *  - Host-side objects (allocator, sequence manager, swap manager) are not
+ *    thread-safe, as in the reference (src/paged_attention.rs:86-87); callers
+ *    serialise access, as the reference's generator does with a Mutex
+ *    (src/generator.rs:109-112).
+ *
+ * Device layout of a pool (one transformer layer):
+ *   k_pages, v_pages   : [num_blocks][n_kv_heads][block_size][head_dim]
+ *   k_scales, v_scales : [num_blocks][n_kv_heads][block_size][head_dim/scale_group]
+ *                        f32, only for AIR_KV_INT8 / AIR_KV_FP8 pools
+ *   slot = block * block_size + offset          (src/paged_attention.rs:216-234)
+ * One block's bytes (K + V + scales) equal the reference's page size formula
+ * n_heads * head_dim * 2 * dtype_bytes * BLOCK_SIZE (src/kv_swap.rs:37-38)
+ * plus the scales of quantized pools.
+ */
+#ifndef AIR_KV_H
+#define AIR_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define AIR_KV_OK 0
+#define AIR_KV_E_INVALID_ARG (-1) /* bad pointer, size, dtype or shape */
+#define AIR_KV_E_OOM (-2)         /* no free blocks / device allocation failed */
+#define AIR_KV_E_NOT_FOUND (-3)   /* unknown sequence id / nothing evicted */
+#define AIR_KV_E_HIP (-4)         /* a HIP runtime call failed */
+#define AIR_KV_E_STATE (-5)       /* operation invalid in the object's state */
+
+/* ---- element types ----------------------------------------------------- */
+#define AIR_KV_F32 0
+#define AIR_KV_BF16 1  /* stored with round-to-nearest-even (half 2.7.1 bf16::from_f32) */
+#define AIR_KV_INT8 2  /* Q8_0 codes, src/kv_cache.rs:54-75, + f32 scale per group */
+#define AIR_KV_FP8 3   /* reference E4M3 encoding, src/fp8.rs:54-112, + f32 scale per group */
+
+/* gather output layouts */
+#define AIR_KV_LAYOUT_HEAD_MAJOR 0  /* out[h][t][d]: flash_decode's k_cache (src/flash_decode.rs:153-163) */
+#define AIR_KV_LAYOUT_TOKEN_MAJOR 1 /* out[t][h][d]: the dense [seq, n_kv, d] view (src/kv_cache.rs:121-122) */
+
+/* Copies the last error message of this thread (NUL-terminated, truncated to
+ * `cap`).  Returns the full message length. */
+int air_kv_last_error(char *buf, size_t cap);
+
+/* ======================================================================== */
+/* Host side: block allocator, block tables, sequences                      */
+/* ======================================================================== */
+
+/* Replaces BlockAllocator (src/paged_attention.rs:89-196).  Block ids are
+ * PhysicalBlockId(u32) (:50-51).  `free_order` (may be NULL) sets the initial
+ * FIFO order of the free list (a permutation of 0..capacity-1); NULL gives
+ * the reference's 0..capacity order (:103-105).  `block_size` replaces the
+ * BLOCK_SIZE const (:40). */
+typedef struct air_block_allocator air_block_allocator;
+int air_block_allocator_create(int64_t capacity, int32_t block_size, const uint32_t *free_order,
+                               air_block_allocator **out);
+int air_block_allocator_destroy(air_block_allocator *a);
+/* allocate (:115-121): AIR_KV_E_OOM where the reference returns None. */
+int air_block_allocator_allocate(air_block_allocator *a, uint32_t *block);
+/* share (:124-126) */
+int air_block_allocator_share(air_block_allocator *a, uint32_t block);
+/* release (:129-135).  Releasing a block whose refcount is already 0 returns
+ * AIR_KV_E_STATE; the reference would push it onto the free list twice. */
+int air_block_allocator_release(air_block_allocator *a, uint32_t block);
+/* ref_count (:138-140) */
+int air_block_allocator_ref_count(const air_block_allocator *a, uint32_t block, uint32_t *rc);
+/* num_free_blocks / num_used_blocks (:143-150) */
+int64_t air_block_allocator_num_free(const air_block_allocator *a);
+int64_t air_block_allocator_num_used(const air_block_allocator *a);
+/* cow_write (:155-167): *out = block when it has a single owner, else a new
+ * block (metadata copied, old refcount decremented); AIR_KV_E_OOM = None.
+ * Page contents are copied on the device by air_kv_copy_blocks. */
+int air_block_allocator_cow_write(air_block_allocator *a, uint32_t block, uint32_t *out);
+/* append_token (:170-178): AIR_KV_E_STATE where the reference asserts. */
+int air_block_allocator_append_token(air_block_allocator *a, uint32_t block, int32_t *is_full);
+/* block fill metadata PhysicalBlock{num_tokens, is_full} (:63-80) */
+int air_block_allocator_block_info(const air_block_allocator *a, uint32_t block,
+                                   int32_t *num_tokens, int32_t *is_full);
+/* can_allocate (:182-184): 1 or 0 */
+int air_block_allocator_can_allocate(const air_block_allocator *a, int64_t n);
+/* utilization (:193-195) */
+float air_block_allocator_utilization(const air_block_allocator *a);
+/* num_blocks_for_tokens (:188-190) */
+int64_t air_num_blocks_for_tokens(int64_t n_tokens, int32_t block_size);
+
+/* Replaces SequenceManager (src/paged_attention.rs:243-382). */
+typedef struct air_seq_manager air_seq_manager;
+int air_seq_manager_create(int64_t capacity, int32_t block_size, const uint32_t *free_order,
+                           air_seq_manager **out);
+int air_seq_manager_destroy(air_seq_manager *m);
+/* The manager's allocator (borrowed; lives as long as the manager). */
+air_block_allocator *air_seq_manager_allocator(air_seq_manager *m);
+/* create_sequence (:260-265): monotonic ids */
+int air_seq_create(air_seq_manager *m, uint32_t *seq);
+/* append_token (:269-286): *block = the physical block of the new token.
+ * AIR_KV_E_NOT_FOUND = "sequence not found", AIR_KV_E_OOM = "out of memory". */
+int air_seq_append_token(air_seq_manager *m, uint32_t seq, uint32_t *block);
+/* n successive append_token calls; slots[i] = block * block_size + pos % block_size
+ * of the i-th new token (the slot_mapping air_kv_append consumes).  On failure
+ * *n_done tokens were appended (as n separate reference calls would leave). */
+int air_seq_append_slots(air_seq_manager *m, uint32_t seq, int32_t n, int64_t *slots,
+                         int32_t *n_done);
+/* fork_sequence (:290-310) */
+int air_seq_fork(air_seq_manager *m, uint32_t parent, uint32_t *child);
+/* free_sequence (:313-319): unknown ids are ignored, as in the reference. */
+int air_seq_free(air_seq_manager *m, uint32_t seq);
+/* cow_last_block (:327-335): AIR_KV_E_NOT_FOUND where the reference returns
+ * None for a missing sequence or an empty table, AIR_KV_E_OOM for a failed
+ * allocation.  *old_block / *new_block tell the caller which page to copy. */
+int air_seq_cow_last_block(air_seq_manager *m, uint32_t seq, uint32_t *old_block,
+                           uint32_t *new_block);
+/* table (:322-324): copies up to `cap` block ids. */
+int air_seq_table(const air_seq_manager *m, uint32_t seq, uint32_t *blocks, int32_t cap,
+                  int32_t *n_blocks, int64_t *n_tokens);
+/* Flattened int32 block tables [n][max_blocks] (unused entries = -1) and
+ * int32 seq_lens[n] for the device kernels (BlockTable, :202-235). */
+int air_seq_export_tables(const air_seq_manager *m, const uint32_t *seqs, int32_t n,
+                          int32_t max_blocks, int32_t *tables, int32_t *seq_lens);
+/* num_sequences (:338-340), can_schedule (:344-346) */
+int64_t air_seq_num_sequences(const air_seq_manager *m);
+int air_seq_can_schedule(const air_seq_manager *m);
+/* swap_out (:353-362): releases the blocks and returns their ids. */
+int air_seq_swap_out(air_seq_manager *m, uint32_t seq, uint32_t *blocks, int32_t cap,
+                     int32_t *n_blocks);
+/* swap_in (:369-381): allocates n fresh blocks for the sequence. */
+int air_seq_swap_in(air_seq_manager *m, uint32_t seq, int32_t n_blocks, uint32_t *blocks);
+
+/* Replaces KvSwapManager (src/kv_swap.rs:22-121).  The reference's
+ * gpu_read / gpu_write closures (:55-57, :83-86) become callbacks; the pair
+ * air_kv_pool_read_cb / air_kv_pool_write_cb binds them to a device pool. */
+typedef void (*air_kv_block_read_fn)(void *ctx, uint32_t block, uint8_t *dst, size_t bytes);
+typedef void (*air_kv_block_write_fn)(void *ctx, uint32_t block, const uint8_t *src, size_t bytes);
+typedef struct air_kv_swap air_kv_swap;
+int air_kv_swap_create(int64_t capacity, int32_t block_size, size_t block_bytes, air_kv_swap **out);
+int air_kv_swap_destroy(air_kv_swap *s);
+air_seq_manager *air_kv_swap_seq_manager(air_kv_swap *s);
+/* evict (:55-74): copies every block of the sequence to host memory, then swap_out. */
+int air_kv_swap_evict(air_kv_swap *s, uint32_t seq, air_kv_block_read_fn read, void *ctx,
+                      uint32_t *released, int32_t cap, int32_t *n_released);
+/* restore (:83-98): swap_in, then writes the saved bytes to the new blocks.
+ * As in the reference, the saved bytes are dropped if swap_in fails. */
+int air_kv_swap_restore(air_kv_swap *s, uint32_t seq, air_kv_block_write_fn write, void *ctx,
+                        uint32_t *blocks, int32_t cap, int32_t *n_blocks);
+int air_kv_swap_is_evicted(const air_kv_swap *s, uint32_t seq);
+int64_t air_kv_swap_evicted_count(const air_kv_swap *s);
+int64_t air_kv_swap_cpu_bytes_used(const air_kv_swap *s);
+/* maybe_evict (:112-121): *evicted = 1 when an eviction happened. */
+int air_kv_swap_maybe_evict(air_kv_swap *s, uint32_t seq, int64_t free_threshold,
+                            air_kv_block_read_fn read, void *ctx, int32_t *evicted);
+
+/* ======================================================================== */
+/* Device side: the paged pool and its kernels                              */
+/* ======================================================================== */
+
+typedef struct air_kv_pool_desc {
+    int64_t num_blocks;  /* pool capacity in blocks (MAX_BLOCKS, src/paged_attention.rs:45, as a runtime value) */
+    int32_t block_size;  /* tokens per block; 16 or 32 (reference default 16) */
+    int32_t n_kv_heads;
+    int32_t head_dim;    /* multiple of 32, at most 256 */
+    int32_t dtype;       /* AIR_KV_F32 / BF16 / INT8 / FP8 */
+    int32_t scale_group; /* elements per scale along head_dim (INT8/FP8); 32 = Q8_0 (src/kv_cache.rs:26) */
+} air_kv_pool_desc;
+
+typedef struct air_kv_pool air_kv_pool;
+
+/* Allocates the pool on the current HIP device.  Pages are zero-filled. */
+int air_kv_pool_create(const air_kv_pool_desc *desc, air_kv_pool **out);
+int air_kv_pool_destroy(air_kv_pool *pool);
+/* Pool geometry, device base pointers and the bytes of one block
+ * (K + V + scales), the unit of air_kv_read_blocks / write_blocks. */
+int air_kv_pool_info(const air_kv_pool *pool, air_kv_pool_desc *desc, void **k_pages,
+                     void **v_pages, void **k_scales, void **v_scales, size_t *block_bytes);
+
+/* Reshape-and-cache: writes k[t][h][:], v[t][h][:] (f32, [n_tokens][n_kv_heads]
+ * [head_dim], device) into slot slot_mapping[t] (int64, device), converting to
+ * the pool dtype (bf16 RNE; INT8/FP8 quantize each group of scale_group
+ * elements with its own scale).  Replaces the Tensor::cat append of
+ * src/model.rs:569 and the Q8 quantize of save_layer (src/kv_cache.rs:307-315).
+ * Negative slots are skipped; slots beyond the pool are skipped and counted
+ * (air_kv_pool_error_count). */
+int air_kv_append(air_kv_pool *pool, void *stream, const float *k, const float *v,
+                  const int64_t *slot_mapping, int32_t n_tokens);
+
+/* Gather: copies sequence b's first seq_lens[b] tokens from its pages into
+ * out_k / out_v + out_offsets[b] elements (all device pointers), in
+ * AIR_KV_LAYOUT_HEAD_MAJOR or TOKEN_MAJOR order, as out_dtype (AIR_KV_F32, or
+ * AIR_KV_BF16; INT8/FP8 pools are dequantized q*scale as in
+ * src/kv_cache.rs:78-92 and src/fp8.rs:263-264).  block_tables is int32
+ * [batch][max_blocks], seq_lens int32 [batch].  Replaces load_layer's dense
+ * view (src/kv_cache.rs:244-283).  Out-of-range table entries are skipped and
+ * counted. */
+int air_kv_gather(air_kv_pool *pool, void *stream, const int32_t *block_tables,
+                  const int32_t *seq_lens, const int64_t *out_offsets, int32_t batch,
+                  int32_t max_blocks, void *out_k, void *out_v, int32_t out_dtype,
+                  int32_t out_layout);
+
+/* Workspace bytes air_paged_decode needs for this launch shape. */
+int air_paged_decode_workspace_size(const air_kv_pool *pool, int32_t n_q_heads, int32_t batch,
+                                    int32_t max_blocks, int32_t max_splits, size_t *bytes);
+
+/* Split-K paged decode attention for one new token per sequence:
+ *   out[b][h] = softmax(q[b][h] . K_b[h / group]^T * scale) . V_b[h / group]
+ * over all seq_lens[b] cached tokens, group = n_q_heads / n_kv_heads (the GQA
+ * map of src/chunked_attn.rs:240-243).  Replaces ops::attention for seq_q = 1
+ * (src/ops.rs:333-357, :514-568) and generalises flash_decode
+ * (src/flash_decode.rs:153-173: split-K partials merged by log-sum-exp,
+ * :114-142) to paged storage.  q: [batch][n_q_heads][head_dim] as q_dtype
+ * (AIR_KV_F32 or AIR_KV_BF16); out likewise as out_dtype.  The reference's
+ * scale is 1/sqrt(head_dim).  max_splits bounds the partitions per sequence
+ * (1..256).  A sequence of length 0 produces zeros.  The workspace is device
+ * memory of at least air_paged_decode_workspace_size bytes. */
+int air_paged_decode(air_kv_pool *pool, void *stream, const void *q, int32_t q_dtype,
+                     int32_t n_q_heads, const int32_t *block_tables, const int32_t *seq_lens,
+                     int32_t batch, int32_t max_blocks, float scale, int32_t max_splits,
+                     void *workspace, size_t ws_bytes, void *out, int32_t out_dtype);
+
+/* Copies whole blocks src[i] -> dst[i] (int32, device): the page copy that
+ * BlockAllocator::cow_write leaves to "a real impl" (src/paged_attention.rs:160). */
+int air_kv_copy_blocks(air_kv_pool *pool, void *stream, const int32_t *src_blocks,
+                       const int32_t *dst_blocks, int32_t n);
+
+/* Page-granular device<->host copies for swap (the gpu_read / gpu_write
+ * closures of src/kv_swap.rs:55-98).  ids are host int32; host buffers hold
+ * n * block_bytes bytes, block i at offset i * block_bytes laid out as
+ * K slab, V slab, K scales, V scales.  Both calls synchronise the stream. */
+int air_kv_read_blocks(air_kv_pool *pool, void *stream, const int32_t *ids, int32_t n, void *host_dst);
+int air_kv_write_blocks(air_kv_pool *pool, void *stream, const int32_t *ids, int32_t n,
+                        const void *host_src);
+/* air_kv_block_read_fn / write_fn adapters over a pool (ctx = air_kv_pool*),
+ * on the default stream. */
+void air_kv_pool_read_cb(void *ctx, uint32_t block, uint8_t *dst, size_t bytes);
+void air_kv_pool_write_cb(void *ctx, uint32_t block, const uint8_t *src, size_t bytes);
+
+/* Number of out-of-range slots / table entries the kernels have skipped since
+ * the pool was created or last reset.  Synchronises the stream. */
+int air_kv_pool_error_count(air_kv_pool *pool, void *stream, int64_t *count, int32_t reset);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* AIR_KV_H */

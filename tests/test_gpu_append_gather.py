@@ -1,0 +1,260 @@
+"""GPU parity: append (reshape-and-cache, incl. quantize-on-append) and gather
+against the oracle, bit-exact, through the C ABI."""
+import numpy as np
+import pytest
+
+import airkv
+import oracle
+from airkv import workloads
+from gpu_helpers import (assert_bits_equal, device_pool_for, host_pool_for, log,
+                         replay_batches_on_oracle, run_appends, torch_mod)
+
+pytestmark = pytest.mark.gpu
+
+C1_PREFILL = [37, 128, 200, 511]
+
+
+def _seq_rows(w, prefill, steps):
+    """Source-row indices of each sequence, in append order."""
+    n = len(prefill)
+    rows = [[] for _ in range(n)]
+    off = 0
+    for i, L in enumerate(prefill):
+        rows[i].extend(range(off, off + L))
+        off += L
+    for _ in range(steps):
+        for i in range(n):
+            rows[i].append(off + i)
+        off += n
+    return rows
+
+
+def _gather(pool, tables, lens, out_dtype, layout):
+    torch = torch_mod()
+    per = lens.astype(np.int64) * pool.n_kv_heads * pool.head_dim
+    offs = np.concatenate([[0], np.cumsum(per)[:-1]]).astype(np.int64)
+    tdt = torch.float32 if out_dtype == airkv.F32 else torch.bfloat16
+    ok = torch.zeros(int(per.sum()), dtype=tdt, device="cuda")
+    ov = torch.zeros_like(ok)
+    pool.gather(torch.from_numpy(tables).cuda(), torch.from_numpy(lens).cuda(),
+                torch.from_numpy(offs).cuda(), ok, ov, out_dtype, layout)
+    torch.cuda.synchronize()
+    if out_dtype == airkv.F32:
+        return ok.cpu().numpy(), ov.cpu().numpy(), offs
+    return (ok.view(torch.int16).cpu().numpy().view(np.uint16),
+            ov.view(torch.int16).cpu().numpy().view(np.uint16), offs)
+
+
+@pytest.mark.parametrize("dtype", [airkv.F32, airkv.BF16, airkv.INT8, airkv.FP8])
+def test_c1_append_gather_bitexact(dtype):
+    log(f"c1 append/gather dtype={dtype}")
+    w = workloads.c1_workload()
+    w.cfg = workloads.Config(w.cfg.name, 8, 8, 64, 16, dtype, 4)
+    # block tables / slot mappings identical to the restated allocator
+    mgr_o, seqs_o, batches_o = replay_batches_on_oracle(w, C1_PREFILL, 16)
+    assert len(batches_o) == len(w.batches)
+    for a, b in zip(w.batches, batches_o):
+        assert np.array_equal(a, b)
+    k, v = next(workloads.kv_rows(w.n_rows, 8, 64, seed=11, chunk_rows=1 << 20))
+    pool, host = device_pool_for(w), host_pool_for(w)
+    run_appends(w, k, v, pool, host)
+    pk, pv, pks, pvs = pool.snapshot()
+    assert_bits_equal(pk, host.k, "k pages")
+    assert_bits_equal(pv, host.v, "v pages")
+    if dtype in (airkv.INT8, airkv.FP8):
+        assert_bits_equal(pks, host.k_scales, "k scales")
+        assert_bits_equal(pvs, host.v_scales, "v scales")
+    assert pool.error_count() == 0
+
+    tables, lens = w.tables()
+    assert lens.tolist() == [53, 144, 216, 527]
+    assert [int((t >= 0).sum()) for t in tables] == [4, 9, 14, 33]
+    for s, so in zip(w.seqs, seqs_o):
+        assert w.mgr.table(s).physical_blocks == mgr_o.table(so).physical_blocks
+    outs = [airkv.F32] if dtype == airkv.F32 else [airkv.F32, airkv.BF16]
+    rows = _seq_rows(w, C1_PREFILL, 16)
+    for out_dtype in outs:
+        for layout in (airkv.LAYOUT_HEAD_MAJOR, airkv.LAYOUT_TOKEN_MAJOR):
+            gk, gv, offs = _gather(pool, tables, lens, out_dtype, layout)
+            hk, hv, hoffs, bad = host.gather(tables, lens, out_dtype, layout)
+            assert bad == 0 and np.array_equal(offs, hoffs)
+            assert_bits_equal(gk, hk, f"gathered k out={out_dtype} layout={layout}")
+            assert_bits_equal(gv, hv, f"gathered v out={out_dtype} layout={layout}")
+            if dtype == airkv.F32 and layout == airkv.LAYOUT_TOKEN_MAJOR:
+                # gather(append(x)) == x, bit for bit
+                for b, r in enumerate(rows):
+                    n = len(r) * 8 * 64
+                    assert_bits_equal(gk[offs[b]:offs[b] + n].reshape(len(r), 8, 64), k[r], "roundtrip k")
+                    assert_bits_equal(gv[offs[b]:offs[b] + n].reshape(len(r), 8, 64), v[r], "roundtrip v")
+    if dtype == airkv.BF16:
+        gk, _, offs = _gather(pool, tables, lens, airkv.BF16, airkv.LAYOUT_TOKEN_MAJOR)
+        for b, r in enumerate(rows):
+            n = len(r) * 8 * 64
+            assert_bits_equal(gk[offs[b]:offs[b] + n].reshape(len(r), 8, 64),
+                              oracle.bf16_from_f32(k[r]), "bf16 roundtrip == rne(x)")
+    if dtype == airkv.INT8:
+        # the direct pin: dequantized gather of sequence b equals the
+        # reference Q8Tensor::quantize/dequantize of its dense [seq, heads,
+        # dim] tensor flattened (src/kv_cache.rs:307-315, :54-92)
+        gk, _, offs = _gather(pool, tables, lens, airkv.F32, airkv.LAYOUT_TOKEN_MAJOR)
+        for b, r in enumerate(rows):
+            q, s = oracle.q8_quantize(k[r].reshape(-1))
+            n = len(r) * 8 * 64
+            assert_bits_equal(gk[offs[b]:offs[b] + n], oracle.q8_dequantize(q, s), "Q8Tensor pin")
+
+
+def test_untouched_slots_keep_their_contents():
+    """Every appended slot is written exactly once; all other bytes of the
+    pool are left alone (pages pre-filled with a sentinel via write_blocks)."""
+    torch = torch_mod()
+    w = workloads.c1_workload(seed=9)
+    w.cfg = workloads.Config(w.cfg.name, 8, 8, 64, 16, airkv.BF16, 4)
+    pool, host = device_pool_for(w), host_pool_for(w, fill=0x7BCD)
+    sentinel = np.full((w.num_blocks, pool.block_bytes // 2), 0x7BCD, np.uint16).view(np.uint8)
+    pool.write_blocks(np.arange(w.num_blocks, dtype=np.int32), sentinel)
+    k, v = next(workloads.kv_rows(w.n_rows, 8, 64, seed=12, chunk_rows=1 << 20))
+    run_appends(w, k, v, pool, host)
+    pk, pv, _, _ = pool.snapshot()
+    assert_bits_equal(pk, host.k, "k pages")
+    assert_bits_equal(pv, host.v, "v pages")
+    written = set()
+    for slots in w.batches:
+        for s in slots.tolist():
+            assert s not in written
+            written.add(s)
+    assert len(written) == w.n_rows
+    untouched = np.ones(w.num_blocks * 16, bool)
+    untouched[list(written)] = False
+    rows = pk.transpose(0, 2, 1, 3).reshape(w.num_blocks * 16, -1)
+    assert np.all(rows[untouched] == 0x7BCD)
+    torch.cuda.synchronize()
+
+
+def _special_rows(n_rows, d, seed):
+    rng = np.random.default_rng(seed)
+    bits = rng.integers(0, 2 ** 32, size=(n_rows, d), dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32).copy()
+    specials = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1e-40, -1e-40, 1.4e-45, 448.0, -448.0,
+                         256.0, 255.99998, 240.0, 1.0625, -1.0625, 1.9375, 2.5, -2.5, 0.5,
+                         3.4e38, -3.4e38, 1e-8, 9e-9, 127.0], np.float32)
+    for i in range(0, n_rows, 3):
+        x[i, :len(specials)] = specials
+        rng.shuffle(x[i])
+    # some rows of small normal values (realistic magnitudes)
+    x[1::3] = rng.standard_normal((len(x[1::3]), d)).astype(np.float32)
+    # rows with one huge outlier per group
+    x[2::3] = rng.standard_normal((len(x[2::3]), d)).astype(np.float32)
+    x[2::3, ::32] *= 1e4
+    return x
+
+
+@pytest.mark.parametrize("dtype", [airkv.BF16, airkv.INT8, airkv.FP8])
+def test_codec_edge_cases_bitexact(dtype):
+    """Random bit patterns (NaN, inf, denormals, huge) plus hand-picked
+    boundary values: codes and scales match the oracle bit for bit."""
+    torch = torch_mod()
+    log(f"codec edge cases dtype={dtype}")
+    nkv, d, bs, nb = 4, 128, 16, 64
+    n = nb * bs
+    k = _special_rows(n * nkv, d, 21).reshape(n, nkv, d)
+    v = _special_rows(n * nkv, d, 22).reshape(n, nkv, d)
+    slots = workloads.lcg_permutation(n, 5).astype(np.int64)
+    pool = airkv.KvPool(nb, bs, nkv, d, dtype, 32)
+    host = oracle.HostPool(nb, bs, nkv, d, dtype, 32)
+    pool.append(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(), torch.from_numpy(slots).cuda())
+    host.append(k, v, slots)
+    pk, pv, pks, pvs = pool.snapshot()
+    assert_bits_equal(pk, host.k, "k codes")
+    assert_bits_equal(pv, host.v, "v codes")
+    if dtype != airkv.BF16:
+        assert_bits_equal(pks, host.k_scales, "k scales")
+        assert_bits_equal(pvs, host.v_scales, "v scales")
+
+
+def test_fp8_encoder_sweep_all_high_halves():
+    """The encoder's result depends only on the sign, exponent and the top
+    four mantissa bits (plus NaN-ness), so every 16-bit high half with low
+    halves {0x0000, 0x0001, 0xFFFF} exercises every branch and rounding
+    case.  Groups carry 448.0 so the scale is exactly 1 and the code is
+    F8E4M3::from_f32(x) itself."""
+    torch = torch_mod()
+    log("fp8 encoder sweep")
+    hi = np.arange(1 << 16, dtype=np.uint32) << 16
+    xs = np.concatenate([(hi | lo).view(np.float32) for lo in (0x0000, 0x0001, 0xFFFF)])
+    a = np.abs(xs)
+    xs = xs[~(a > 448.0)]                      # keeps NaNs and |x| <= 448
+    per_group = 31
+    ng = -(-len(xs) // per_group)
+    pad = np.zeros(ng * per_group, np.float32)
+    pad[:len(xs)] = xs
+    groups = np.concatenate([np.full((ng, 1), 448.0, np.float32), pad.reshape(ng, per_group)], 1)
+    d = 128
+    nrows = -(-groups.shape[0] // 4)          # 4 groups of 32 per row
+    full = np.zeros((nrows * 4, 32), np.float32)
+    full[:, 0] = 448.0
+    full[:groups.shape[0]] = groups
+    rows = full.reshape(nrows, 1, d)
+    bs = 16
+    nb = -(-nrows // bs)
+    pool = airkv.KvPool(nb, bs, 1, d, airkv.FP8, 32)
+    slots = torch.arange(nrows, dtype=torch.int64, device="cuda")
+    t = torch.from_numpy(rows).cuda()
+    pool.append(t, t, slots)
+    pk, _, pks, _ = pool.snapshot()
+    codes = pk.reshape(-1, 32)[:full.shape[0]]
+    scales = pks.reshape(-1)[:full.shape[0]]
+    assert np.all(scales == 1.0)
+    want = oracle.fp8_from_f32(full)
+    assert_bits_equal(codes, want, "fp8 codes")
+
+
+def test_invalid_slots_are_skipped_and_counted():
+    torch = torch_mod()
+    pool = airkv.KvPool(4, 16, 2, 64, airkv.BF16, 32)
+    pool.error_count(reset=True)
+    k = torch.randn(3, 2, 64, device="cuda")
+    slots = torch.tensor([5, 64, -1], dtype=torch.int64, device="cuda")   # 64 == 4 * 16: out of range
+    pool.append(k, k, slots)
+    assert pool.error_count(reset=True) == 1
+    pk, _, _, _ = pool.snapshot()
+    rows = pk.transpose(0, 2, 1, 3).reshape(64, 2, 64)
+    assert np.array_equal(rows[5], oracle.bf16_from_f32(k[0].cpu().numpy()))
+    assert np.count_nonzero(np.delete(rows, 5, axis=0)) == 0
+    # a table entry outside the pool within seq_len: skipped and counted
+    tables = torch.tensor([[0, 99]], dtype=torch.int32, device="cuda")
+    lens = torch.tensor([20], dtype=torch.int32, device="cuda")
+    out = torch.zeros(20 * 2 * 64, dtype=torch.bfloat16, device="cuda")
+    pool.gather(tables, lens, torch.zeros(1, dtype=torch.int64, device="cuda"), out, out.clone())
+    assert pool.error_count(reset=True) >= 1
+
+
+def test_copy_blocks_and_swap_roundtrip():
+    """CoW page copy, and evict/restore through the pool-backed swap
+    callbacks: restored pages hold the evicted bytes under new block ids."""
+    torch = torch_mod()
+    cfg = workloads.Config("swap", 8, 4, 128, 16, airkv.INT8, 2)
+    pool = airkv.KvPool(32, 16, 4, 128, airkv.INT8, 32)
+    swap = airkv.KvSwapManager(32, pool.block_bytes, 16)
+    mgr = swap.seq_mgr
+    s = mgr.create_sequence()
+    slots = mgr.append_slots(s, 40)
+    k = torch.randn(40, 4, 128, device="cuda")
+    v = torch.randn(40, 4, 128, device="cuda")
+    pool.append(k, v, torch.from_numpy(slots).cuda())
+    before = pool.read_blocks(mgr.table(s).physical_blocks)
+    # CoW: fork, copy the shared last block, compare
+    c = mgr.fork_sequence(s)
+    old, new = mgr.cow_last_block(c)
+    assert old != new
+    pool.copy_blocks(torch.tensor([old], dtype=torch.int32, device="cuda"),
+                     torch.tensor([new], dtype=torch.int32, device="cuda"))
+    assert np.array_equal(pool.read_blocks([new]), pool.read_blocks([old]))
+    mgr.free_sequence(c)
+    cb = airkv.pool_callbacks(pool)
+    released = swap.evict(s, cb[0:1] + cb[2:3])
+    assert len(released) == 3 and swap.is_evicted(s)
+    # scribble over the released blocks
+    pool.write_blocks(released, np.zeros((3, pool.block_bytes), np.uint8))
+    new_blocks = swap.restore(s, cb[1:2] + cb[2:3])
+    assert len(new_blocks) == 3
+    assert np.array_equal(pool.read_blocks(new_blocks), before)

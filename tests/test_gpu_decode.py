@@ -1,0 +1,190 @@
+"""GPU parity: split-K paged decode attention against the oracle (gather +
+flash_decode with chunk 64, src/flash_decode.rs:153-173) through the C ABI.
+
+Tolerances (relative to max |reference|): 1e-3 for f32/bf16 caches and 2e-2
+for int8/fp8 caches, the oracle running on the same dequantized cache.
+"""
+import numpy as np
+import pytest
+
+import airkv
+import oracle
+from airkv import workloads
+from gpu_helpers import (device_pool_for, host_pool_for, log, rel_err, run_appends, torch_mod)
+
+pytestmark = pytest.mark.gpu
+
+TOL = {airkv.F32: 1e-3, airkv.BF16: 1e-3, airkv.INT8: 2e-2, airkv.FP8: 2e-2}
+
+
+def _decode_case(cfg, lens, seed, q_bf16=True, max_splits=64, outliers=None, out_bf16=False):
+    torch = torch_mod()
+    w = workloads.build_prefill_decode(cfg, lens, seed, decode_steps=1)
+    k, v = next(workloads.kv_rows(w.n_rows, cfg.n_kv_heads, cfg.head_dim, seed=seed + 100,
+                                  outliers=outliers, chunk_rows=1 << 24))
+    pool, host = device_pool_for(w), host_pool_for(w)
+    run_appends(w, k, v, pool, host)
+    tables, seq_lens = w.tables()
+    rng = np.random.default_rng(seed + 7)
+    q = rng.standard_normal((cfg.batch, cfg.n_q_heads, cfg.head_dim)).astype(np.float32)
+    qt = torch.from_numpy(q).cuda()
+    if q_bf16:
+        qt = qt.to(torch.bfloat16)
+        q = qt.float().cpu().numpy()
+    out = torch.zeros(q.shape, dtype=torch.bfloat16 if out_bf16 else torch.float32, device="cuda")
+    pool.paged_decode(qt, torch.from_numpy(tables).cuda(), torch.from_numpy(seq_lens).cuda(), out,
+                      max_splits=max_splits)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    want = host.paged_decode(q, tables, seq_lens, chunk=64)
+    assert pool.error_count() == 0
+    return got, want, (pool, host, tables, seq_lens, q)
+
+
+@pytest.mark.parametrize("dtype", [airkv.F32, airkv.BF16, airkv.INT8, airkv.FP8])
+@pytest.mark.parametrize("group", [1, 4, 8])
+def test_decode_matches_oracle_small(dtype, group):
+    log(f"decode small dtype={dtype} group={group}")
+    nkv = 2 if group == 8 else 4
+    cfg = workloads.Config("small", nkv * group, nkv, 128, 16, dtype, 5)
+    lens = [1, 17, 64, 300, 777]
+    got, want, _ = _decode_case(cfg, lens, seed=30 + group)
+    err = rel_err(got, want)
+    log(f"  rel err {err:.2e}")
+    assert err <= TOL[dtype]
+
+
+def test_c2_shape_bf16_scaled():
+    """configs[1] geometry (32 q / 8 kv, d 128, bs 16) at batch 8 and
+    contexts U[512, 1500], q in bf16."""
+    cfg = workloads.Config("c2s", 32, 8, 128, 16, airkv.BF16, 8)
+    lens = workloads.c2_lengths(8, 512, 1500, seed=2)
+    got, want, _ = _decode_case(cfg, lens, seed=41)
+    err = rel_err(got, want)
+    log(f"c2 scaled rel err {err:.2e}")
+    assert err <= 1e-3
+
+
+def test_c3_shape_int8_outliers_scaled():
+    """configs[2] geometry (64 q / 8 kv, int8 Q8_0) with 1% outlier channels
+    x20, batch 3, context 1000."""
+    cfg = workloads.Config("c3s", 64, 8, 128, 16, airkv.INT8, 3)
+    out_ch = workloads.outlier_channels(8, 128)
+    got, want, _ = _decode_case(cfg, [1000, 1000, 1000], seed=43, outliers=out_ch)
+    err = rel_err(got, want)
+    log(f"c3 scaled rel err {err:.2e}")
+    assert err <= 2e-2
+
+
+def test_c4_shape_fp8_many_splits():
+    """configs[3] geometry (fp8, bs 32) with contexts long enough to use the
+    maximum of 64 partitions."""
+    cfg = workloads.Config("c4s", 64, 8, 128, 32, airkv.FP8, 2)
+    got, want, (pool, _, tables, _, _) = _decode_case(cfg, [20000, 9000], seed=44)
+    ws = pool.decode_workspace_size(64, 2, tables.shape[1], 64)
+    assert ws == 2 * 64 * 64 * 130 * 4            # 64 partitions in use
+    err = rel_err(got, want)
+    log(f"c4 scaled rel err {err:.2e}")
+    assert err <= 2e-2
+
+
+@pytest.mark.parametrize("kv_len,seed_q,bound,chunk", [(128, 1, 1e-4, 32), (4096, 10, 1e-3, 64),
+                                                       (32, 20, 1e-5, 32)])
+def test_reference_flash_decode_inputs(kv_len, seed_q, bound, chunk):
+    """The reference's own flash_decode tests (src/flash_decode.rs:232-275):
+    the same LCG inputs (HD 64, one head) stored in an f32 paged pool; the
+    GPU output must meet the reference's L-inf bound against
+    reference_attention."""
+    torch = torch_mod()
+    hd = 64
+    q = oracle.lcg_fill(seed_q, hd)
+    k = oracle.lcg_fill(seed_q + 1, kv_len * hd).reshape(kv_len, 1, hd)
+    v = oracle.lcg_fill(seed_q + 2, kv_len * hd).reshape(kv_len, 1, hd)
+    nb = -(-kv_len // 16)
+    pool = airkv.KvPool(nb, 16, 1, hd, airkv.F32, 32)
+    slots = torch.from_numpy(workloads.lcg_permutation(nb, 77).astype(np.int64)).cuda()
+    slots = (slots[:, None] * 16 + torch.arange(16, device="cuda")[None, :]).reshape(-1)[:kv_len]
+    pool.append(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(), slots.contiguous())
+    table = (slots[::16] // 16).to(torch.int32).reshape(1, -1).contiguous()
+    out = torch.zeros(1, 1, hd, device="cuda")
+    pool.paged_decode(torch.from_numpy(q).cuda().reshape(1, 1, hd), table,
+                      torch.tensor([kv_len], dtype=torch.int32, device="cuda"), out)
+    got = out.cpu().numpy().reshape(hd)
+    want = oracle.reference_attention(q, k.reshape(-1), v.reshape(-1), kv_len, hd)
+    assert oracle.max_abs_error(got, want) < bound
+    assert oracle.max_abs_error(got, oracle.flash_decode(q, k.reshape(-1), v.reshape(-1), kv_len, hd,
+                                                         chunk)) < bound
+
+
+def test_special_cases():
+    """Closed forms: a single token returns its V row; identical keys give the
+    mean of V; an empty sequence gives zeros; max_splits does not change the
+    answer beyond rounding."""
+    torch = torch_mod()
+    d = 128
+    pool = airkv.KvPool(64, 16, 1, d, airkv.F32, 32)
+    k = torch.randn(1, d, device="cuda").repeat(200, 1).reshape(200, 1, d)
+    v = torch.randn(200, 1, d, device="cuda")
+    pool.append(k.contiguous(), v, torch.arange(200, dtype=torch.int64, device="cuda"))
+    table = torch.arange(13, dtype=torch.int32, device="cuda").reshape(1, 13).repeat(3, 1).contiguous()
+    lens = torch.tensor([1, 200, 0], dtype=torch.int32, device="cuda")
+    q = torch.randn(3, 1, d, device="cuda")
+    out = torch.full((3, 1, d), 7.0, device="cuda")
+    pool.paged_decode(q, table, lens, out, max_splits=1)
+    assert torch.equal(out[0, 0], v[0, 0])
+    assert torch.allclose(out[1, 0], v.mean(0)[0], atol=1e-5)
+    assert torch.count_nonzero(out[2]) == 0
+    out2 = torch.empty_like(out)
+    pool.paged_decode(q, table, lens, out2, max_splits=64)
+    assert torch.allclose(out, out2, atol=1e-5)
+
+
+def test_full_c2_against_torch_fp32():
+    """configs[1] at full size (batch 64, contexts U[512, 4096], pool 1.25x):
+    the paged decode agrees with a plain torch float32 attention over the
+    gathered per-sequence K/V within 1e-3 relative."""
+    torch = torch_mod()
+    log("full c2")
+    cfg = workloads.CONFIGS["c2"]
+    lens = workloads.c2_lengths()
+    w = workloads.build_prefill_decode(cfg, lens, seed=2)
+    pool = device_pool_for(w)
+    gen = workloads.kv_rows(w.n_rows, 8, 128, seed=5, device="cuda", chunk_rows=1 << 16)
+    buf_k, buf_v, have = None, None, 0
+    for slots in w.batches:
+        n = len(slots)
+        parts_k, parts_v = [], []
+        while n > 0:
+            if buf_k is None or have == buf_k.shape[0]:
+                buf_k, buf_v = next(gen)
+                have = 0
+            take = min(n, buf_k.shape[0] - have)
+            parts_k.append(buf_k[have:have + take])
+            parts_v.append(buf_v[have:have + take])
+            have += take
+            n -= take
+        pool.append(torch.cat(parts_k).contiguous(), torch.cat(parts_v).contiguous(),
+                    torch.from_numpy(slots).cuda())
+    tables, seq_lens = w.tables()
+    tt, lt = torch.from_numpy(tables).cuda(), torch.from_numpy(seq_lens).cuda()
+    q = torch.randn(64, 32, 128, device="cuda").to(torch.bfloat16)
+    out = torch.empty(64, 32, 128, device="cuda")
+    pool.paged_decode(q, tt, lt, out)
+    per = seq_lens.astype(np.int64) * 8 * 128
+    offs = np.concatenate([[0], np.cumsum(per)[:-1]]).astype(np.int64)
+    gk = torch.empty(int(per.sum()), dtype=torch.bfloat16, device="cuda")
+    gv = torch.empty_like(gk)
+    pool.gather(tt, lt, torch.from_numpy(offs).cuda(), gk, gv)
+    worst = 0.0
+    for b in range(64):
+        L = int(seq_lens[b])
+        K = gk[offs[b]:offs[b] + L * 1024].view(8, L, 128).float()
+        V = gv[offs[b]:offs[b] + L * 1024].view(8, L, 128).float()
+        qb = q[b].float().view(8, 4, 128)
+        s = torch.matmul(qb, K.transpose(1, 2).contiguous()) / np.sqrt(128.0)
+        p = torch.softmax(s, dim=-1)
+        ref = torch.matmul(p, V).reshape(32, 128)
+        worst = max(worst, (out[b] - ref).abs().max().item() / ref.abs().max().item())
+    log(f"full c2 worst rel err {worst:.2e}")
+    assert worst <= 1e-3
+    assert pool.error_count() == 0
