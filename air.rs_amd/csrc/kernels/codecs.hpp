@@ -52,6 +52,16 @@ __device__ __forceinline__ float fp8_decode(uint32_t b) {
     return b == 0x7Fu ? __uint_as_float(0x7FC00000u) : v;
 }
 
+// One step of the absmax fold `m.max(v.abs())` (src/kv_cache.rs:60,
+// src/fp8.rs:228-232): Rust's f32::max returns the other operand when one is
+// NaN, signalling or quiet.  v_max_f32 in IEEE mode turns a signalling NaN
+// into a quiet NaN result instead, so the fold is a compare-select, which
+// ignores every NaN and never produces one from a non-NaN accumulator.
+__device__ __forceinline__ float absmax_step(float m, float x) {
+    const float a = fabsf(x);
+    return a > m ? a : m;
+}
+
 // Rust `f32::round` then saturating `as i8` after a clamp to +-127
 // (src/kv_cache.rs:69): NaN -> 0.
 __device__ __forceinline__ int8_t q8_code(float x, float inv) {

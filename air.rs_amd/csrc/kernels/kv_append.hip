@@ -54,8 +54,8 @@ __device__ __forceinline__ void store_row_chunk(const float (&x)[8], void *pages
         // reduction equals the reference's sequential fold.
         float m = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(x[j]));
-        for (int mask = 1; mask < lanes_per_group; mask <<= 1) m = fmaxf(m, __shfl_xor(m, mask));
+        for (int j = 0; j < 8; ++j) m = absmax_step(m, x[j]);
+        for (int mask = 1; mask < lanes_per_group; mask <<= 1) m = absmax_step(m, __shfl_xor(m, mask));
         uint32_t lo = 0, hi = 0;
         float scale;
         if constexpr (DT == AIR_KV_INT8) {

@@ -8,7 +8,9 @@
  * exactly once, as Rust's f32 arithmetic does (Rust never contracts a*b+c).
  * Rust scalar facts relied upon (language spec): f32::round rounds half away
  * from zero (C roundf); `x as i8` saturates and maps NaN to 0; f32::max
- * returns the non-NaN operand (C fmaxf); `u32::MAX as f32` is 4294967296.0f.
+ * returns the other operand when one is NaN, signalling NaNs included
+ * (rust_max below; glibc fmaxf instead returns NaN for a signalling NaN);
+ * `u32::MAX as f32` is 4294967296.0f.
  *
  * Parity status of each function is recorded in its header comment; the
  * checks live in tests/test_oracle_*.py.
@@ -20,6 +22,14 @@
 #include <string.h>
 
 static inline uint32_t f2u(float x) { uint32_t u; memcpy(&u, &x, 4); return u; }
+
+/* Rust f32::max: "If one of the arguments is NaN, then the other argument is
+ * returned", for quiet and signalling NaNs alike. */
+static inline float rust_max(float a, float b) {
+    if (isnan(a)) return b;
+    if (isnan(b)) return a;
+    return a > b ? a : b;
+}
 static inline float u2f(uint32_t u) { float x; memcpy(&x, &u, 4); return x; }
 
 /* ------------------------------------------------------------------------ */
@@ -52,7 +62,7 @@ void orc_box_muller_fill(uint64_t seed, float *out, size_t n) {
         float u1 = (float)(state >> 11) / two53;
         state = state * 6364136223846793005ULL + 1442695040888963407ULL;
         float u2 = (float)(state >> 11) / two53;
-        u1 = fmaxf(u1, 1e-10f);
+        u1 = rust_max(u1, 1e-10f);
         float r = sqrtf(-2.0f * logf(u1));
         float theta = 2.0f * 3.14159265358979323846f * u2;
         out[i++] = r * cosf(theta);
@@ -137,7 +147,7 @@ static inline int8_t rust_as_i8(float r) {
  * q = clamp(round(x * inv), -127, 127) as i8 (clamp keeps NaN, cast -> 0). */
 float orc_q8_quantize_group(const float *x, int n, int8_t *q) {
     float max_abs = 0.0f;
-    for (int i = 0; i < n; ++i) max_abs = fmaxf(max_abs, fabsf(x[i]));
+    for (int i = 0; i < n; ++i) max_abs = rust_max(max_abs, fabsf(x[i]));
     float scale = (max_abs == 0.0f) ? 1.0f : max_abs / 127.0f;
     float inv = 1.0f / scale;
     for (int i = 0; i < n; ++i) {
@@ -167,7 +177,7 @@ void orc_q8_dequantize(const int8_t *q, const float *scales, size_t n, float *ou
  * code = F8E4M3::from_f32(x / scale) (a true division, :237). */
 float orc_fp8_quantize_group(const float *x, int n, uint8_t *q) {
     float max_abs = 0.0f;
-    for (int i = 0; i < n; ++i) max_abs = fmaxf(max_abs, fabsf(x[i]));
+    for (int i = 0; i < n; ++i) max_abs = rust_max(max_abs, fabsf(x[i]));
     float scale = (max_abs < 1e-8f) ? 1.0f : max_abs / 448.0f;
     for (int i = 0; i < n; ++i) q[i] = orc_fp8_from_f32(x[i] / scale);
     return scale;
@@ -177,7 +187,7 @@ float orc_fp8_quantize_group(const float *x, int n, uint8_t *q) {
  * bf16 buffer, no clamp, saturating `as i8`. */
 float orc_pd_int8_quantize(const uint16_t *bf16, size_t n, int8_t *q) {
     float max_val = 0.0f;
-    for (size_t i = 0; i < n; ++i) max_val = fmaxf(max_val, fabsf(orc_bf16_to_f32(bf16[i])));
+    for (size_t i = 0; i < n; ++i) max_val = rust_max(max_val, fabsf(orc_bf16_to_f32(bf16[i])));
     float scale = max_val > 0.0f ? max_val / 127.0f : 1.0f;
     float inv = 1.0f / scale;
     for (size_t i = 0; i < n; ++i) q[i] = rust_as_i8(roundf(orc_bf16_to_f32(bf16[i]) * inv));
@@ -321,7 +331,7 @@ void orc_chunk_attention(const float *q, const float *k_chunk, const float *v_ch
         scores[i] = dot * scale;
     }
     float m = -INFINITY;
-    for (int i = 0; i < chunk_len; ++i) m = fmaxf(m, scores[i]);
+    for (int i = 0; i < chunk_len; ++i) m = rust_max(m, scores[i]);
     float l = 0.0f;
     for (int i = 0; i < chunk_len; ++i) { scores[i] = expf(scores[i] - m); l += scores[i]; }
     for (int j = 0; j < head_dim; ++j) out[j] = 0.0f;
@@ -340,7 +350,7 @@ int orc_reduce_chunks(const float *outs, const float *maxes, const float *sums,
                       int n_chunks, int head_dim, float *out) {
     if (n_chunks <= 0) return -1;
     float gm = -INFINITY;
-    for (int p = 0; p < n_chunks; ++p) gm = fmaxf(gm, maxes[p]);
+    for (int p = 0; p < n_chunks; ++p) gm = rust_max(gm, maxes[p]);
     float *rs = (float *)malloc(sizeof(float) * (size_t)n_chunks);
     float total = 0.0f;
     for (int p = 0; p < n_chunks; ++p) { rs[p] = expf(maxes[p] - gm) * sums[p]; total += rs[p]; }
@@ -384,7 +394,7 @@ void orc_reference_attention(const float *q, const float *k, const float *v,
         s[i] = dot * scale;
     }
     float m = -INFINITY;
-    for (int i = 0; i < kv_len; ++i) m = fmaxf(m, s[i]);
+    for (int i = 0; i < kv_len; ++i) m = rust_max(m, s[i]);
     float sum = 0.0f;
     for (int i = 0; i < kv_len; ++i) { s[i] = expf(s[i] - m); sum += s[i]; }
     for (int j = 0; j < head_dim; ++j) out[j] = 0.0f;

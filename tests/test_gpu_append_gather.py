@@ -171,6 +171,41 @@ def test_codec_edge_cases_bitexact(dtype):
         assert_bits_equal(pvs, host.v_scales, "v scales")
 
 
+def _q8_tie_groups(n_groups, seed):
+    """Groups of 32 N(0,1) values in which some x * (1/scale) rounds (in f32)
+    to an exact k + 0.5 while the exact product does not: f32::round must
+    see the rounded product (half away from zero), not a fused one."""
+    rng = np.random.default_rng(seed)
+    found = []
+    while len(found) < n_groups:
+        x = rng.standard_normal((1 << 15, 32)).astype(np.float32)
+        m = np.abs(x).max(1)
+        scale = m / np.float32(127.0)
+        inv = np.float32(1.0) / scale
+        prod = x * inv[:, None]
+        tie = (prod - np.trunc(prod) == np.float32(0.5)) | (prod - np.trunc(prod) == np.float32(-0.5))
+        exact = x.astype(np.float64) * inv.astype(np.float64)[:, None]
+        tie &= exact != prod.astype(np.float64)
+        for i in np.nonzero(tie.any(1))[0][: n_groups - len(found)]:
+            found.append(x[i])
+    return np.stack(found)
+
+
+def test_q8_rounding_ties_bitexact():
+    torch = torch_mod()
+    groups = _q8_tie_groups(64, 31)             # 64 groups -> 16 rows of 128
+    rows = groups.reshape(16, 1, 128)
+    pool = airkv.KvPool(1, 16, 1, 128, airkv.INT8, 32)
+    host = oracle.HostPool(1, 16, 1, 128, airkv.INT8, 32)
+    t = torch.from_numpy(rows).cuda()
+    slots = np.arange(16, dtype=np.int64)
+    pool.append(t, t, torch.from_numpy(slots).cuda())
+    host.append(rows, rows, slots)
+    pk, _, pks, _ = pool.snapshot()
+    assert_bits_equal(pks, host.k_scales, "tie scales")
+    assert_bits_equal(pk, host.k, "tie codes")
+
+
 def test_fp8_encoder_sweep_all_high_halves():
     """The encoder's result depends only on the sign, exponent and the top
     four mantissa bits (plus NaN-ness), so every 16-bit high half with low

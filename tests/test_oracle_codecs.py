@@ -262,6 +262,24 @@ def test_q8_closed_forms():
     assert len(s) == 2 and s[1] == np.float32(39.0) / np.float32(127.0)
 
 
+@pytest.mark.parametrize("nan_bits", [0x7F800001, 0xFFBFFFFF, 0x7FC00000, 0xFFC00001])
+def test_absmax_ignores_every_nan(nan_bits):
+    """Rust's f32::max returns the other operand when one is NaN, signalling
+    NaNs included (std docs), so a NaN anywhere in a group leaves the scale
+    to the other values.  (glibc fmaxf would return NaN for a signalling NaN
+    and reset the fold, giving 2/127 here.)"""
+    x = np.array([5.0, 1.0, 2.0] + [0.5] * 29, np.float32)
+    for pos in (0, 1, 31):
+        xb = x.view(np.uint32).copy()
+        xb[pos] = nan_bits
+        xs = xb.view(np.float32)
+        q, s = oracle.q8_quantize(xs)
+        want = max(float(v) for i, v in enumerate(x) if i != pos)
+        assert s[0] == np.float32(want) / np.float32(127.0) and q[pos] == 0
+        q, s = oracle.fp8_quantize_group(xs)
+        assert s == np.float32(want) / np.float32(448.0) and q[pos] == 0x7F
+
+
 def test_q8_matches_float64_brute_force_on_small_groups():
     """Each code is the integer nearest to x/scale (ties away), clamped; this
     is evaluated in float64 from the f32 scale, and may differ from the f32
