@@ -148,9 +148,8 @@ class KvPool:
             raise ValueError("block_tables rows differ from batch")
         _dev(seq_lens, torch.int32, "seq_lens", (batch,))
         max_blocks = block_tables.shape[1]
-        need = self.decode_workspace_size(n_q, batch, max_blocks, max_splits)
         if workspace is None:
-            workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
+            workspace = self.new_workspace(n_q, batch, max_blocks, max_splits)
         _dev(workspace, workspace.dtype, "workspace")
         ws_bytes = workspace.numel() * workspace.element_size()
         if scale is None:

@@ -22,6 +22,7 @@
 #include "../host/status.hpp"
 #include "../pool.hpp"
 #include "codecs.hpp"
+#include "decode_common.hpp"
 
 namespace airkv {
 namespace {
@@ -30,23 +31,6 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kTile = 64;          // tokens per online-softmax step
 constexpr int kTargetPart = 256;   // preferred tokens per partition
-
-struct DecodeArgs {
-    const void *q;
-    int32_t q_dtype, n_q_heads;
-    const int32_t *tables, *lens;
-    int32_t batch, max_blocks, part_tokens, num_parts;
-    float scale_log2;              // softmax scale * log2(e)
-    int32_t n_kv_heads, block_size, scale_group;
-    int64_t num_blocks;
-    const void *k_pages, *v_pages;
-    const float *k_scales, *v_scales;
-    float *part_o;                 // [batch][n_q][num_parts][D]
-    float *part_ml;                // [batch][n_q][num_parts][2] (max in log2 units, sum)
-    void *out;
-    int32_t out_dtype;
-    unsigned long long *errors;
-};
 
 // Raw storage of 8 cache elements in registers.
 template <int DT> struct Raw8;
@@ -355,10 +339,12 @@ int plan_decode(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int32_t 
     if (n_q_heads <= 0 || n_q_heads % nkv)
         return fail(AIR_KV_E_INVALID_ARG, "n_q_heads %d is not a multiple of n_kv_heads %d", n_q_heads, nkv);
     const int g = n_q_heads / nkv;
-    if (g != 1 && g != 2 && g != 4 && g != 8)
-        return fail(AIR_KV_E_INVALID_ARG, "GQA group %d unsupported (1, 2, 4 or 8)", g);
-    if (d != 64 && d != 128 && d != 256)
-        return fail(AIR_KV_E_INVALID_ARG, "decode supports head_dim 64, 128 or 256 (pool has %d)", d);
+    if (!decode_mfma_supported(p.desc.dtype, d, bs, g)) {
+        if (g != 1 && g != 2 && g != 4 && g != 8)
+            return fail(AIR_KV_E_INVALID_ARG, "GQA group %d unsupported for this pool (1, 2, 4 or 8)", g);
+        if (d != 64 && d != 128 && d != 256)
+            return fail(AIR_KV_E_INVALID_ARG, "decode supports head_dim 64, 128 or 256 (pool has %d)", d);
+    }
     if (batch < 0 || batch > 65535) return fail(AIR_KV_E_INVALID_ARG, "batch %d out of range", batch);
     if (max_blocks <= 0) return fail(AIR_KV_E_INVALID_ARG, "max_blocks must be positive");
     if (max_splits < 1 || max_splits > 256)
@@ -388,15 +374,17 @@ hipError_t launch_decode(const air_kv_pool &p, hipStream_t s, const DecodePlan &
     a.part_tokens = plan.part_tokens; a.num_parts = plan.num_parts;
     a.scale_log2 = scale * 1.4426950408889634f;
     a.n_kv_heads = p.desc.n_kv_heads; a.block_size = p.desc.block_size;
-    a.scale_group = p.desc.scale_group; a.num_blocks = p.desc.num_blocks;
+    a.scale_group = p.desc.scale_group; a.group = plan.group; a.num_blocks = p.desc.num_blocks;
     a.k_pages = p.k_pages; a.v_pages = p.v_pages;
     a.k_scales = p.k_scales; a.v_scales = p.v_scales;
     const size_t n_slots = (size_t)batch * n_q_heads * plan.num_parts;
     a.part_o = (float *)workspace;
-    a.part_ml = (float *)workspace + n_slots * p.desc.head_dim;
+    a.part_ml = a.part_o + n_slots * p.desc.head_dim;
     a.out = out; a.out_dtype = out_dtype;
     a.errors = p.errors;
     const int d = p.desc.head_dim, g = plan.group, nkv = p.desc.n_kv_heads;
+    if (decode_mfma_supported(p.desc.dtype, d, p.desc.block_size, g))
+        return launch_decode_mfma(a, s, p.desc.dtype, d);
     switch (p.desc.dtype) {
     case AIR_KV_F32: return launch_g<AIR_KV_F32>(a, s, nkv, d, g);
     case AIR_KV_BF16: return launch_g<AIR_KV_BF16>(a, s, nkv, d, g);

@@ -219,6 +219,19 @@ def main():
         extra["step_append_us"] = round(ms_sa * 1e3, 2)
         log(f"gather {extra['gather_gbps']} GB/s, append {extra['append_gbps']} GB/s")
 
+    # ---- measured ceilings: plain device copy and read-only stream ---------
+    # (the copy is also the known-size kernel that calibrates the FETCH_SIZE /
+    # WRITE_SIZE counters of the profiling runs: 1 GiB read + 1 GiB written)
+    nbytes = 1 << 30
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).uniform_()
+    dst = torch.empty_like(src)
+    ms_c = timed_loop(torch, lambda: dst.copy_(src), 20)
+    extra["copy_gbps"] = round(2 * nbytes / (ms_c * 1e-3) / 1e9, 1)
+    ms_r = timed_loop(torch, lambda: src.sum(dtype=torch.float32), 20)
+    extra["read_gbps"] = round(nbytes / (ms_r * 1e-3) / 1e9, 1)
+    del src, dst
+    log(f"copy ceiling {extra['copy_gbps']} GB/s, read ceiling {extra['read_gbps']} GB/s")
+
     cpu = None
     if not args.no_cpu:
         q_last = step_q[-1].float().cpu().numpy()

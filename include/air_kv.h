@@ -218,6 +218,7 @@ int air_kv_gather(air_kv_pool *pool, void *stream, const int32_t *block_tables,
 int air_paged_decode_workspace_size(const air_kv_pool *pool, int32_t n_q_heads, int32_t batch,
                                     int32_t max_blocks, int32_t max_splits, size_t *bytes);
 
+
 /* Split-K paged decode attention for one new token per sequence:
  *   out[b][h] = softmax(q[b][h] . K_b[h / group]^T * scale) . V_b[h / group]
  * over all seq_lens[b] cached tokens, group = n_q_heads / n_kv_heads (the GQA
@@ -228,7 +229,8 @@ int air_paged_decode_workspace_size(const air_kv_pool *pool, int32_t n_q_heads, 
  * (AIR_KV_F32 or AIR_KV_BF16); out likewise as out_dtype.  The reference's
  * scale is 1/sqrt(head_dim).  max_splits bounds the partitions per sequence
  * (1..256).  A sequence of length 0 produces zeros.  The workspace is device
- * memory of at least air_paged_decode_workspace_size bytes. */
+ * memory of at least air_paged_decode_workspace_size bytes (no initialisation
+ * needed); calls that share a workspace must be ordered (same stream). */
 int air_paged_decode(air_kv_pool *pool, void *stream, const void *q, int32_t q_dtype,
                      int32_t n_q_heads, const int32_t *block_tables, const int32_t *seq_lens,
                      int32_t batch, int32_t max_blocks, float scale, int32_t max_splits,

@@ -82,11 +82,56 @@ def test_c4_shape_fp8_many_splits():
     cfg = workloads.Config("c4s", 64, 8, 128, 32, airkv.FP8, 2)
     got, want, (pool, _, tables, _, _) = _decode_case(cfg, [20000, 9000], seed=44)
     ws = pool.decode_workspace_size(64, 2, tables.shape[1], 64)
-    parts = ws // (2 * 64 * 130 * 4)              # partitions per sequence
-    assert ws % (2 * 64 * 130 * 4) == 0 and 60 <= parts <= 64
+    per_part = 2 * 64 * 130 * 4                   # partial (o, max, sum) of every (seq, q head)
+    parts = ws // per_part                        # partitions per sequence
+    assert ws % per_part == 0 and 60 <= parts <= 64
     err = rel_err(got, want)
     log(f"c4 scaled rel err {err:.2e}")
     assert err <= 2e-2
+
+
+def test_c5_shape_bf16_block32():
+    """configs[4] geometry (bf16, block_size 32) with lognormal contexts."""
+    cfg = workloads.Config("c5s", 32, 8, 128, 32, airkv.BF16, 6)
+    lens = workloads.c5_lengths(6, median=300, lo=16, hi=2000, seed=8)
+    got, want, _ = _decode_case(cfg, lens, seed=45)
+    err = rel_err(got, want)
+    log(f"c5 scaled rel err {err:.2e}")
+    assert err <= 1e-3
+
+
+@pytest.mark.parametrize("q_bf16,out_bf16", [(False, False), (False, True), (True, True)])
+def test_bf16_group16_query_and_output_dtypes(q_bf16, out_bf16):
+    """GQA group 16 (32 q / 2 kv heads); f32 queries take the split hi/lo
+    bf16 path, bf16 outputs are rounded once at the end."""
+    cfg = workloads.Config("g16", 32, 2, 128, 16, airkv.BF16, 3)
+    got, want, _ = _decode_case(cfg, [40, 513, 2100], seed=46, q_bf16=q_bf16, out_bf16=out_bf16)
+    err = rel_err(got, want)
+    log(f"g16 q_bf16={q_bf16} out_bf16={out_bf16} rel err {err:.2e}")
+    assert err <= (4e-3 if out_bf16 else 1e-3)
+
+
+def test_workspace_reuse_across_calls():
+    """Calls that share one workspace give the same answers as fresh
+    workspaces, for varying batches."""
+    torch = torch_mod()
+    cfg = workloads.Config("reuse", 32, 8, 128, 16, airkv.BF16, 6)
+    w = workloads.build_prefill_decode(cfg, [700, 1500, 33, 2600, 260, 900], seed=47)
+    k, v = next(workloads.kv_rows(w.n_rows, 8, 128, seed=48, chunk_rows=1 << 24))
+    pool = device_pool_for(w)
+    run_appends(w, k, v, pool)
+    tables, lens = w.tables()
+    tt, lt = torch.from_numpy(tables).cuda(), torch.from_numpy(lens).cuda()
+    ws = pool.new_workspace(32, 6, tables.shape[1], 64)
+    for it in range(6):
+        nb = [6, 3, 6, 1, 5, 6][it]
+        q = torch.randn(nb, 32, 128, device="cuda").to(torch.bfloat16)
+        out = torch.empty(nb, 32, 128, device="cuda")
+        pool.paged_decode(q, tt[:nb].contiguous(), lt[:nb].contiguous(), out, workspace=ws)
+        ref = torch.empty_like(out)
+        pool.paged_decode(q, tt[:nb].contiguous(), lt[:nb].contiguous(), ref)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), it
 
 
 @pytest.mark.parametrize("kv_len,seed_q,bound,chunk", [(128, 1, 1e-4, 32), (4096, 10, 1e-3, 64),
