@@ -16,6 +16,10 @@
 namespace airkv {
 namespace {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 constexpr int kThreads = 256;
 
 struct AppendArgs {
@@ -35,18 +39,18 @@ __device__ __forceinline__ void store_row_chunk(const float (&x)[8], void *pages
                                                 int lanes_per_group, bool valid) {
     if constexpr (DT == AIR_KV_F32) {
         if (valid) {
-            float4 *o = reinterpret_cast<float4 *>((float *)pages + elem);
-            o[0] = make_float4(x[0], x[1], x[2], x[3]);
-            o[1] = make_float4(x[4], x[5], x[6], x[7]);
+            f32x4 *o = reinterpret_cast<f32x4 *>((float *)pages + elem);
+            __builtin_nontemporal_store(f32x4{x[0], x[1], x[2], x[3]}, o);
+            __builtin_nontemporal_store(f32x4{x[4], x[5], x[6], x[7]}, o + 1);
         }
     } else if constexpr (DT == AIR_KV_BF16) {
         if (valid) {
-            uint4 w;
-            w.x = (uint32_t)bf16_rne(x[0]) | ((uint32_t)bf16_rne(x[1]) << 16);
-            w.y = (uint32_t)bf16_rne(x[2]) | ((uint32_t)bf16_rne(x[3]) << 16);
-            w.z = (uint32_t)bf16_rne(x[4]) | ((uint32_t)bf16_rne(x[5]) << 16);
-            w.w = (uint32_t)bf16_rne(x[6]) | ((uint32_t)bf16_rne(x[7]) << 16);
-            *reinterpret_cast<uint4 *>((uint16_t *)pages + elem) = w;
+            u32x4 w;
+            w[0] = (uint32_t)bf16_rne(x[0]) | ((uint32_t)bf16_rne(x[1]) << 16);
+            w[1] = (uint32_t)bf16_rne(x[2]) | ((uint32_t)bf16_rne(x[3]) << 16);
+            w[2] = (uint32_t)bf16_rne(x[4]) | ((uint32_t)bf16_rne(x[5]) << 16);
+            w[3] = (uint32_t)bf16_rne(x[6]) | ((uint32_t)bf16_rne(x[7]) << 16);
+            __builtin_nontemporal_store(w, reinterpret_cast<u32x4 *>((uint16_t *)pages + elem));
         }
     } else {
         // absmax fold from 0.0 with a NaN-ignoring max (src/kv_cache.rs:60,
@@ -77,7 +81,7 @@ __device__ __forceinline__ void store_row_chunk(const float (&x)[8], void *pages
             for (int j = 0; j < 4; ++j) hi |= (uint32_t)fp8_code(x[4 + j], scale) << (8 * j);
         }
         if (valid) {
-            *reinterpret_cast<uint2 *>((uint8_t *)pages + elem) = make_uint2(lo, hi);
+            __builtin_nontemporal_store(u32x2{lo, hi}, reinterpret_cast<u32x2 *>((uint8_t *)pages + elem));
             if (lead) scales[scale_idx] = scale;
         }
     }
@@ -98,13 +102,15 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(AppendArgs a) {
 
     float kx[8], vx[8];
     if (valid) {
-        const float4 *ks = reinterpret_cast<const float4 *>(a.k + row * a.head_dim + c * 8);
-        const float4 *vs = reinterpret_cast<const float4 *>(a.v + row * a.head_dim + c * 8);
-        float4 k0 = ks[0], k1 = ks[1], v0 = vs[0], v1 = vs[1];
-        kx[0] = k0.x; kx[1] = k0.y; kx[2] = k0.z; kx[3] = k0.w;
-        kx[4] = k1.x; kx[5] = k1.y; kx[6] = k1.z; kx[7] = k1.w;
-        vx[0] = v0.x; vx[1] = v0.y; vx[2] = v0.z; vx[3] = v0.w;
-        vx[4] = v1.x; vx[5] = v1.y; vx[6] = v1.z; vx[7] = v1.w;
+        const f32x4 *ks = reinterpret_cast<const f32x4 *>(a.k + row * a.head_dim + c * 8);
+        const f32x4 *vs = reinterpret_cast<const f32x4 *>(a.v + row * a.head_dim + c * 8);
+        const f32x4 k0 = __builtin_nontemporal_load(ks), k1 = __builtin_nontemporal_load(ks + 1);
+        const f32x4 v0 = __builtin_nontemporal_load(vs), v1 = __builtin_nontemporal_load(vs + 1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            kx[j] = k0[j]; kx[4 + j] = k1[j];
+            vx[j] = v0[j]; vx[4 + j] = v1[j];
+        }
     } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) kx[j] = vx[j] = 0.0f;

@@ -15,6 +15,10 @@
 namespace airkv {
 namespace {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 constexpr int kThreads = 256;
 constexpr int kMaxSeqsPerLaunch = 4096;   // LDS prefix: 16 KB
 
@@ -33,24 +37,24 @@ struct GatherArgs {
 
 template <int DT>
 __device__ __forceinline__ void load8(const void *pages, const float *scales, int64_t elem,
-                                      int64_t scale_idx, float (&x)[8], uint4 *raw) {
+                                      int64_t scale_idx, float (&x)[8], u32x4 *raw) {
     if constexpr (DT == AIR_KV_F32) {
-        const float4 *p = reinterpret_cast<const float4 *>((const float *)pages + elem);
-        float4 a = p[0], b = p[1];
-        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+        const f32x4 *p = reinterpret_cast<const f32x4 *>((const float *)pages + elem);
+        const f32x4 a = __builtin_nontemporal_load(p), b = __builtin_nontemporal_load(p + 1);
+        x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3]; x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
     } else if constexpr (DT == AIR_KV_BF16) {
-        uint4 w = *reinterpret_cast<const uint4 *>((const uint16_t *)pages + elem);
+        const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>((const uint16_t *)pages + elem));
         *raw = w;
-        uint32_t u[4] = {w.x, w.y, w.z, w.w};
+        uint32_t u[4] = {w[0], w[1], w[2], w[3]};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             x[2 * j] = __uint_as_float(u[j] << 16);
             x[2 * j + 1] = __uint_as_float(u[j] & 0xFFFF0000u);
         }
     } else {
-        uint2 w = *reinterpret_cast<const uint2 *>((const uint8_t *)pages + elem);
+        const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>((const uint8_t *)pages + elem));
         const float s = scales[scale_idx];
-        uint32_t u[2] = {w.x, w.y};
+        uint32_t u[2] = {w[0], w[1]};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             uint32_t byte = (u[j >> 2] >> (8 * (j & 3))) & 0xFFu;
@@ -66,20 +70,21 @@ __device__ __forceinline__ void load8(const void *pages, const float *scales, in
 }
 
 template <int DT, int OUT>
-__device__ __forceinline__ void store8(void *out, int64_t elem, const float (&x)[8], uint4 raw) {
+__device__ __forceinline__ void store8(void *out, int64_t elem, const float (&x)[8], u32x4 raw) {
     if constexpr (OUT == AIR_KV_F32) {
-        float4 *o = reinterpret_cast<float4 *>((float *)out + elem);
-        o[0] = make_float4(x[0], x[1], x[2], x[3]);
-        o[1] = make_float4(x[4], x[5], x[6], x[7]);
+        f32x4 *o = reinterpret_cast<f32x4 *>((float *)out + elem);
+        __builtin_nontemporal_store(f32x4{x[0], x[1], x[2], x[3]}, o);
+        __builtin_nontemporal_store(f32x4{x[4], x[5], x[6], x[7]}, o + 1);
     } else if constexpr (DT == AIR_KV_BF16) {
-        *reinterpret_cast<uint4 *>((uint16_t *)out + elem) = raw;   // raw bits, no re-rounding
+        // raw bits, no re-rounding
+        __builtin_nontemporal_store(raw, reinterpret_cast<u32x4 *>((uint16_t *)out + elem));
     } else {
-        uint4 w;
-        w.x = (uint32_t)bf16_rne(x[0]) | ((uint32_t)bf16_rne(x[1]) << 16);
-        w.y = (uint32_t)bf16_rne(x[2]) | ((uint32_t)bf16_rne(x[3]) << 16);
-        w.z = (uint32_t)bf16_rne(x[4]) | ((uint32_t)bf16_rne(x[5]) << 16);
-        w.w = (uint32_t)bf16_rne(x[6]) | ((uint32_t)bf16_rne(x[7]) << 16);
-        *reinterpret_cast<uint4 *>((uint16_t *)out + elem) = w;
+        u32x4 w;
+        w[0] = (uint32_t)bf16_rne(x[0]) | ((uint32_t)bf16_rne(x[1]) << 16);
+        w[1] = (uint32_t)bf16_rne(x[2]) | ((uint32_t)bf16_rne(x[3]) << 16);
+        w[2] = (uint32_t)bf16_rne(x[4]) | ((uint32_t)bf16_rne(x[5]) << 16);
+        w[3] = (uint32_t)bf16_rne(x[6]) | ((uint32_t)bf16_rne(x[7]) << 16);
+        __builtin_nontemporal_store(w, reinterpret_cast<u32x4 *>((uint16_t *)out + elem));
     }
 }
 
@@ -159,7 +164,7 @@ __global__ __launch_bounds__(kThreads) void kv_gather_kernel(GatherArgs a) {
                                                 ? ((int64_t)h * len + t) * d + col
                                                 : (t * a.n_kv_heads + h) * d + col);
             float xk[8], xv[8];
-            uint4 rk = make_uint4(0, 0, 0, 0), rv = rk;
+            u32x4 rk = {0, 0, 0, 0}, rv = rk;
             load8<DT>(a.k_pages, a.k_scales, src, sidx, xk, &rk);
             load8<DT>(a.v_pages, a.v_scales, src, sidx, xv, &rv);
             store8<DT, OUT>(a.out_k, dst, xk, rk);

@@ -30,7 +30,10 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kTile = 64;          // tokens per online-softmax step
-constexpr int kTargetPart = 256;   // preferred tokens per partition
+#ifndef AIRKV_DECODE_PART
+#define AIRKV_DECODE_PART 256      // build-time tuning knob: preferred tokens per partition
+#endif
+constexpr int kTargetPart = AIRKV_DECODE_PART;
 
 // Raw storage of 8 cache elements in registers.
 template <int DT> struct Raw8;

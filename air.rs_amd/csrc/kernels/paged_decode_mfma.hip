@@ -48,6 +48,20 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxParts = 256;             // bound of max_splits
 
+// Build-time tuning knobs (defaults are the shipped configuration).
+#ifndef AIRKV_DECODE_WAVES_PER_EU
+#define AIRKV_DECODE_WAVES_PER_EU 2        // register budget: waves per SIMD
+#endif
+#ifndef AIRKV_DECODE_NT_LOADS
+#define AIRKV_DECODE_NT_LOADS 0            // non-temporal K/V loads
+#endif
+
+// Buffer descriptor word 3 for raw (untyped) buffer access on gfx9-class
+// GPUs, and the cache-policy bits of the K/V loads (1 = glc... 2 = slc, i.e.
+// streaming / non-temporal).
+constexpr int kBufferWord3 = 0x00020000;
+constexpr int kLoadAux = AIRKV_DECODE_NT_LOADS ? 2 : 0;
+
 __device__ __forceinline__ f32x4 mfma_qk(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
@@ -76,7 +90,8 @@ __device__ __forceinline__ void store_out(const DecodeArgs &a, int64_t idx, floa
 }
 
 template <int D, int BS, int GMAX, bool QF32>
-__global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AIRKV_DECODE_WAVES_PER_EU)))
+void decode_mfma_kernel(DecodeArgs a) {
     constexpr int KSTEPS = D / 32;            // QK k-steps
     constexpr int DTILES = D / 16;            // PV output tiles along head_dim
     constexpr int VCH = D / 8;                // 16-byte chunks per V row
@@ -109,6 +124,18 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeArgs a) {
     const int n_active = (int)((len + a.part_tokens - 1) / a.part_tokens);
     const int n_tiles = (int)((end - start + 15) / 16);
     const int my_tiles = wave < n_tiles ? (n_tiles - wave + kWaves - 1) / kWaves : 0;
+
+    // Block ids of this wave's tiles, 64 at a time: lane k of `tbl` holds the id
+    // of tile wave + 4 * (c0 + k).  The first chunk is requested before the Q
+    // loads so both latencies overlap.
+    const int32_t *table = a.tables + (int64_t)b * a.max_blocks;
+    int32_t tbl = 0;
+    int c0 = 0;
+    auto load_table = [&](int first) {
+        const int kk = first + lane;
+        tbl = kk < my_tiles ? table[(start + 16 * (int64_t)(wave + kWaves * kk)) / BS] : 0;
+    };
+    load_table(0);
 
     // ---- Q^T in the B-operand layout: lane holds q[h = r16][8*g4 + 32*ks .. +8]
     u32x4 qhi[KSTEPS], qlo[KSTEPS];
@@ -145,36 +172,44 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeArgs a) {
     for (int n = 0; n < DTILES; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -INFINITY, l_run = 0.0f;
 
-    const int32_t *table = a.tables + (int64_t)b * a.max_blocks;
     const uint16_t *kp = (const uint16_t *)a.k_pages;
     const uint16_t *vp = (const uint16_t *)a.v_pages;
     uint16_t *sv = reinterpret_cast<uint16_t *>(smem) + wave * VTILE;
     const int vrow = lane / VCH, vch = lane % VCH;
-    const int k_off = r16 * D + 8 * g4;                 // lane's K element offset in a tile
-    const int v_off = vrow * D + vch * 8;               // lane's V element offset in a tile
+    const int k_boff = (r16 * D + 8 * g4) * 2;          // lane's K byte offset in a tile
+    const int v_boff = (vrow * D + vch * 8) * 2;        // lane's V byte offset in a tile
 
-    // Block ids of this wave's tiles, 64 at a time: lane k of `tbl` holds the id
-    // of tile wave + 4 * (c0 + k), or -1 for an entry outside the pool (counted).
-    // Tiles are loaded unconditionally (a bad id reads block 0) and skipped at
-    // compute time, so no branch ever merges freshly loaded registers.
-    int32_t tbl = -1;
-    int c0 = 0;
+    // Tiles are loaded unconditionally (an id outside the pool reads block 0)
+    // and skipped at compute time, so no branch ever merges freshly loaded
+    // registers.
     auto load_tile = [&](int k, u32x4 (&kr)[KSTEPS], u32x4 (&vr)[VLOADS]) -> bool {
         int32_t blk = __builtin_amdgcn_readlane(tbl, k - c0);
-        const bool ok = blk >= 0;
+        const bool ok = blk >= 0 && blk < a.num_blocks;
         blk = ok ? blk : 0;
         const int64_t t0 = start + 16 * (int64_t)(wave + kWaves * k);
         const int64_t base = (((int64_t)blk * a.n_kv_heads + kh) * BS + (t0 % BS)) * D;
-        const uint16_t *kt = kp + base, *vt = vp + base;
+        // Buffer loads: the tile's base lives in a scalar resource descriptor
+        // and each lane's offset is a loop-invariant register, so no vector
+        // address register is rewritten while earlier loads are in flight.
+        // The descriptor also bounds the access to the 16-row tile.
+        const __amdgpu_buffer_rsrc_t rk =
+            __builtin_amdgcn_make_buffer_rsrc((void *)(kp + base), (short)0, 16 * D * 2, kBufferWord3);
+        const __amdgpu_buffer_rsrc_t rv =
+            __builtin_amdgcn_make_buffer_rsrc((void *)(vp + base), (short)0, 16 * D * 2, kBufferWord3);
 #pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) kr[ks] = *reinterpret_cast<const u32x4 *>(kt + k_off + 32 * ks);
+        for (int ks = 0; ks < KSTEPS; ++ks)
+            kr[ks] = __builtin_amdgcn_raw_buffer_load_b128(rk, k_boff + 64 * ks, 0, kLoadAux);
 #pragma unroll
-        for (int v = 0; v < VLOADS; ++v) vr[v] = *reinterpret_cast<const u32x4 *>(vt + v_off + v * VRPL * D);
+        for (int v = 0; v < VLOADS; ++v)
+            vr[v] = __builtin_amdgcn_raw_buffer_load_b128(rv, v_boff + v * VRPL * D * 2, 0, kLoadAux);
         return ok;
     };
 
     auto compute_tile = [&](int k, const u32x4 (&kr)[KSTEPS], const u32x4 (&vr)[VLOADS], bool ok) {
-        if (!ok) return;                                // table entry outside the pool: skipped
+        // A table entry outside the pool is counted and its tile masked out;
+        // the tile still runs every instruction, so the loaded registers are
+        // consumed on all paths and the loads in flight never need draining.
+        if (!ok && lane == 0) atomicAdd(a.errors, 1ull);
         const int64_t t0 = start + 16 * (int64_t)(wave + kWaves * k);
         f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -185,7 +220,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeArgs a) {
         // lane holds S[token 4*g4 + i][head r16]
         float sc[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sc[i] = (t0 + 4 * g4 + i < end) ? s[i] * a.scale_log2 : -INFINITY;
+        for (int i = 0; i < 4; ++i) sc[i] = (ok && t0 + 4 * g4 + i < end) ? s[i] * a.scale_log2 : -INFINITY;
         float mt = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
         mt = fmaxf(mt, __shfl_xor(mt, 16));
         mt = fmaxf(mt, __shfl_xor(mt, 32));
@@ -195,8 +230,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeArgs a) {
         // rescale of the accumulators.  The final normalisation uses the same
         // max, so the result is unchanged.
         if (__ballot(mt > m_run + 8.0f) != 0ull) {
-            const float m_new = fmaxf(m_run, mt);      // finite: token t0 is always valid
-            const float alpha = exp2f(m_run - m_new);  // exp2(-inf) = 0 on the first tile
+            const float m_new = fmaxf(m_run, mt);
+            const float alpha = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - m_new);
             l_run *= alpha;
 #pragma unroll
             for (int n = 0; n < DTILES; ++n) acc[n] *= alpha;
@@ -204,7 +239,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeArgs a) {
         }
         float p[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p[i] = exp2f(sc[i] - m_run);
+        for (int i = 0; i < 4; ++i) p[i] = (sc[i] == -INFINITY) ? 0.0f : exp2f(sc[i] - m_run);
         l_run += (p[0] + p[1]) + (p[2] + p[3]);
         // P^T as the B operand (lane: tokens 4*g4 .. +3 of head r16), hi + lo halves
         uint32_t h[4], l[4];
@@ -218,7 +253,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeArgs a) {
         for (int v = 0; v < VLOADS; ++v) {
             const int row = v * VRPL + vrow;
             u32x4 w = vr[v];
-            if (t0 + row >= end) w = u32x4{0, 0, 0, 0};
+            if (!ok || t0 + row >= end) w = u32x4{0, 0, 0, 0};
             u32x2 *dst = reinterpret_cast<u32x2 *>(sv + row * PITCH + vch * 8);
             dst[0] = u32x2{w[0], w[1]};
             dst[1] = u32x2{w[2], w[3]};
@@ -237,26 +272,23 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(DecodeArgs a) {
 
     for (; c0 < my_tiles; c0 += 64) {
         const int c1 = my_tiles - c0 < 64 ? my_tiles : c0 + 64;
-        {
-            const int kk = c0 + lane;
-            int32_t id = kk < c1 ? table[(start + 16 * (int64_t)(wave + kWaves * kk)) / BS] : 0;
-            if (kk < c1 && (id < 0 || id >= a.num_blocks)) {
-                atomicAdd(a.errors, 1ull);
-                id = -1;
-            }
-            tbl = id;
-        }
-        // Two register sets used alternately.  The next load is issued
-        // unconditionally (past the end it re-reads the last tile, an L2 hit)
-        // so no branch joins paths with different loads in flight.
-        u32x4 ka[KSTEPS], va[VLOADS], kb[KSTEPS], vb[VLOADS];
-        bool oka = load_tile(c0, ka, va), okb;
-        for (int k = c0; k < c1; k += 2) {
-            okb = load_tile(k + 1 < c1 ? k + 1 : c1 - 1, kb, vb);
+        if (c0 > 0) load_table(c0);
+        // Three register sets used in rotation: two tiles are in flight while
+        // the third is computed.  Loads are issued unconditionally (past the
+        // end they re-read the last tile, an L2 hit) so no branch joins paths
+        // with different loads in flight.
+        auto clampk = [&](int k) { return k < c1 ? k : c1 - 1; };
+        u32x4 ka[KSTEPS], va[VLOADS], kb[KSTEPS], vb[VLOADS], kc[KSTEPS], vc[VLOADS];
+        bool oka = load_tile(c0, ka, va), okb = load_tile(clampk(c0 + 1), kb, vb), okc;
+        for (int k = c0; k < c1; k += 3) {
+            okc = load_tile(clampk(k + 2), kc, vc);
             compute_tile(k, ka, va, oka);
             if (k + 1 >= c1) break;
-            oka = load_tile(k + 2 < c1 ? k + 2 : c1 - 1, ka, va);
+            oka = load_tile(clampk(k + 3), ka, va);
             compute_tile(k + 1, kb, vb, okb);
+            if (k + 2 >= c1) break;
+            okb = load_tile(clampk(k + 4), kb, vb);
+            compute_tile(k + 2, kc, vc, okc);
         }
     }
 
