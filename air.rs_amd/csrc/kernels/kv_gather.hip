@@ -187,12 +187,7 @@ hipError_t launch_gather(const air_kv_pool &p, hipStream_t s, const int32_t *tab
                          const int32_t *lens, const int64_t *out_offsets, int32_t batch,
                          int32_t max_blocks, void *out_k, void *out_v, int32_t out_dtype,
                          int32_t out_layout) {
-    int cus = 256;
-    {
-        int dev = 0;
-        if (hipGetDevice(&dev) == hipSuccess)
-            (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    }
+    const int cus = p.cus;
     for (int32_t b0 = 0; b0 < batch; b0 += kMaxSeqsPerLaunch) {
         const int32_t nb = batch - b0 < kMaxSeqsPerLaunch ? batch - b0 : kMaxSeqsPerLaunch;
         GatherArgs a;

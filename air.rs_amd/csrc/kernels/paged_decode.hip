@@ -352,6 +352,11 @@ int plan_decode(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int32_t 
     if (max_blocks <= 0) return fail(AIR_KV_E_INVALID_ARG, "max_blocks must be positive");
     if (max_splits < 1 || max_splits > 256)
         return fail(AIR_KV_E_INVALID_ARG, "max_splits %d outside 1..256", max_splits);
+    plan->group = g;
+    if (decode_mfma_supported(p.desc.dtype, d, bs, g))
+        return plan_decode_mfma(p, n_q_heads, batch, max_blocks, max_splits, plan);
+    plan->mfma = false;
+    plan->slices = plan->batch_per_launch = plan->slots = 0;
     const int64_t max_ctx = (int64_t)max_blocks * bs;
     int64_t parts = (max_ctx + kTargetPart - 1) / kTargetPart;
     parts = parts < 1 ? 1 : (parts > max_splits ? max_splits : parts);
@@ -359,7 +364,6 @@ int plan_decode(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int32_t 
     part_tokens = (part_tokens + bs - 1) / bs * bs;
     if (part_tokens > INT32_MAX) return fail(AIR_KV_E_INVALID_ARG, "max_blocks too large");
     parts = (max_ctx + part_tokens - 1) / part_tokens;
-    plan->group = g;
     plan->part_tokens = (int32_t)part_tokens;
     plan->num_parts = (int32_t)parts;
     plan->ws_bytes = (size_t)batch * n_q_heads * (size_t)parts * (size_t)(d + 2) * sizeof(float);
@@ -375,19 +379,20 @@ hipError_t launch_decode(const air_kv_pool &p, hipStream_t s, const DecodePlan &
     a.tables = tables; a.lens = lens;
     a.batch = batch; a.max_blocks = max_blocks;
     a.part_tokens = plan.part_tokens; a.num_parts = plan.num_parts;
+    a.slices = plan.slices; a.slots = plan.slots;
     a.scale_log2 = scale * 1.4426950408889634f;
     a.n_kv_heads = p.desc.n_kv_heads; a.block_size = p.desc.block_size;
     a.scale_group = p.desc.scale_group; a.group = plan.group; a.num_blocks = p.desc.num_blocks;
     a.k_pages = p.k_pages; a.v_pages = p.v_pages;
     a.k_scales = p.k_scales; a.v_scales = p.v_scales;
+    a.out = out; a.out_dtype = out_dtype;
+    a.errors = p.errors;
+    a.prefix = nullptr;
+    if (plan.mfma) return launch_decode_mfma(a, plan, workspace, s);
     const size_t n_slots = (size_t)batch * n_q_heads * plan.num_parts;
     a.part_o = (float *)workspace;
     a.part_ml = a.part_o + n_slots * p.desc.head_dim;
-    a.out = out; a.out_dtype = out_dtype;
-    a.errors = p.errors;
     const int d = p.desc.head_dim, g = plan.group, nkv = p.desc.n_kv_heads;
-    if (decode_mfma_supported(p.desc.dtype, d, p.desc.block_size, g))
-        return launch_decode_mfma(a, s, p.desc.dtype, d);
     switch (p.desc.dtype) {
     case AIR_KV_F32: return launch_g<AIR_KV_F32>(a, s, nkv, d, g);
     case AIR_KV_BF16: return launch_g<AIR_KV_BF16>(a, s, nkv, d, g);

@@ -1,9 +1,21 @@
 // Paged decode attention on the matrix cores (bf16 pages, head_dim 128).
 //
-// One workgroup owns one (split-K partition, kv head, sequence) and all G <= 16
-// query heads of that kv head (GQA group), so each K/V byte is read from HBM
-// once.  Its four waves take 16-token tiles of the partition round robin:
+// Work distribution.  The cached tokens of the batch are cut into 16-token
+// tiles, numbered sequence after sequence (tile t of the batch belongs to the
+// sequence b with prefix[b] <= t < prefix[b + 1], prefix[b] = tiles of the
+// sequences before b).  For each kv head these tiles are split into `slices`
+// equal contiguous ranges of `chunk` tiles, one per wave, so every wave
+// streams the same number of K/V bytes whatever the length mix of the batch
+// (a grid of per-sequence partitions leaves the GPU waiting on the longest
+// sequences).  A slice may end inside a sequence and continue into the next:
+// at every sequence boundary the wave emits the (max, sum, O) of the piece it
+// holds.  The pieces of sequence b come from slices w0(b) = prefix[b] / chunk
+// .. w1(b) = (prefix[b + 1] - 1) / chunk and are stored at slots b + w, which
+// never collide across sequences because w0(b + 1) >= w1(b).  A sequence that
+// lies in one slice is normalised and written by that wave; the others are
+// combined by decode_merge_kernel by log-sum-exp (src/flash_decode.rs:114-142).
 //
+// Per 16-token tile, on the matrix cores:
 //   S  = K . Q^T   v_mfma_f32_16x16x32_bf16, M = 16 tokens, N = 16 heads (G
 //                  used), K = head_dim in steps of 32.  K is loaded straight
 //                  from its page in the A-operand layout (row = lane % 16,
@@ -19,18 +31,15 @@
 //                  its V tile in LDS (row pitch 264 B: the four token groups
 //                  land on different banks) and reads it back transposed.
 //
-// Each wave reads the block ids of all its tiles with one vector load (lane k
-// holds the id of the wave's k-th tile) and takes them with readlane, so tile
-// addresses come from scalar registers and no load ever waits on another.  K
-// and V of the next tile are in flight while the current tile is computed
-// (two register sets, used alternately).  The four waves merge their
-// (max, sum, O) through LDS; a sequence with a single partition writes its
-// output directly, otherwise the partition stores an unnormalised partial that
-// decode_merge_kernel combines by log-sum-exp (src/flash_decode.rs:114-142).
+// Each wave resolves the sequence, block id and valid token count of 64 of its
+// tiles at once (lane k: tile k), then takes them with readlane, so tile
+// addresses live in scalar registers and no load waits on another.  Three
+// register sets rotate: two tiles are in flight while the third is computed.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
 
+#include "../host/status.hpp"
 #include "../pool.hpp"
 #include "codecs.hpp"
 #include "decode_common.hpp"
@@ -46,7 +55,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kMaxParts = 256;             // bound of max_splits
+constexpr int kMaxBatch = 4096;            // sequences per launch (the host splits larger batches)
+constexpr int kMinChunk = 4;               // tiles per slice at least
 
 // Build-time tuning knobs (defaults are the shipped configuration).
 #ifndef AIRKV_DECODE_WAVES_PER_EU
@@ -57,8 +67,7 @@ constexpr int kMaxParts = 256;             // bound of max_splits
 #endif
 
 // Buffer descriptor word 3 for raw (untyped) buffer access on gfx9-class
-// GPUs, and the cache-policy bits of the K/V loads (1 = glc... 2 = slc, i.e.
-// streaming / non-temporal).
+// GPUs, and the cache-policy bits of the K/V loads (2 = slc: streaming).
 constexpr int kBufferWord3 = 0x00020000;
 constexpr int kLoadAux = AIRKV_DECODE_NT_LOADS ? 2 : 0;
 
@@ -89,7 +98,75 @@ __device__ __forceinline__ void store_out(const DecodeArgs &a, int64_t idx, floa
     else ((uint16_t *)a.out)[idx] = bf16_rne(v);
 }
 
-template <int D, int BS, int GMAX, bool QF32>
+// Four consecutive outputs (idx a multiple of 4).
+__device__ __forceinline__ void store_out4(const DecodeArgs &a, int64_t idx, f32x4 v) {
+    if (a.out_dtype == AIR_KV_F32) {
+        *reinterpret_cast<f32x4 *>((float *)a.out + idx) = v;
+    } else {
+        const u32x2 w = {(uint32_t)bf16_rne(v[0]) | ((uint32_t)bf16_rne(v[1]) << 16),
+                         (uint32_t)bf16_rne(v[2]) | ((uint32_t)bf16_rne(v[3]) << 16)};
+        *reinterpret_cast<u32x2 *>((uint16_t *)a.out + idx) = w;
+    }
+}
+
+__device__ __forceinline__ int64_t clamp_len(int64_t len, int64_t max_len) {
+    return len < 0 ? 0 : (len > max_len ? max_len : len);
+}
+
+// Tiles per slice: an equal share of `total`, at least kMinChunk.
+__device__ __forceinline__ int slice_chunk(int total, int slices) {
+    const int c = (total + slices - 1) / slices;
+    return c < kMinChunk ? kMinChunk : c;
+}
+
+// pre[b] = tiles (ceil(len / 16), len clamped to [0, max_blocks * BS]) of the
+// sequences before b, for b = 0..batch, in LDS.  All threads take part.
+template <int BS>
+__device__ void tile_prefix(const DecodeArgs &a, int32_t *pre, int32_t *wsum) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int B = a.batch;
+    const int64_t max_len = (int64_t)a.max_blocks * BS;
+    for (int b = tid; b < B; b += kThreads)
+        pre[b + 1] = (int32_t)((clamp_len(a.lens[b], max_len) + 15) / 16);
+    if (tid == 0) pre[0] = 0;
+    __syncthreads();
+    // each thread scans a run of `per` entries; runs are chained by a
+    // wave-level then a workgroup-level exclusive scan of the run sums
+    const int per = (B + kThreads - 1) / kThreads;
+    const int lo = 1 + tid * per;
+    const int hi = lo + per < B + 1 ? lo + per : B + 1;
+    int sum = 0;
+    for (int i = lo; i < hi; ++i) sum += pre[i];
+    int incl = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int run = incl - sum;
+    for (int w = 0; w < wave; ++w) run += wsum[w];
+    for (int i = lo; i < hi; ++i) {
+        run += pre[i];
+        pre[i] = run;
+    }
+    __syncthreads();
+}
+
+// The sequence holding tile t (0 <= t < pre[B]): the b with pre[b] <= t < pre[b + 1].
+// The loop count depends on B only, so the lanes of a wave stay converged.
+__device__ __forceinline__ int seq_of_tile(const int32_t *pre, int B, int t) {
+    int lo = 0, hi = B;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (pre[mid] <= t) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+template <int D, int BS, bool QF32>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AIRKV_DECODE_WAVES_PER_EU)))
 void decode_mfma_kernel(DecodeArgs a) {
     constexpr int KSTEPS = D / 32;            // QK k-steps
@@ -99,82 +176,89 @@ void decode_mfma_kernel(DecodeArgs a) {
     constexpr int VLOADS = 16 / VRPL;         // V loads per 16-token tile
     constexpr int PITCH = D + 4;              // LDS row pitch in bf16 elements
     constexpr int VTILE = 16 * PITCH;         // bf16 elements per wave's V tile
-    constexpr int MERGE_FLOATS = kWaves * GMAX * D;
-    constexpr int SMEM = (VTILE * 2 * kWaves > MERGE_FLOATS * 4) ? VTILE * 2 * kWaves : MERGE_FLOATS * 4;
     static_assert(BS % 16 == 0, "a 16-token tile must not straddle pages");
-    __shared__ __align__(16) unsigned char smem[SMEM];
-    __shared__ float s_m[kWaves][16], s_l[kWaves][16];
+    __shared__ int32_t s_pre[kMaxBatch + 1];
+    __shared__ int32_t s_wsum[kWaves];
+    __shared__ __align__(16) uint16_t s_v[kWaves * VTILE];
 
-    const int part = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+    tile_prefix<BS>(a, s_pre, s_wsum);
+    const int B = a.batch;
+    const int total = s_pre[B];
+    const int chunk = slice_chunk(total, a.slices);
+    if (blockIdx.x == 0)                       // for the merge kernel
+        for (int i = threadIdx.x; i <= B; i += kThreads) a.prefix[i] = s_pre[i];
+
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: scalar loop control
     const int g4 = lane >> 4, r16 = lane & 15;
     const int G = a.group;
+    // Consecutive waves take consecutive kv heads of one slice: their pages
+    // are neighbours within the same blocks.
+    const int gw = blockIdx.x * kWaves + wave;
+    const int kh = gw % a.n_kv_heads, w = gw / a.n_kv_heads;
+    if (w >= a.slices || (int64_t)w * chunk >= total) return;
+    const int lo = w * chunk;
+    const int hi = total - lo < chunk ? total : lo + chunk;
     const int64_t max_len = (int64_t)a.max_blocks * BS;
-    int64_t len = a.lens[b];
-    len = len < 0 ? 0 : (len > max_len ? max_len : len);
-    const int64_t start = (int64_t)part * a.part_tokens;
-    if (start >= len) {
-        if (len == 0 && part == 0)                      // empty sequence: zeros
-            for (int idx = tid; idx < G * D; idx += kThreads)
-                store_out(a, ((int64_t)b * a.n_q_heads + kh * G) * D + idx, 0.0f);
-        return;
-    }
-    const int64_t end = start + a.part_tokens < len ? start + a.part_tokens : len;
-    const int n_active = (int)((len + a.part_tokens - 1) / a.part_tokens);
-    const int n_tiles = (int)((end - start + 15) / 16);
-    const int my_tiles = wave < n_tiles ? (n_tiles - wave + kWaves - 1) / kWaves : 0;
 
-    // Block ids of this wave's tiles, 64 at a time: lane k of `tbl` holds the id
-    // of tile wave + 4 * (c0 + k).  The first chunk is requested before the Q
-    // loads so both latencies overlap.
-    const int32_t *table = a.tables + (int64_t)b * a.max_blocks;
-    int32_t tbl = 0;
-    int c0 = 0;
-    auto load_table = [&](int first) {
-        const int kk = first + lane;
-        tbl = kk < my_tiles ? table[(start + 16 * (int64_t)(wave + kWaves * kk)) / BS] : 0;
+    // Per 64-tile window starting at tile c0, lane k describes tile c0 + k:
+    // its sequence, tile index within the sequence, block id and valid tokens.
+    int32_t tbl = 0, seq_l = 0, j_l = 0, nv_l = 0;
+    uint64_t first_m = 0, last_m = 0;      // tile starts / ends a piece
+    auto load_window = [&](int c0) {
+        const int t = c0 + lane < hi ? c0 + lane : hi - 1;
+        const int bq = seq_of_tile(s_pre, B, t);
+        const int j = t - s_pre[bq];
+        const int64_t len = clamp_len(a.lens[bq], max_len);
+        tbl = a.tables[(int64_t)bq * a.max_blocks + (16 * j) / BS];
+        seq_l = bq;
+        j_l = j;
+        const int64_t rest = len - 16 * (int64_t)j;
+        nv_l = rest < 16 ? (int)rest : 16;
+        const bool valid = c0 + lane < hi;
+        first_m = __ballot(valid && (t == lo || j == 0));
+        last_m = __ballot(valid && (t + 1 == hi || t + 1 == s_pre[bq + 1]));
     };
-    load_table(0);
 
     // ---- Q^T in the B-operand layout: lane holds q[h = r16][8*g4 + 32*ks .. +8]
+    // The loads go through a buffer descriptor that spans exactly the group's
+    // G query rows: lanes of heads >= G fall outside it and read zeros, so
+    // there is no branch (a branch around a load inside the tile loop costs
+    // the compiler ~50 extra registers).
     u32x4 qhi[KSTEPS], qlo[KSTEPS];
-    {
-        const int64_t qrow = ((int64_t)b * a.n_q_heads + kh * G + r16) * D;
+    auto load_q = [&](int bq) {
+        constexpr int QB = QF32 ? 4 : 2;
+        const char *qg = (const char *)a.q + ((int64_t)bq * a.n_q_heads + kh * G) * D * QB;
+        const __amdgpu_buffer_rsrc_t rq =
+            __builtin_amdgcn_make_buffer_rsrc((void *)qg, (short)0, G * D * QB, kBufferWord3);
+        const int qoff = (r16 * D + 8 * g4) * QB;
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
-            const int d0 = 8 * g4 + 32 * ks;
-            u32x4 hi = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
-            if (r16 < G) {
-                if constexpr (QF32) {
-                    const f32x4 *qp = reinterpret_cast<const f32x4 *>((const float *)a.q + qrow + d0);
-                    const f32x4 x0 = qp[0], x1 = qp[1];
-                    const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-                    uint32_t h[8], l[8];
+            if constexpr (QF32) {
+                const u32x4 x0 = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 32 * ks * QB, 0, 0);
+                const u32x4 x1 = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 32 * ks * QB + 16, 0, 0);
+                const uint32_t x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+                uint32_t hh[8], ll[8];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) split_bf16(x[j], h[j], l[j]);
+                for (int j = 0; j < 8; ++j) split_bf16(__uint_as_float(x[j]), hh[j], ll[j]);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        hi[j] = h[2 * j] | (h[2 * j + 1] << 16);
-                        lo[j] = l[2 * j] | (l[2 * j + 1] << 16);
-                    }
-                } else {
-                    hi = *reinterpret_cast<const u32x4 *>((const uint16_t *)a.q + qrow + d0);
+                for (int j = 0; j < 4; ++j) {
+                    qhi[ks][j] = hh[2 * j] | (hh[2 * j + 1] << 16);
+                    qlo[ks][j] = ll[2 * j] | (ll[2 * j + 1] << 16);
                 }
+            } else {
+                qhi[ks] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 32 * ks * QB, 0, 0);
+                qlo[ks] = u32x4{0, 0, 0, 0};
             }
-            qhi[ks] = hi;
-            qlo[ks] = lo;
         }
-    }
+    };
 
     f32x4 acc[DTILES];
-#pragma unroll
-    for (int n = 0; n < DTILES; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -INFINITY, l_run = 0.0f;
 
     const uint16_t *kp = (const uint16_t *)a.k_pages;
     const uint16_t *vp = (const uint16_t *)a.v_pages;
-    uint16_t *sv = reinterpret_cast<uint16_t *>(smem) + wave * VTILE;
+    uint16_t *sv = s_v + wave * VTILE;
     const int vrow = lane / VCH, vch = lane % VCH;
     const int k_boff = (r16 * D + 8 * g4) * 2;          // lane's K byte offset in a tile
     const int v_boff = (vrow * D + vch * 8) * 2;        // lane's V byte offset in a tile
@@ -182,12 +266,12 @@ void decode_mfma_kernel(DecodeArgs a) {
     // Tiles are loaded unconditionally (an id outside the pool reads block 0)
     // and skipped at compute time, so no branch ever merges freshly loaded
     // registers.
-    auto load_tile = [&](int k, u32x4 (&kr)[KSTEPS], u32x4 (&vr)[VLOADS]) -> bool {
-        int32_t blk = __builtin_amdgcn_readlane(tbl, k - c0);
+    auto load_tile = [&](int idx, u32x4 (&kr)[KSTEPS], u32x4 (&vr)[VLOADS]) -> bool {
+        int32_t blk = __builtin_amdgcn_readlane(tbl, idx);
+        const int j = __builtin_amdgcn_readlane(j_l, idx);
         const bool ok = blk >= 0 && blk < a.num_blocks;
         blk = ok ? blk : 0;
-        const int64_t t0 = start + 16 * (int64_t)(wave + kWaves * k);
-        const int64_t base = (((int64_t)blk * a.n_kv_heads + kh) * BS + (t0 % BS)) * D;
+        const int64_t base = (((int64_t)blk * a.n_kv_heads + kh) * BS + (16 * j) % BS) * D;
         // Buffer loads: the tile's base lives in a scalar resource descriptor
         // and each lane's offset is a loop-invariant register, so no vector
         // address register is rewritten while earlier loads are in flight.
@@ -205,12 +289,44 @@ void decode_mfma_kernel(DecodeArgs a) {
         return ok;
     };
 
-    auto compute_tile = [&](int k, const u32x4 (&kr)[KSTEPS], const u32x4 (&vr)[VLOADS], bool ok) {
+    // The piece of sequence bq held by this wave ends: write it out.
+    auto emit = [&](int bq) {
+        float l = l_run + __shfl_xor(l_run, 16);
+        l += __shfl_xor(l, 32);
+        const int w0 = s_pre[bq] / chunk, w1 = (s_pre[bq + 1] - 1) / chunk;
+        if (r16 < G) {
+            if (w0 == w1) {                  // the whole sequence: final output
+                const float inv = 1.0f / l;
+                const int64_t orow = ((int64_t)bq * a.n_q_heads + kh * G + r16) * D + 4 * g4;
+#pragma unroll
+                for (int n = 0; n < DTILES; ++n) store_out4(a, orow + 16 * n, acc[n] * inv);
+            } else {
+                const int64_t row = ((int64_t)kh * a.slots + bq + w) * G + r16;
+                float *po = a.part_o + row * D + 4 * g4;
+#pragma unroll
+                for (int n = 0; n < DTILES; ++n) *reinterpret_cast<f32x4 *>(po + 16 * n) = acc[n];
+                if (g4 == 0) {
+                    a.part_ml[row * 2] = m_run;
+                    a.part_ml[row * 2 + 1] = l;
+                }
+            }
+        }
+    };
+
+    auto compute_tile = [&](int k, int idx, const u32x4 (&kr)[KSTEPS], const u32x4 (&vr)[VLOADS], bool ok) {
+        const int bq = __builtin_amdgcn_readlane(seq_l, idx);
+        if ((first_m >> idx) & 1) {          // a new sequence starts in this slice
+            if (k != lo) load_q(bq);
+            m_run = -INFINITY;
+            l_run = 0.0f;
+#pragma unroll
+            for (int n = 0; n < DTILES; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
         // A table entry outside the pool is counted and its tile masked out;
         // the tile still runs every instruction, so the loaded registers are
         // consumed on all paths and the loads in flight never need draining.
         if (!ok && lane == 0) atomicAdd(a.errors, 1ull);
-        const int64_t t0 = start + 16 * (int64_t)(wave + kWaves * k);
+        const int nv = ok ? __builtin_amdgcn_readlane(nv_l, idx) : 0;   // valid tokens
         f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
@@ -220,7 +336,7 @@ void decode_mfma_kernel(DecodeArgs a) {
         // lane holds S[token 4*g4 + i][head r16]
         float sc[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sc[i] = (ok && t0 + 4 * g4 + i < end) ? s[i] * a.scale_log2 : -INFINITY;
+        for (int i = 0; i < 4; ++i) sc[i] = 4 * g4 + i < nv ? s[i] * a.scale_log2 : -INFINITY;
         float mt = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
         mt = fmaxf(mt, __shfl_xor(mt, 16));
         mt = fmaxf(mt, __shfl_xor(mt, 32));
@@ -252,11 +368,11 @@ void decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
         for (int v = 0; v < VLOADS; ++v) {
             const int row = v * VRPL + vrow;
-            u32x4 w = vr[v];
-            if (!ok || t0 + row >= end) w = u32x4{0, 0, 0, 0};
+            u32x4 x = vr[v];
+            if (row >= nv) x = u32x4{0, 0, 0, 0};
             u32x2 *dst = reinterpret_cast<u32x2 *>(sv + row * PITCH + vch * 8);
-            dst[0] = u32x2{w[0], w[1]};
-            dst[1] = u32x2{w[2], w[3]};
+            dst[0] = u32x2{x[0], x[1]};
+            dst[1] = u32x2{x[2], x[3]};
         }
         // O^T[d][h] += V^T[d][t] P^T[t][h]; A lane holds V[t = 4*g4 + jj][d = 16n + r16]
         const uint16_t *col = sv + (4 * g4) * PITCH + r16;
@@ -268,141 +384,100 @@ void decode_mfma_kernel(DecodeArgs a) {
             acc[n] = mfma_pv(av, p_hi, acc[n]);
             acc[n] = mfma_pv(av, p_lo, acc[n]);
         }
+        if ((last_m >> idx) & 1) emit(bq);
     };
 
-    for (; c0 < my_tiles; c0 += 64) {
-        const int c1 = my_tiles - c0 < 64 ? my_tiles : c0 + 64;
-        if (c0 > 0) load_table(c0);
+    for (int c0 = lo; c0 < hi; c0 += 64) {
+        load_window(c0);
+        if (c0 == lo) load_q(__builtin_amdgcn_readlane(seq_l, 0));
+        const int n = hi - c0 < 64 ? hi - c0 : 64;
         // Three register sets used in rotation: two tiles are in flight while
         // the third is computed.  Loads are issued unconditionally (past the
         // end they re-read the last tile, an L2 hit) so no branch joins paths
         // with different loads in flight.
-        auto clampk = [&](int k) { return k < c1 ? k : c1 - 1; };
+        auto clampi = [&](int i) { return i < n ? i : n - 1; };
         u32x4 ka[KSTEPS], va[VLOADS], kb[KSTEPS], vb[VLOADS], kc[KSTEPS], vc[VLOADS];
-        bool oka = load_tile(c0, ka, va), okb = load_tile(clampk(c0 + 1), kb, vb), okc;
-        for (int k = c0; k < c1; k += 3) {
-            okc = load_tile(clampk(k + 2), kc, vc);
-            compute_tile(k, ka, va, oka);
-            if (k + 1 >= c1) break;
-            oka = load_tile(clampk(k + 3), ka, va);
-            compute_tile(k + 1, kb, vb, okb);
-            if (k + 2 >= c1) break;
-            okb = load_tile(clampk(k + 4), kb, vb);
-            compute_tile(k + 2, kc, vc, okc);
-        }
-    }
-
-    // ---- merge the four waves (head h = r16; lane holds O^T[d = 16n + 4*g4 + i][h])
-    l_run += __shfl_xor(l_run, 16);
-    l_run += __shfl_xor(l_run, 32);
-    if (lane < 16) {
-        s_m[wave][lane] = m_run;
-        s_l[wave][lane] = l_run;
-    }
-    __syncthreads();                                   // V tiles are dead from here on
-    float *so = reinterpret_cast<float *>(smem);       // [wave][GMAX][D]
-    if (r16 < G) {
-#pragma unroll
-        for (int n = 0; n < DTILES; ++n)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) so[(wave * GMAX + r16) * D + 16 * n + 4 * g4 + i] = acc[n][i];
-    }
-    __syncthreads();
-
-    const int64_t slot_base = ((int64_t)b * a.n_q_heads + kh * G) * a.num_parts;
-    for (int idx = tid; idx < G * D; idx += kThreads) {
-        const int h = idx / D, d = idx - h * D;
-        float m = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) m = fmaxf(m, s_m[w][h]);
-        float wsum = 0.0f, o = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float f = exp2f(s_m[w][h] - m);       // a wave without tiles has m = -inf: f = 0
-            wsum += f * s_l[w][h];
-            o += f * so[(w * GMAX + h) * D + d];
-        }
-        if (n_active == 1) {
-            store_out(a, ((int64_t)b * a.n_q_heads + kh * G + h) * D + d, o / wsum);
-        } else {
-            const int64_t slot = slot_base + (int64_t)h * a.num_parts + part;
-            a.part_o[slot * D + d] = o;
-            if (d == 0) {
-                a.part_ml[slot * 2] = m;
-                a.part_ml[slot * 2 + 1] = wsum;
-            }
+        bool oka = load_tile(0, ka, va), okb = load_tile(clampi(1), kb, vb), okc;
+        for (int i = 0; i < n; i += 3) {
+            okc = load_tile(clampi(i + 2), kc, vc);
+            compute_tile(c0 + i, i, ka, va, oka);
+            if (i + 1 >= n) break;
+            oka = load_tile(clampi(i + 3), ka, va);
+            compute_tile(c0 + i + 1, i + 1, kb, vb, okb);
+            if (i + 2 >= n) break;
+            okb = load_tile(clampi(i + 4), kb, vb);
+            compute_tile(c0 + i + 2, i + 2, kc, vc, okc);
         }
     }
 }
 
-// Log-sum-exp merge of the partitions of one (sequence, kv head): the G x D
-// outputs of its query heads.  Weights come from the partitions' (max, sum)
-// staged in LDS; each thread then sums its output over the partitions with
-// independent, unrolled loads.
-template <int D, int GMAX>
+// Log-sum-exp merge of the pieces of one (sequence, kv head): the G x D
+// outputs of its query heads.  Also writes zeros for an empty sequence and
+// counts sequence lengths outside [0, max_blocks * block_size].
+template <int D>
 __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
-    __shared__ float s_w[GMAX][kMaxParts];
-    __shared__ float s_inv[GMAX];
+    __shared__ float s_mx[16], s_inv[16];
     const int b = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x;
     const int G = a.group;
     const int64_t max_len = (int64_t)a.max_blocks * a.block_size;
-    int64_t len = a.lens[b];
-    if (tid == 0 && kh == 0 && (len < 0 || len > max_len)) atomicAdd(a.errors, 1ull);
-    len = len < 0 ? 0 : (len > max_len ? max_len : len);
-    const int n_active = (int)((len + a.part_tokens - 1) / a.part_tokens);
-    if (n_active <= 1) return;                          // written by the split kernel
-    const int64_t slot_base = ((int64_t)b * a.n_q_heads + kh * G) * a.num_parts;
-    // one wave per head: max over partitions, then weights exp2(m_p - m) / sum
+    if (tid == 0 && kh == 0 && (a.lens[b] < 0 || a.lens[b] > max_len)) atomicAdd(a.errors, 1ull);
+    const int p0 = a.prefix[b], p1 = a.prefix[b + 1];
+    const int64_t obase = ((int64_t)b * a.n_q_heads + kh * G) * D;
+    if (p0 == p1) {                                      // empty sequence: zeros
+        for (int idx = tid; idx < G * D; idx += kThreads) store_out(a, obase + idx, 0.0f);
+        return;
+    }
+    const int chunk = slice_chunk(a.prefix[a.batch], a.slices);
+    const int w0 = p0 / chunk, w1 = (p1 - 1) / chunk;
+    if (w0 == w1) return;                                // written by its slice
+    const int n = w1 - w0 + 1;
+    // row of (piece p, head h): row0 + p * G + h
+    const int64_t row0 = ((int64_t)kh * a.slots + b + w0) * G;
     const int lane = tid & 63, wave = tid >> 6;
     for (int h = wave; h < G; h += kWaves) {
-        const float *ml = a.part_ml + (slot_base + (int64_t)h * a.num_parts) * 2;
         float m = -INFINITY;
-        for (int p = lane; p < n_active; p += 64) m = fmaxf(m, ml[2 * p]);
+        for (int p = lane; p < n; p += 64) m = fmaxf(m, a.part_ml[(row0 + (int64_t)p * G + h) * 2]);
 #pragma unroll
         for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s));
         float l = 0.0f;
-        for (int p = lane; p < n_active; p += 64) {
-            const float w = exp2f(ml[2 * p] - m);
-            s_w[h][p] = w;
-            l += w * ml[2 * p + 1];
+        for (int p = lane; p < n; p += 64) {
+            const float *ml = a.part_ml + (row0 + (int64_t)p * G + h) * 2;
+            l += exp2f(ml[0] - m) * ml[1];
         }
 #pragma unroll
         for (int s = 32; s >= 1; s >>= 1) l += __shfl_xor(l, s);
-        if (lane == 0) s_inv[h] = 1.0f / l;
+        if (lane == 0) {
+            s_mx[h] = m;
+            s_inv[h] = 1.0f / l;
+        }
     }
     __syncthreads();
     for (int idx = tid; idx < G * D; idx += kThreads) {
         const int h = idx / D, d = idx - h * D;
-        const float *po = a.part_o + (slot_base + (int64_t)h * a.num_parts) * D + d;
+        const float m = s_mx[h];
         float o = 0.0f;
-#pragma unroll 8
-        for (int p = 0; p < n_active; ++p) o += s_w[h][p] * po[(int64_t)p * D];
-        store_out(a, ((int64_t)b * a.n_q_heads + kh * G + h) * D + d, o * s_inv[h]);
+#pragma unroll 4
+        for (int p = 0; p < n; ++p) {
+            const int64_t row = row0 + (int64_t)p * G + h;
+            o += exp2f(a.part_ml[row * 2] - m) * a.part_o[row * D + d];
+        }
+        store_out(a, obase + idx, o * s_inv[h]);
     }
 }
 
-template <int BS, int GMAX, bool QF32>
+template <int BS, bool QF32>
 hipError_t launch_cfg(const DecodeArgs &a, hipStream_t s) {
-    dim3 grid((unsigned)a.num_parts, (unsigned)a.n_kv_heads, (unsigned)a.batch);
-    hipLaunchKernelGGL((decode_mfma_kernel<128, BS, GMAX, QF32>), grid, dim3(kThreads), 0, s, a);
+    const int64_t waves = (int64_t)a.n_kv_heads * a.slices;
+    const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves));
+    hipLaunchKernelGGL((decode_mfma_kernel<128, BS, QF32>), grid, dim3(kThreads), 0, s, a);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a.num_parts == 1) return e;
-    hipLaunchKernelGGL((decode_merge_kernel<128, GMAX>), dim3((unsigned)a.batch, (unsigned)a.n_kv_heads),
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((decode_merge_kernel<128>), dim3((unsigned)a.batch, (unsigned)a.n_kv_heads),
                        dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 
-template <int BS, int GMAX>
-hipError_t launch_q(const DecodeArgs &a, hipStream_t s) {
-    return a.q_dtype == AIR_KV_F32 ? launch_cfg<BS, GMAX, true>(a, s) : launch_cfg<BS, GMAX, false>(a, s);
-}
-
-template <int BS>
-hipError_t launch_bs(const DecodeArgs &a, hipStream_t s) {
-    if (a.group <= 4) return launch_q<BS, 4>(a, s);
-    if (a.group <= 8) return launch_q<BS, 8>(a, s);
-    return launch_q<BS, 16>(a, s);
-}
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 }  // namespace
 
@@ -411,10 +486,52 @@ bool decode_mfma_supported(int dtype, int head_dim, int block_size, int group) {
            group >= 1 && group <= 16;
 }
 
-hipError_t launch_decode_mfma(const DecodeArgs &a, hipStream_t s, int dtype, int head_dim) {
-    (void)dtype;
-    (void)head_dim;
-    return a.block_size == 16 ? launch_bs<16>(a, s) : launch_bs<32>(a, s);
+// Slices per kv head: enough waves for AIRKV_DECODE_WAVES_PER_EU waves on
+// every SIMD (4 per compute unit), at most batch * max_splits.  The workspace
+// holds the tile prefix and (slices + batch) partial rows per query head.
+int plan_decode_mfma(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int32_t max_blocks,
+                     int32_t max_splits, DecodePlan *plan) {
+    const int nkv = p.desc.n_kv_heads, d = p.desc.head_dim, bs = p.desc.block_size;
+    const int32_t nb = batch < kMaxBatch ? batch : kMaxBatch;
+    const int64_t tiles_per_seq = ((int64_t)max_blocks * bs + 15) / 16;
+    if ((int64_t)nb * tiles_per_seq > INT32_MAX)
+        return fail(AIR_KV_E_INVALID_ARG, "batch x max_blocks too large for one decode launch");
+    const int64_t machine_waves = (int64_t)p.cus * 4 * AIRKV_DECODE_WAVES_PER_EU;
+    int64_t slices = (machine_waves + nkv - 1) / nkv;
+    const int64_t cap = (int64_t)(nb > 0 ? nb : 1) * max_splits;
+    slices = slices > cap ? cap : slices;
+    plan->mfma = true;
+    plan->part_tokens = plan->num_parts = 0;
+    plan->slices = (int32_t)slices;
+    plan->batch_per_launch = nb;
+    plan->slots = (int32_t)(slices + nb);
+    plan->ws_bytes = align256((size_t)(nb + 1) * 4) + align256((size_t)n_q_heads * plan->slots * 2 * 4) +
+                     (size_t)n_q_heads * plan->slots * d * 4;
+    return AIR_KV_OK;
+}
+
+hipError_t launch_decode_mfma(const DecodeArgs &base, const DecodePlan &plan, void *workspace,
+                              hipStream_t s) {
+    for (int32_t b0 = 0; b0 < base.batch; b0 += plan.batch_per_launch) {
+        DecodeArgs a = base;
+        a.batch = base.batch - b0 < plan.batch_per_launch ? base.batch - b0 : plan.batch_per_launch;
+        const int64_t q_row = (int64_t)b0 * a.n_q_heads * 128;
+        a.q = (const char *)base.q + q_row * (base.q_dtype == AIR_KV_F32 ? 4 : 2);
+        a.out = (char *)base.out + q_row * (base.out_dtype == AIR_KV_F32 ? 4 : 2);
+        a.tables = base.tables + (int64_t)b0 * a.max_blocks;
+        a.lens = base.lens + b0;
+        char *ws = (char *)workspace;
+        a.prefix = (int32_t *)ws;
+        ws += align256((size_t)(plan.batch_per_launch + 1) * 4);
+        a.part_ml = (float *)ws;
+        ws += align256((size_t)a.n_q_heads * plan.slots * 2 * 4);
+        a.part_o = (float *)ws;
+        hipError_t e = a.block_size == 16
+                           ? (a.q_dtype == AIR_KV_F32 ? launch_cfg<16, true>(a, s) : launch_cfg<16, false>(a, s))
+                           : (a.q_dtype == AIR_KV_F32 ? launch_cfg<32, true>(a, s) : launch_cfg<32, false>(a, s));
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace airkv

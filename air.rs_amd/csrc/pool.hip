@@ -52,6 +52,9 @@ int air_kv_pool_create(const air_kv_pool_desc *desc, air_kv_pool **out) {
 
     hipError_t e = hipGetDevice(&p->device);
     if (e != hipSuccess) { delete p; return hip_fail(e, "hipGetDevice"); }
+    if (hipDeviceGetAttribute(&p->cus, hipDeviceAttributeMultiprocessorCount, p->device) != hipSuccess ||
+        p->cus <= 0)
+        p->cus = 256;
     const size_t pages = p->page_slab_bytes * (size_t)d.num_blocks;
     const size_t scales = p->scale_slab_bytes * (size_t)d.num_blocks;
     auto cleanup = [&](hipError_t err, const char *what) {

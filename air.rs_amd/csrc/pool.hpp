@@ -10,6 +10,7 @@
 struct air_kv_pool {
     air_kv_pool_desc desc;
     int device = 0;
+    int cus = 256;               // compute units of that device (launch sizing)
     void *k_pages = nullptr;     // [num_blocks][n_kv_heads][block_size][head_dim]
     void *v_pages = nullptr;
     float *k_scales = nullptr;   // [num_blocks][n_kv_heads][block_size][head_dim/scale_group]
@@ -29,9 +30,15 @@ inline bool dtype_quantized(int dt) { return dt == AIR_KV_INT8 || dt == AIR_KV_F
 // Partitioning of one decode launch (shared by the workspace query).
 struct DecodePlan {
     int32_t group;        // q heads per kv head
+    bool mfma;            // matrix-core kernel with balanced slices (else fixed partitions)
+    // fixed partitions (vector kernel)
     int32_t part_tokens;  // tokens per split-K partition (multiple of block_size)
     int32_t num_parts;    // partitions per sequence
-    size_t ws_bytes;      // partial outputs + (max, sum) per (seq, q head, part)
+    // balanced slices (matrix-core kernel)
+    int32_t slices;       // slices per kv head (one wave each)
+    int32_t batch_per_launch;
+    int32_t slots;        // partial rows per (kv head, q head of the group): slices + batch
+    size_t ws_bytes;
 };
 int plan_decode(const air_kv_pool &pool, int32_t n_q_heads, int32_t batch, int32_t max_blocks,
                 int32_t max_splits, DecodePlan *plan);

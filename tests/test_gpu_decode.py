@@ -17,7 +17,10 @@ pytestmark = pytest.mark.gpu
 TOL = {airkv.F32: 1e-3, airkv.BF16: 1e-3, airkv.INT8: 2e-2, airkv.FP8: 2e-2}
 
 
-def _decode_case(cfg, lens, seed, q_bf16=True, max_splits=64, outliers=None, out_bf16=False):
+def _decode_case(cfg, lens, seed, q_bf16=True, max_splits=64, outliers=None, out_bf16=False,
+                 empty=()):
+    """Decode of cfg with prefill `lens` (+1 decode token each) on the GPU and
+    on the oracle; sequences listed in `empty` are decoded with length 0."""
     torch = torch_mod()
     w = workloads.build_prefill_decode(cfg, lens, seed, decode_steps=1)
     k, v = next(workloads.kv_rows(w.n_rows, cfg.n_kv_heads, cfg.head_dim, seed=seed + 100,
@@ -25,6 +28,7 @@ def _decode_case(cfg, lens, seed, q_bf16=True, max_splits=64, outliers=None, out
     pool, host = device_pool_for(w), host_pool_for(w)
     run_appends(w, k, v, pool, host)
     tables, seq_lens = w.tables()
+    seq_lens[list(empty)] = 0
     rng = np.random.default_rng(seed + 7)
     q = rng.standard_normal((cfg.batch, cfg.n_q_heads, cfg.head_dim)).astype(np.float32)
     qt = torch.from_numpy(q).cuda()
@@ -74,6 +78,46 @@ def test_c3_shape_int8_outliers_scaled():
     err = rel_err(got, want)
     log(f"c3 scaled rel err {err:.2e}")
     assert err <= 2e-2
+
+
+def test_slices_span_and_share_sequences():
+    """Matrix-core path (bf16, d 128): 300 short sequences (1..80 tokens, some
+    decoded empty) and two long ones.  The balanced slices then end inside
+    sequences, hold several sequences each, and the long sequences spread over
+    many slices; every case must agree with the oracle."""
+    cfg = workloads.Config("mix", 32, 8, 128, 16, airkv.BF16, 300)
+    rng = np.random.default_rng(60)
+    lens = rng.integers(0, 80, size=300)
+    lens[7], lens[150] = 6000, 2500
+    empty = [0, 1, 33, 34, 35, 299]
+    got, want, _ = _decode_case(cfg, lens.tolist(), seed=61, empty=empty)
+    assert np.count_nonzero(got[empty]) == 0
+    err = rel_err(got, want)
+    log(f"mixed slices rel err {err:.2e}")
+    assert err <= 1e-3
+
+
+@pytest.mark.parametrize("max_splits", [1, 3])
+def test_slices_capped_by_max_splits(max_splits):
+    """max_splits caps the slices per kv head at batch x max_splits (here far
+    fewer than the GPU's waves): long slices, the same answers."""
+    cfg = workloads.Config("cap", 32, 8, 128, 32, airkv.BF16, 4)
+    got, want, _ = _decode_case(cfg, [3000, 17, 900, 4100], seed=62, max_splits=max_splits)
+    err = rel_err(got, want)
+    log(f"max_splits={max_splits} rel err {err:.2e}")
+    assert err <= 1e-3
+
+
+def test_batch_above_one_launch():
+    """More sequences than one launch takes (4096): the host runs the batch
+    in consecutive launches over the same workspace."""
+    cfg = workloads.Config("wide", 8, 2, 128, 16, airkv.BF16, 4200)
+    rng = np.random.default_rng(63)
+    lens = rng.integers(1, 40, size=4200)
+    got, want, _ = _decode_case(cfg, lens.tolist(), seed=64, empty=[4095, 4096])
+    err = rel_err(got, want)
+    log(f"batch 4200 rel err {err:.2e}")
+    assert err <= 1e-3
 
 
 def test_c4_shape_fp8_many_splits():
