@@ -67,6 +67,20 @@ def test_fp8_decode_all_256_codes_match_closed_form():
     assert table[0x80] == 0.0 and math.copysign(1, table[0x80]) == 1.0
 
 
+def test_fp8_decode_fixture_is_what_its_script_writes():
+    """The committed fixture is the value-domain table of
+    tests/golden/make_fp8_decode.py (Python floats, not the oracle's code)."""
+    import os
+    import sys
+    here = os.path.join(os.path.dirname(__file__), "golden")
+    sys.path.insert(0, here)
+    try:
+        import make_fp8_decode
+    finally:
+        sys.path.remove(here)
+    assert make_fp8_decode.table_bytes() == open(os.path.join(here, "fp8_e4m3_decode.bin"), "rb").read()
+
+
 def test_fp8_decode_table_matches_committed_fixture():
     import os
     path = os.path.join(os.path.dirname(__file__), "golden", "fp8_e4m3_decode.bin")
