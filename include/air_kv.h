@@ -214,7 +214,8 @@ int air_kv_gather(air_kv_pool *pool, void *stream, const int32_t *block_tables,
                   int32_t max_blocks, void *out_k, void *out_v, int32_t out_dtype,
                   int32_t out_layout);
 
-/* Workspace bytes air_paged_decode needs for this launch shape. */
+/* Workspace bytes air_paged_decode needs for this launch shape (it depends on
+ * the pool's device: the slice count follows its compute-unit count). */
 int air_paged_decode_workspace_size(const air_kv_pool *pool, int32_t n_q_heads, int32_t batch,
                                     int32_t max_blocks, int32_t max_splits, size_t *bytes);
 
@@ -227,8 +228,14 @@ int air_paged_decode_workspace_size(const air_kv_pool *pool, int32_t n_q_heads, 
  * (src/flash_decode.rs:153-173: split-K partials merged by log-sum-exp,
  * :114-142) to paged storage.  q: [batch][n_q_heads][head_dim] as q_dtype
  * (AIR_KV_F32 or AIR_KV_BF16); out likewise as out_dtype.  The reference's
- * scale is 1/sqrt(head_dim).  max_splits bounds the partitions per sequence
- * (1..256).  A sequence of length 0 produces zeros.  The workspace is device
+ * scale is 1/sqrt(head_dim).  max_splits (1..256) bounds the split-K work
+ * division: bf16 pools with head_dim 128 (the matrix-core kernel) cut the
+ * batch's cached tokens into at most batch * max_splits equal slices per kv
+ * head, where a slice may end inside a sequence and hold several; other pools
+ * cut each sequence into at most max_splits partitions.  Out-of-pool table
+ * entries are skipped and counted (air_kv_pool_error_count); seq_lens outside
+ * [0, max_blocks * block_size] are clamped and counted.  A sequence of length
+ * 0 produces zeros.  The workspace is device
  * memory of at least air_paged_decode_workspace_size bytes (no initialisation
  * needed); calls that share a workspace must be ordered (same stream). */
 int air_paged_decode(air_kv_pool *pool, void *stream, const void *q, int32_t q_dtype,
