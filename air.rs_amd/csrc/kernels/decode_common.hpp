@@ -33,7 +33,7 @@ struct DecodeArgs {
     unsigned long long *errors;
 };
 
-bool decode_mfma_supported(int dtype, int head_dim, int block_size, int group);
+bool decode_mfma_supported(int dtype, int head_dim, int block_size, int group, int scale_group);
 int plan_decode_mfma(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int32_t max_blocks,
                      int32_t max_splits, DecodePlan *plan);
 hipError_t launch_decode_mfma(const DecodeArgs &a, const DecodePlan &plan, void *workspace,

@@ -342,7 +342,7 @@ int plan_decode(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int32_t 
     if (n_q_heads <= 0 || n_q_heads % nkv)
         return fail(AIR_KV_E_INVALID_ARG, "n_q_heads %d is not a multiple of n_kv_heads %d", n_q_heads, nkv);
     const int g = n_q_heads / nkv;
-    if (!decode_mfma_supported(p.desc.dtype, d, bs, g)) {
+    if (!decode_mfma_supported(p.desc.dtype, d, bs, g, p.desc.scale_group)) {
         if (g != 1 && g != 2 && g != 4 && g != 8)
             return fail(AIR_KV_E_INVALID_ARG, "GQA group %d unsupported for this pool (1, 2, 4 or 8)", g);
         if (d != 64 && d != 128 && d != 256)
@@ -353,9 +353,10 @@ int plan_decode(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int32_t 
     if (max_splits < 1 || max_splits > 256)
         return fail(AIR_KV_E_INVALID_ARG, "max_splits %d outside 1..256", max_splits);
     plan->group = g;
-    if (decode_mfma_supported(p.desc.dtype, d, bs, g))
+    if (decode_mfma_supported(p.desc.dtype, d, bs, g, p.desc.scale_group))
         return plan_decode_mfma(p, n_q_heads, batch, max_blocks, max_splits, plan);
     plan->mfma = false;
+    plan->dtype = p.desc.dtype;
     plan->slices = plan->batch_per_launch = plan->slots = 0;
     const int64_t max_ctx = (int64_t)max_blocks * bs;
     int64_t parts = (max_ctx + kTargetPart - 1) / kTargetPart;

@@ -168,14 +168,55 @@ __device__ __forceinline__ int seq_of_tile(const int32_t *pre, int B, int t) {
     return lo;
 }
 
-template <int D, int BS, bool QF32>
+// Raw registers of one 16-token tile as loaded, before any conversion.
+// bf16 pages: K in the MFMA A-operand layout (lane: row r16, head_dim 8*g4 +
+// 32*ks .. +8 for step ks) and four 16-byte V chunks.  1-byte pages (int8
+// Q8_0 codes, fp8): lane holds 32 contiguous codes -- exactly one scale group
+// of 32 -- of one K row and one V row, plus the two f32 scales.
+template <int DT> struct Tile {
+    u32x4 k[2], v[2];
+    uint32_t ks, vs;
+};
+template <> struct Tile<AIR_KV_BF16> {
+    u32x4 k[4], v[4];
+};
+
+// Four 1-byte codes of one word times `s`, as two bf16 pairs.  The f32 value
+// is the reference's dequantized cache element, q as f32 * scale
+// (src/kv_cache.rs:78-92) or to_f32(code) * scale (src/fp8.rs:263-264),
+// computed with one rounding; it is then rounded to bf16 for the matrix
+// cores.  int8: the code is biased to an unsigned byte (x ^ 0x80 = q + 128)
+// so one byte-to-float conversion applies, and fma(q + 128, s, -128 s) is
+// code * s with a single rounding.  fp8: the hardware converts the OCP E4M3
+// encoding, which agrees with the reference decoder on every code its
+// encoder emits (zero exponent fields only as +-0, 0xFF never; 0x7F is NaN
+// in both).
+template <int DT>
+__device__ __forceinline__ u32x2 dequant4(uint32_t w, float s) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    f32x2 lo, hi;
+    if constexpr (DT == AIR_KV_INT8) {
+        const uint32_t u = w ^ 0x80808080u;
+        const float off = -128.0f * s;
+        lo = f32x2{__builtin_fmaf((float)(u & 0xFFu), s, off), __builtin_fmaf((float)((u >> 8) & 0xFFu), s, off)};
+        hi = f32x2{__builtin_fmaf((float)((u >> 16) & 0xFFu), s, off), __builtin_fmaf((float)(u >> 24), s, off)};
+    } else {
+        lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false) * s;
+        hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true) * s;
+    }
+    return u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2)),
+                 __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2))};
+}
+
+template <int D, int BS, bool QF32, int DT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AIRKV_DECODE_WAVES_PER_EU)))
 void decode_mfma_kernel(DecodeArgs a) {
+    static_assert(D == 128, "lane mappings assume head_dim 128");
+    constexpr bool QUANT = DT != AIR_KV_BF16;
+    constexpr int EB = QUANT ? 1 : 2;         // bytes per cache element
     constexpr int KSTEPS = D / 32;            // QK k-steps
     constexpr int DTILES = D / 16;            // PV output tiles along head_dim
-    constexpr int VCH = D / 8;                // 16-byte chunks per V row
-    constexpr int VRPL = 64 / VCH;            // V rows per wave load
-    constexpr int VLOADS = 16 / VRPL;         // V loads per 16-token tile
     constexpr int PITCH = D + 4;              // LDS row pitch in bf16 elements
     constexpr int VTILE = 16 * PITCH;         // bf16 elements per wave's V tile
     static_assert(BS % 16 == 0, "a 16-token tile must not straddle pages");
@@ -222,7 +263,11 @@ void decode_mfma_kernel(DecodeArgs a) {
         last_m = __ballot(valid && (t + 1 == hi || t + 1 == s_pre[bq + 1]));
     };
 
-    // ---- Q^T in the B-operand layout: lane holds q[h = r16][8*g4 + 32*ks .. +8]
+    // ---- Q^T in the B-operand layout.  The QK contraction runs over head_dim
+    // in an order of our choosing as long as K and Q agree: bf16 pages use
+    // d = 32*ks + 8*g4 + j (16 contiguous K bytes per lane and step), 1-byte
+    // pages d = 32*g4 + 8*ks + j (a lane's four steps cover one 32-element
+    // scale group, loaded as 32 contiguous codes).
     // The loads go through a buffer descriptor that spans exactly the group's
     // G query rows: lanes of heads >= G fall outside it and read zeros, so
     // there is no branch (a branch around a load inside the tile loop costs
@@ -233,12 +278,13 @@ void decode_mfma_kernel(DecodeArgs a) {
         const char *qg = (const char *)a.q + ((int64_t)bq * a.n_q_heads + kh * G) * D * QB;
         const __amdgpu_buffer_rsrc_t rq =
             __builtin_amdgcn_make_buffer_rsrc((void *)qg, (short)0, G * D * QB, kBufferWord3);
-        const int qoff = (r16 * D + 8 * g4) * QB;
+        const int qoff = (r16 * D + (QUANT ? 32 : 8) * g4) * QB;
+        constexpr int step = (QUANT ? 8 : 32) * QB;
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
             if constexpr (QF32) {
-                const u32x4 x0 = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 32 * ks * QB, 0, 0);
-                const u32x4 x1 = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 32 * ks * QB + 16, 0, 0);
+                const u32x4 x0 = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + step * ks, 0, 0);
+                const u32x4 x1 = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + step * ks + 16, 0, 0);
                 const uint32_t x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
                 uint32_t hh[8], ll[8];
 #pragma unroll
@@ -249,7 +295,7 @@ void decode_mfma_kernel(DecodeArgs a) {
                     qlo[ks][j] = ll[2 * j] | (ll[2 * j + 1] << 16);
                 }
             } else {
-                qhi[ks] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 32 * ks * QB, 0, 0);
+                qhi[ks] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + step * ks, 0, 0);
                 qlo[ks] = u32x4{0, 0, 0, 0};
             }
         }
@@ -258,36 +304,58 @@ void decode_mfma_kernel(DecodeArgs a) {
     f32x4 acc[DTILES];
     float m_run = -INFINITY, l_run = 0.0f;
 
-    const uint16_t *kp = (const uint16_t *)a.k_pages;
-    const uint16_t *vp = (const uint16_t *)a.v_pages;
+    const char *kp = (const char *)a.k_pages;
+    const char *vp = (const char *)a.v_pages;
     uint16_t *sv = s_v + wave * VTILE;
-    const int vrow = lane / VCH, vch = lane % VCH;
-    const int k_boff = (r16 * D + 8 * g4) * 2;          // lane's K byte offset in a tile
-    const int v_boff = (vrow * D + vch * 8) * 2;        // lane's V byte offset in a tile
+    // Lane offsets inside a tile (loop invariant).  bf16: K as the A operand,
+    // V as 16-byte chunks of rows lane / 16 + 4 * v.  1-byte: K row r16 and V
+    // row lane / 4, 32 codes from column 32 * g4 (K) or 32 * (lane % 4) (V).
+    const int vrow = QUANT ? lane >> 2 : lane >> 4;
+    const int vcol = QUANT ? 32 * (lane & 3) : 8 * (lane & 15);
+    const int k_boff = QUANT ? r16 * D + 32 * g4 : (r16 * D + 8 * g4) * 2;
+    const int v_boff = (vrow * D + vcol) * EB;
+    const int n_sc = QUANT ? D / a.scale_group : 0;              // scales per row
+    const int k_soff = QUANT ? (r16 * n_sc + (32 * g4) / a.scale_group) * 4 : 0;
+    const int v_soff = QUANT ? (vrow * n_sc + vcol / a.scale_group) * 4 : 0;
 
     // Tiles are loaded unconditionally (an id outside the pool reads block 0)
     // and skipped at compute time, so no branch ever merges freshly loaded
     // registers.
-    auto load_tile = [&](int idx, u32x4 (&kr)[KSTEPS], u32x4 (&vr)[VLOADS]) -> bool {
+    auto load_tile = [&](int idx, Tile<DT> &t) -> bool {
         int32_t blk = __builtin_amdgcn_readlane(tbl, idx);
         const int j = __builtin_amdgcn_readlane(j_l, idx);
         const bool ok = blk >= 0 && blk < a.num_blocks;
         blk = ok ? blk : 0;
-        const int64_t base = (((int64_t)blk * a.n_kv_heads + kh) * BS + (16 * j) % BS) * D;
+        const int64_t row0 = ((int64_t)blk * a.n_kv_heads + kh) * BS + (16 * j) % BS;
         // Buffer loads: the tile's base lives in a scalar resource descriptor
         // and each lane's offset is a loop-invariant register, so no vector
         // address register is rewritten while earlier loads are in flight.
         // The descriptor also bounds the access to the 16-row tile.
         const __amdgpu_buffer_rsrc_t rk =
-            __builtin_amdgcn_make_buffer_rsrc((void *)(kp + base), (short)0, 16 * D * 2, kBufferWord3);
+            __builtin_amdgcn_make_buffer_rsrc((void *)(kp + row0 * D * EB), (short)0, 16 * D * EB, kBufferWord3);
         const __amdgpu_buffer_rsrc_t rv =
-            __builtin_amdgcn_make_buffer_rsrc((void *)(vp + base), (short)0, 16 * D * 2, kBufferWord3);
+            __builtin_amdgcn_make_buffer_rsrc((void *)(vp + row0 * D * EB), (short)0, 16 * D * EB, kBufferWord3);
+        if constexpr (QUANT) {
 #pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks)
-            kr[ks] = __builtin_amdgcn_raw_buffer_load_b128(rk, k_boff + 64 * ks, 0, kLoadAux);
+            for (int i = 0; i < 2; ++i) {
+                t.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, k_boff + 16 * i, 0, kLoadAux);
+                t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, v_boff + 16 * i, 0, kLoadAux);
+            }
+            const int64_t srow = row0 * n_sc;
+            const __amdgpu_buffer_rsrc_t rks = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)(a.k_scales + srow), (short)0, 16 * n_sc * 4, kBufferWord3);
+            const __amdgpu_buffer_rsrc_t rvs = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)(a.v_scales + srow), (short)0, 16 * n_sc * 4, kBufferWord3);
+            t.ks = __builtin_amdgcn_raw_buffer_load_b32(rks, k_soff, 0, kLoadAux);
+            t.vs = __builtin_amdgcn_raw_buffer_load_b32(rvs, v_soff, 0, kLoadAux);
+        } else {
 #pragma unroll
-        for (int v = 0; v < VLOADS; ++v)
-            vr[v] = __builtin_amdgcn_raw_buffer_load_b128(rv, v_boff + v * VRPL * D * 2, 0, kLoadAux);
+            for (int ks = 0; ks < KSTEPS; ++ks)
+                t.k[ks] = __builtin_amdgcn_raw_buffer_load_b128(rk, k_boff + 64 * ks, 0, kLoadAux);
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                t.v[v] = __builtin_amdgcn_raw_buffer_load_b128(rv, v_boff + v * 4 * D * 2, 0, kLoadAux);
+        }
         return ok;
     };
 
@@ -315,7 +383,7 @@ void decode_mfma_kernel(DecodeArgs a) {
         }
     };
 
-    auto compute_tile = [&](int k, int idx, const u32x4 (&kr)[KSTEPS], const u32x4 (&vr)[VLOADS], bool ok) {
+    auto compute_tile = [&](int k, int idx, const Tile<DT> &t, bool ok) {
         const int bq = __builtin_amdgcn_readlane(seq_l, idx);
         if ((first_m >> idx) & 1) {          // a new sequence starts in this slice
             if (k != lo) load_q(bq);
@@ -329,11 +397,24 @@ void decode_mfma_kernel(DecodeArgs a) {
         // consumed on all paths and the loads in flight never need draining.
         if (!ok && lane == 0) atomicAdd(a.errors, 1ull);
         const int nv = ok ? __builtin_amdgcn_readlane(nv_l, idx) : 0;   // valid tokens
+        u32x4 kop[KSTEPS];                   // K as bf16 A operands
+        if constexpr (QUANT) {
+            const float ksc = __uint_as_float(t.ks);
+#pragma unroll
+            for (int ks = 0; ks < KSTEPS; ++ks) {
+                const u32x2 x = dequant4<DT>(t.k[ks >> 1][(ks & 1) * 2], ksc);
+                const u32x2 y = dequant4<DT>(t.k[ks >> 1][(ks & 1) * 2 + 1], ksc);
+                kop[ks] = u32x4{x[0], x[1], y[0], y[1]};
+            }
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < KSTEPS; ++ks) kop[ks] = t.k[ks];
+        }
         f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
-            s = mfma_qk(kr[ks], qhi[ks], s);
-            if constexpr (QF32) s = mfma_qk(kr[ks], qlo[ks], s);
+            s = mfma_qk(kop[ks], qhi[ks], s);
+            if constexpr (QF32) s = mfma_qk(kop[ks], qlo[ks], s);
         }
         // lane holds S[token 4*g4 + i][head r16]
         float sc[4];
@@ -365,16 +446,27 @@ void decode_mfma_kernel(DecodeArgs a) {
         for (int i = 0; i < 4; ++i) split_bf16(p[i], h[i], l[i]);
         const u32x2 p_hi = {h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
         const u32x2 p_lo = {l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
-        // V tile -> LDS (token rows beyond the sequence are zeroed: p = 0 there,
-        // but stale page bytes may hold non-finite values)
+        // V tile -> LDS as bf16 (token rows beyond the sequence are zeroed: p = 0
+        // there, but stale page bytes may hold non-finite values)
+        if constexpr (QUANT) {
+            const float vsc = __uint_as_float(t.vs);
+            const bool live = vrow < nv;
+            u32x2 *dst = reinterpret_cast<u32x2 *>(sv + vrow * PITCH + vcol);
 #pragma unroll
-        for (int v = 0; v < VLOADS; ++v) {
-            const int row = v * VRPL + vrow;
-            u32x4 x = vr[v];
-            if (row >= nv) x = u32x4{0, 0, 0, 0};
-            u32x2 *dst = reinterpret_cast<u32x2 *>(sv + row * PITCH + vch * 8);
-            dst[0] = u32x2{x[0], x[1]};
-            dst[1] = u32x2{x[2], x[3]};
+            for (int i = 0; i < 8; ++i) {
+                const u32x2 x = dequant4<DT>(t.v[i >> 2][i & 3], vsc);
+                dst[i] = live ? x : u32x2{0, 0};
+            }
+        } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int row = v * 4 + vrow;
+                u32x4 x = t.v[v];
+                if (row >= nv) x = u32x4{0, 0, 0, 0};
+                u32x2 *dst = reinterpret_cast<u32x2 *>(sv + row * PITCH + vcol);
+                dst[0] = u32x2{x[0], x[1]};
+                dst[1] = u32x2{x[2], x[3]};
+            }
         }
         // O^T[d][h] += V^T[d][t] P^T[t][h]; A lane holds V[t = 4*g4 + jj][d = 16n + r16]
         const uint16_t *col = sv + (4 * g4) * PITCH + r16;
@@ -398,17 +490,17 @@ void decode_mfma_kernel(DecodeArgs a) {
         // end they re-read the last tile, an L2 hit) so no branch joins paths
         // with different loads in flight.
         auto clampi = [&](int i) { return i < n ? i : n - 1; };
-        u32x4 ka[KSTEPS], va[VLOADS], kb[KSTEPS], vb[VLOADS], kc[KSTEPS], vc[VLOADS];
-        bool oka = load_tile(0, ka, va), okb = load_tile(clampi(1), kb, vb), okc;
+        Tile<DT> ta, tb, tc;
+        bool oka = load_tile(0, ta), okb = load_tile(clampi(1), tb), okc;
         for (int i = 0; i < n; i += 3) {
-            okc = load_tile(clampi(i + 2), kc, vc);
-            compute_tile(c0 + i, i, ka, va, oka);
+            okc = load_tile(clampi(i + 2), tc);
+            compute_tile(c0 + i, i, ta, oka);
             if (i + 1 >= n) break;
-            oka = load_tile(clampi(i + 3), ka, va);
-            compute_tile(c0 + i + 1, i + 1, kb, vb, okb);
+            oka = load_tile(clampi(i + 3), ta);
+            compute_tile(c0 + i + 1, i + 1, tb, okb);
             if (i + 2 >= n) break;
-            okb = load_tile(clampi(i + 4), kb, vb);
-            compute_tile(c0 + i + 2, i + 2, kc, vc, okc);
+            okb = load_tile(clampi(i + 4), tb);
+            compute_tile(c0 + i + 2, i + 2, tc, okc);
         }
     }
 }
@@ -475,11 +567,11 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
     }
 }
 
-template <int BS, bool QF32>
+template <int BS, bool QF32, int DT>
 hipError_t launch_cfg(const DecodeArgs &a, hipStream_t s) {
     const int64_t waves = (int64_t)a.n_kv_heads * a.slices;
     const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves));
-    hipLaunchKernelGGL((decode_mfma_kernel<128, BS, QF32>), grid, dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((decode_mfma_kernel<128, BS, QF32, DT>), grid, dim3(kThreads), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((decode_merge_kernel<128>), dim3((unsigned)a.batch, (unsigned)a.n_kv_heads),
@@ -487,13 +579,22 @@ hipError_t launch_cfg(const DecodeArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <int DT>
+hipError_t launch_dt(const DecodeArgs &a, hipStream_t s) {
+    if (a.block_size == 16)
+        return a.q_dtype == AIR_KV_F32 ? launch_cfg<16, true, DT>(a, s) : launch_cfg<16, false, DT>(a, s);
+    return a.q_dtype == AIR_KV_F32 ? launch_cfg<32, true, DT>(a, s) : launch_cfg<32, false, DT>(a, s);
+}
+
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 }  // namespace
 
-bool decode_mfma_supported(int dtype, int head_dim, int block_size, int group) {
-    return dtype == AIR_KV_BF16 && head_dim == 128 && (block_size == 16 || block_size == 32) &&
-           group >= 1 && group <= 16;
+bool decode_mfma_supported(int dtype, int head_dim, int block_size, int group, int scale_group) {
+    if (head_dim != 128 || (block_size != 16 && block_size != 32) || group < 1 || group > 16) return false;
+    if (dtype == AIR_KV_BF16) return true;
+    // 1-byte pages: a lane's 32 contiguous codes must share one scale
+    return (dtype == AIR_KV_INT8 || dtype == AIR_KV_FP8) && scale_group >= 32;
 }
 
 // Slices per kv head: enough waves for AIRKV_DECODE_WAVES_PER_EU waves on
@@ -511,6 +612,7 @@ int plan_decode_mfma(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int
     const int64_t cap = (int64_t)(nb > 0 ? nb : 1) * max_splits;
     slices = slices > cap ? cap : slices;
     plan->mfma = true;
+    plan->dtype = p.desc.dtype;
     plan->part_tokens = plan->num_parts = 0;
     plan->slices = (int32_t)slices;
     plan->batch_per_launch = nb;
@@ -536,9 +638,9 @@ hipError_t launch_decode_mfma(const DecodeArgs &base, const DecodePlan &plan, vo
         a.part_ml = (float *)ws;
         ws += align256((size_t)a.n_q_heads * plan.slots * 2 * 4);
         a.part_o = (float *)ws;
-        hipError_t e = a.block_size == 16
-                           ? (a.q_dtype == AIR_KV_F32 ? launch_cfg<16, true>(a, s) : launch_cfg<16, false>(a, s))
-                           : (a.q_dtype == AIR_KV_F32 ? launch_cfg<32, true>(a, s) : launch_cfg<32, false>(a, s));
+        hipError_t e = plan.dtype == AIR_KV_BF16   ? launch_dt<AIR_KV_BF16>(a, s)
+                       : plan.dtype == AIR_KV_INT8 ? launch_dt<AIR_KV_INT8>(a, s)
+                                                   : launch_dt<AIR_KV_FP8>(a, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

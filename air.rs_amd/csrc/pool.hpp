@@ -30,6 +30,7 @@ inline bool dtype_quantized(int dt) { return dt == AIR_KV_INT8 || dt == AIR_KV_F
 // Partitioning of one decode launch (shared by the workspace query).
 struct DecodePlan {
     int32_t group;        // q heads per kv head
+    int32_t dtype;        // page dtype of the pool
     bool mfma;            // matrix-core kernel with balanced slices (else fixed partitions)
     // fixed partitions (vector kernel)
     int32_t part_tokens;  // tokens per split-K partition (multiple of block_size)
