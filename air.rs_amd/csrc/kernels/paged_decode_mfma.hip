@@ -60,7 +60,10 @@ constexpr int kMinChunk = 4;               // tiles per slice at least
 
 // Build-time tuning knobs (defaults are the shipped configuration).
 #ifndef AIRKV_DECODE_WAVES_PER_EU
-#define AIRKV_DECODE_WAVES_PER_EU 2        // register budget: waves per SIMD
+#define AIRKV_DECODE_WAVES_PER_EU 2        // register budget: waves per SIMD, bf16 pages
+#endif
+#ifndef AIRKV_DECODE_QWAVES_PER_EU
+#define AIRKV_DECODE_QWAVES_PER_EU 3       // the same for 1-byte pages (fewer raw registers per tile)
 #endif
 #ifndef AIRKV_DECODE_NT_LOADS
 #define AIRKV_DECODE_NT_LOADS 1            // non-temporal K/V loads
@@ -209,8 +212,14 @@ __device__ __forceinline__ u32x2 dequant4(uint32_t w, float s) {
                  __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2))};
 }
 
+// Waves per SIMD the slice kernel is built for (its register budget) and
+// launched with (slices per kv head).
+constexpr int waves_per_simd(int dt) {
+    return dt == AIR_KV_BF16 ? AIRKV_DECODE_WAVES_PER_EU : AIRKV_DECODE_QWAVES_PER_EU;
+}
+
 template <int D, int BS, bool QF32, int DT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AIRKV_DECODE_WAVES_PER_EU)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(waves_per_simd(DT))))
 void decode_mfma_kernel(DecodeArgs a) {
     static_assert(D == 128, "lane mappings assume head_dim 128");
     constexpr bool QUANT = DT != AIR_KV_BF16;
@@ -440,12 +449,19 @@ void decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) p[i] = (sc[i] == -INFINITY) ? 0.0f : exp2f(sc[i] - m_run);
         l_run += (p[0] + p[1]) + (p[2] + p[3]);
-        // P^T as the B operand (lane: tokens 4*g4 .. +3 of head r16), hi + lo halves
+        // P^T as the B operand (lane: tokens 4*g4 .. +3 of head r16).  bf16
+        // pages take hi + lo bf16 halves (~16 mantissa bits); 1-byte pages,
+        // whose V operand is already a bf16 rounding of code * scale, take
+        // the hi half only.
         uint32_t h[4], l[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) split_bf16(p[i], h[i], l[i]);
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (QUANT) h[i] = bf16_bits(p[i]);
+            else split_bf16(p[i], h[i], l[i]);
+        }
         const u32x2 p_hi = {h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-        const u32x2 p_lo = {l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
+        u32x2 p_lo = {0, 0};
+        if constexpr (!QUANT) p_lo = u32x2{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
         // V tile -> LDS as bf16 (token rows beyond the sequence are zeroed: p = 0
         // there, but stale page bytes may hold non-finite values)
         if constexpr (QUANT) {
@@ -476,7 +492,7 @@ void decode_mfma_kernel(DecodeArgs a) {
             const u32x2 av = {(uint32_t)c[0] | ((uint32_t)c[PITCH] << 16),
                               (uint32_t)c[2 * PITCH] | ((uint32_t)c[3 * PITCH] << 16)};
             acc[n] = mfma_pv(av, p_hi, acc[n]);
-            acc[n] = mfma_pv(av, p_lo, acc[n]);
+            if constexpr (!QUANT) acc[n] = mfma_pv(av, p_lo, acc[n]);
         }
         if ((last_m >> idx) & 1) emit(bq);
     };
@@ -597,8 +613,8 @@ bool decode_mfma_supported(int dtype, int head_dim, int block_size, int group, i
     return (dtype == AIR_KV_INT8 || dtype == AIR_KV_FP8) && scale_group >= 32;
 }
 
-// Slices per kv head: enough waves for AIRKV_DECODE_WAVES_PER_EU waves on
-// every SIMD (4 per compute unit), at most batch * max_splits.  The workspace
+// Slices per kv head: one wave for every wave slot of the GPU (4 SIMDs per
+// compute unit x waves_per_simd), at most batch * max_splits.  The workspace
 // holds the tile prefix and (slices + batch) partial rows per query head.
 int plan_decode_mfma(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int32_t max_blocks,
                      int32_t max_splits, DecodePlan *plan) {
@@ -607,7 +623,7 @@ int plan_decode_mfma(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int
     const int64_t tiles_per_seq = ((int64_t)max_blocks * bs + 15) / 16;
     if ((int64_t)nb * tiles_per_seq > INT32_MAX)
         return fail(AIR_KV_E_INVALID_ARG, "batch x max_blocks too large for one decode launch");
-    const int64_t machine_waves = (int64_t)p.cus * 4 * AIRKV_DECODE_WAVES_PER_EU;
+    const int64_t machine_waves = (int64_t)p.cus * 4 * waves_per_simd(p.desc.dtype);
     int64_t slices = (machine_waves + nkv - 1) / nkv;
     const int64_t cap = (int64_t)(nb > 0 ? nb : 1) * max_splits;
     slices = slices > cap ? cap : slices;
