@@ -12,11 +12,12 @@ from .kv_swap import KvSwapManager, pool_callbacks
 from .paged_attention import (BLOCK_SIZE, MAX_BLOCKS, BlockAllocator, BlockTable,
                               SequenceManager, num_blocks_for_tokens)
 from .pool import KvPool
+from .session import PagedSessionCache
 
 __all__ = [
     "AIR_KV_OK", "AIR_KV_E_INVALID_ARG", "AIR_KV_E_OOM", "AIR_KV_E_NOT_FOUND", "AIR_KV_E_HIP",
     "AIR_KV_E_STATE", "F32", "BF16", "INT8", "FP8", "LAYOUT_HEAD_MAJOR", "LAYOUT_TOKEN_MAJOR",
     "LIB_PATH", "SIGNATURES", "AirKvError", "last_error", "load", "KvSwapManager",
     "pool_callbacks", "BLOCK_SIZE", "MAX_BLOCKS", "BlockAllocator", "BlockTable",
-    "SequenceManager", "num_blocks_for_tokens", "KvPool",
+    "SequenceManager", "num_blocks_for_tokens", "KvPool", "PagedSessionCache",
 ]

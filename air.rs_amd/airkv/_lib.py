@@ -74,6 +74,8 @@ SIGNATURES = {
     "air_seq_fork": (_int, [_P, _u32, _pu32]),
     "air_seq_free": (_int, [_P, _u32]),
     "air_seq_cow_last_block": (_int, [_P, _u32, _pu32, _pu32]),
+    "air_seq_truncate": (_int, [_P, _u32, _i64]),
+    "air_seq_cow_block": (_int, [_P, _u32, _i64, _pu32, _pu32]),
     "air_seq_table": (_int, [_P, _u32, _pu32, _i32, _pi32, _pi64]),
     "air_seq_export_tables": (_int, [_P, _pu32, _i32, _i32, _pi32, _pi32]),
     "air_seq_num_sequences": (_i64, [_P]),
@@ -98,6 +100,17 @@ SIGNATURES = {
     "air_paged_decode_workspace_size": (_int, [_P, _i32, _i32, _i32, _i32, ctypes.POINTER(_SZ)]),
     "air_paged_decode": (_int, [_P, _P, _P, _i32, _i32, _P, _P, _i32, _i32, ctypes.c_float, _i32, _P,
                                 _SZ, _P, _i32]),
+    "air_kv_session_create": (_int, [_P, ctypes.POINTER(_P), _i32, ctypes.POINTER(_P)]),
+    "air_kv_session_destroy": (_int, [_P]),
+    "air_kv_session_fork": (_int, [_P, ctypes.POINTER(_P)]),
+    "air_kv_session_seq_id": (_int, [_P, _pu32]),
+    "air_kv_session_seq_len": (_int, [_P, _i32, _pi64]),
+    "air_kv_session_append": (_int, [_P, _P, _i32, _P, _P, _i64]),
+    "air_kv_session_save": (_int, [_P, _P, _i32, _P, _P, _i64]),
+    "air_kv_session_load": (_int, [_P, _P, _i32, _P, _P, _i32]),
+    "air_kv_session_clear": (_int, [_P]),
+    "air_kv_session_truncate_to": (_int, [_P, _i64]),
+    "air_kv_session_memory_usage": (_int, [_P, ctypes.POINTER(_SZ)]),
     "air_kv_copy_blocks": (_int, [_P, _P, _P, _P, _i32]),
     "air_kv_read_blocks": (_int, [_P, _P, _pi32, _i32, _P]),
     "air_kv_write_blocks": (_int, [_P, _P, _pi32, _i32, _P]),

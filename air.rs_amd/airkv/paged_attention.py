@@ -218,6 +218,19 @@ class SequenceManager:
         _lib.check(rc)
         return o.value, n.value
 
+    def truncate(self, seq, n_tokens):
+        """Keep the first n_tokens tokens of seq and release the blocks past
+        them (no counterpart in the reference; see air_seq_truncate)."""
+        _raise_for(_lib.load().air_seq_truncate(self._h, seq, n_tokens), "truncate")
+
+    def cow_block(self, seq, index):
+        """cow_last_block for the block at table index `index`: returns
+        (old_block, new_block); equal when the block was not shared."""
+        o, n = ctypes.c_uint32(), ctypes.c_uint32()
+        _raise_for(_lib.load().air_seq_cow_block(self._h, seq, index, ctypes.byref(o), ctypes.byref(n)),
+                   "cow_block")
+        return o.value, n.value
+
     def export_tables(self, seqs, max_blocks):
         seqs = np.ascontiguousarray(seqs, np.uint32)
         tables = np.empty((len(seqs), max_blocks), np.int32)

@@ -5,8 +5,7 @@
 #include <vector>
 
 #include "air_kv.h"
-#include "kv_swap.hpp"
-#include "paged_attention.hpp"
+#include "handles.hpp"
 #include "status.hpp"
 
 using airkv::fail;
@@ -18,20 +17,6 @@ std::string &last_error_slot() {
 }
 }  // namespace airkv
 
-struct air_block_allocator {
-    airkv::BlockAllocator *impl;
-    bool owned;
-};
-struct air_seq_manager {
-    airkv::SequenceManager *impl;
-    air_block_allocator alloc_view;
-    bool owned;
-};
-struct air_kv_swap {
-    airkv::KvSwapManager impl;
-    air_seq_manager mgr_view;
-    air_kv_swap(int64_t c, int32_t bs, size_t bb) : impl(c, bs, bb) {}
-};
 
 namespace {
 
@@ -248,6 +233,23 @@ int air_seq_cow_last_block(air_seq_manager *m, uint32_t seq, uint32_t *old_block
     CHECK_MGR(m);
     uint32_t o, nb;
     int rc = m->impl->cow_last_block(seq, &o, &nb);
+    if (rc == AIR_KV_OK) {
+        if (old_block) *old_block = o;
+        if (new_block) *new_block = nb;
+    }
+    return rc;
+}
+
+int air_seq_truncate(air_seq_manager *m, uint32_t seq, int64_t n_tokens) {
+    CHECK_MGR(m);
+    return m->impl->truncate(seq, n_tokens);
+}
+
+int air_seq_cow_block(air_seq_manager *m, uint32_t seq, int64_t index, uint32_t *old_block,
+                      uint32_t *new_block) {
+    CHECK_MGR(m);
+    uint32_t o, nb;
+    int rc = m->impl->cow_block(seq, index, &o, &nb);
     if (rc == AIR_KV_OK) {
         if (old_block) *old_block = o;
         if (new_block) *new_block = nb;

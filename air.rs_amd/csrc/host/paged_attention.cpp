@@ -133,6 +133,42 @@ int SequenceManager::cow_last_block(uint32_t seq, uint32_t *old_block, uint32_t 
     return AIR_KV_OK;
 }
 
+int SequenceManager::truncate(uint32_t seq, int64_t n_tokens) {
+    auto it = tables_.find(seq);
+    if (it == tables_.end()) return fail(AIR_KV_E_NOT_FOUND, "sequence not found (%u)", seq);
+    if (n_tokens < 0) return fail(AIR_KV_E_INVALID_ARG, "truncate: negative length");
+    BlockTable &t = it->second;
+    if (n_tokens >= t.num_tokens) return AIR_KV_OK;
+    const int32_t bs = block_size();
+    const size_t keep = (size_t)BlockAllocator::num_blocks_for_tokens(n_tokens, bs);
+    if (keep > t.physical_blocks.size())
+        return fail(AIR_KV_E_STATE, "sequence %u holds fewer blocks than its length needs", seq);
+    for (size_t i = keep; i < t.physical_blocks.size(); ++i) allocator_.release(t.physical_blocks[i]);
+    t.physical_blocks.resize(keep);
+    t.num_tokens = n_tokens;
+    if (keep > 0) {
+        const uint32_t last = t.physical_blocks.back();
+        if (allocator_.ref_count(last) == 1)
+            allocator_.set_fill(last, (int32_t)(n_tokens - (int64_t)(keep - 1) * bs));
+    }
+    return AIR_KV_OK;
+}
+
+int SequenceManager::cow_block(uint32_t seq, int64_t index, uint32_t *old_block, uint32_t *new_block) {
+    auto it = tables_.find(seq);
+    if (it == tables_.end()) return fail(AIR_KV_E_NOT_FOUND, "sequence not found (%u)", seq);
+    std::vector<uint32_t> &blocks = it->second.physical_blocks;
+    if (index < 0 || index >= (int64_t)blocks.size())
+        return fail(AIR_KV_E_INVALID_ARG, "cow_block: index %lld outside the table", (long long)index);
+    const uint32_t b = blocks[(size_t)index];
+    uint32_t nid;
+    if (!allocator_.cow_write(b, &nid)) return fail(AIR_KV_E_OOM, "out of memory — cow_write");
+    blocks[(size_t)index] = nid;
+    *old_block = b;
+    *new_block = nid;
+    return AIR_KV_OK;
+}
+
 int SequenceManager::swap_out(uint32_t seq, std::vector<uint32_t> *blocks) {   // :353-362
     auto it = tables_.find(seq);
     if (it == tables_.end()) return fail(AIR_KV_E_NOT_FOUND, "sequence not found (%u)", seq);

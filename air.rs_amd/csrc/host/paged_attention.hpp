@@ -42,6 +42,12 @@ public:
     static int64_t num_blocks_for_tokens(int64_t n, int32_t bs) { return (n + bs - 1) / bs; }
     float utilization() const { return (float)num_used_blocks() / (float)total_blocks_; }
 
+    // Fill metadata of a block this caller owns alone (truncation of a sequence).
+    void set_fill(uint32_t id, int32_t num_tokens) {
+        blocks_[id].num_tokens = num_tokens;
+        blocks_[id].is_full = num_tokens == block_size_;
+    }
+
     bool valid(uint32_t id) const { return (int64_t)id < total_blocks_; }
     const PhysicalBlock &block(uint32_t id) const { return blocks_[id]; }
     int64_t total_blocks() const { return total_blocks_; }
@@ -81,6 +87,16 @@ public:
     bool can_schedule() const { return allocator_.can_allocate(1); }
     int swap_out(uint32_t seq, std::vector<uint32_t> *blocks);
     int swap_in(uint32_t seq, int32_t n_blocks, std::vector<uint32_t> *blocks);
+
+    // Extensions the reference has no counterpart for (its dense cache rolls
+    // back with Tensor::narrow, src/kv_cache.rs:364-383):
+    //  * truncate: keep the first n_tokens tokens, release the blocks past
+    //    them (FIFO push_back, like free_sequence) and, when the new last
+    //    block is owned by this sequence alone, set its fill to what remains.
+    //  * cow_block: copy-on-write of the block at table index `index` (the
+    //    reference's cow_last_block generalised to any index).
+    int truncate(uint32_t seq, int64_t n_tokens);
+    int cow_block(uint32_t seq, int64_t index, uint32_t *old_block, uint32_t *new_block);
 
 private:
     BlockAllocator allocator_;

@@ -129,6 +129,16 @@ int air_seq_free(air_seq_manager *m, uint32_t seq);
  * allocation.  *old_block / *new_block tell the caller which page to copy. */
 int air_seq_cow_last_block(air_seq_manager *m, uint32_t seq, uint32_t *old_block,
                            uint32_t *new_block);
+/* No counterpart in the reference (its dense cache rolls back with
+ * Tensor::narrow, src/kv_cache.rs:364-383): keeps the first n_tokens tokens
+ * of `seq`, releases the blocks past them to the free list (in table order)
+ * and, when the new last block belongs to `seq` alone, sets its fill to what
+ * remains.  A no-op when n_tokens >= the sequence's length. */
+int air_seq_truncate(air_seq_manager *m, uint32_t seq, int64_t n_tokens);
+/* cow_last_block generalised to the block at table index `index` (no
+ * counterpart in the reference): a private copy replaces a shared block. */
+int air_seq_cow_block(air_seq_manager *m, uint32_t seq, int64_t index, uint32_t *old_block,
+                      uint32_t *new_block);
 /* table (:322-324): copies up to `cap` block ids. */
 int air_seq_table(const air_seq_manager *m, uint32_t seq, uint32_t *blocks, int32_t cap,
                   int32_t *n_blocks, int64_t *n_tokens);
@@ -242,6 +252,54 @@ int air_paged_decode(air_kv_pool *pool, void *stream, const void *q, int32_t q_d
                      int32_t n_q_heads, const int32_t *block_tables, const int32_t *seq_lens,
                      int32_t batch, int32_t max_blocks, float scale, int32_t max_splits,
                      void *workspace, size_t ws_bytes, void *out, int32_t out_dtype);
+
+/* ------------------------------------------------------------------------ */
+/* SessionKvCache over pages                                                 */
+/* ------------------------------------------------------------------------ */
+
+/* The paged counterpart of SessionKvCache (src/kv_cache.rs:431-446) for one
+ * sequence of `mgr`: layer l keeps its K/V in layer_pools[l] (every pool has
+ * the manager's block_size and at least its capacity in blocks), and all
+ * layers share the sequence's block table.  Creating a session creates the
+ * sequence; destroying it frees the sequence's blocks.  The session is not
+ * thread-safe (like the manager).  Device work is ordered on `stream`; the
+ * session keeps small device and pinned host staging buffers of its own. */
+typedef struct air_kv_session air_kv_session;
+int air_kv_session_create(air_seq_manager *mgr, air_kv_pool *const *layer_pools, int32_t n_layers,
+                          air_kv_session **out);
+int air_kv_session_destroy(air_kv_session *s);
+/* A new session whose sequence is fork_sequence(parent) (src/paged_attention.rs:290-310):
+ * the child shares the parent's blocks and per-layer lengths; a shared block
+ * is copied (in every layer's pool) before either session writes into it. */
+int air_kv_session_fork(air_kv_session *parent, air_kv_session **out);
+int air_kv_session_seq_id(const air_kv_session *s, uint32_t *seq);
+/* seq_len(layer) (:433): tokens stored for the layer, 0 if empty. */
+int air_kv_session_seq_len(const air_kv_session *s, int32_t layer, int64_t *len);
+/* Appends n_new rows k/v (f32 [n_new][n_kv_heads][head_dim], device) after the
+ * layer's stored tokens: the reshape-and-cache that replaces the
+ * Tensor::cat of src/model.rs:569.  Allocates blocks on block boundaries. */
+int air_kv_session_append(air_kv_session *s, void *stream, int32_t layer, const float *k,
+                          const float *v, int64_t n_new);
+/* save(layer, cache) (:436): the layer's cache becomes the n_tokens rows of
+ * k/v (f32 [n_tokens][n_kv_heads][head_dim], device).  The decode loop only
+ * grows a cache by concatenation, so rows already stored are taken as equal to
+ * the first rows of k/v and are not rewritten: rows past the stored length are
+ * appended, and a shorter n_tokens shortens the layer as truncate_to does. */
+int air_kv_session_save(air_kv_session *s, void *stream, int32_t layer, const float *k,
+                        const float *v, int64_t n_tokens);
+/* load(layer) (:439): the layer's tokens as the dense [seq][n_kv_heads][head_dim]
+ * view of LayerCache::Attention (src/kv_cache.rs:121-122) in out_k / out_v
+ * (device, out_dtype AIR_KV_F32 or AIR_KV_BF16; 1-byte pools dequantize). */
+int air_kv_session_load(air_kv_session *s, void *stream, int32_t layer, void *out_k, void *out_v,
+                        int32_t out_dtype);
+/* clear() (:442): every layer empty, all blocks released. */
+int air_kv_session_clear(air_kv_session *s);
+/* truncate_to(pos) (:445, src/kv_cache.rs:364-383): every layer keeps at most
+ * pos tokens; blocks past them are released.  No device work. */
+int air_kv_session_truncate_to(air_kv_session *s, int64_t pos);
+/* Bytes of device memory the session's blocks occupy over all its layers
+ * (the paged form of memory_usage, src/kv_cache.rs:388-414). */
+int air_kv_session_memory_usage(const air_kv_session *s, size_t *bytes);
 
 /* Copies whole blocks src[i] -> dst[i] (int32, device): the page copy that
  * BlockAllocator::cow_write leaves to "a real impl" (src/paged_attention.rs:160). */

@@ -407,3 +407,80 @@ def test_random_ops_match_oracle_tables(block_size):
             assert tp.physical_blocks == to.physical_blocks and tp.num_tokens == to.num_tokens
     for b in range(cap):
         assert P.allocator.ref_count(b) == O.allocator.ref_count(b)
+
+
+# ---- extensions without a reference counterpart (product only) -------------
+
+def test_truncate_releases_trailing_blocks_fifo():
+    """truncate keeps ceil(n/bs) blocks, pushes the others onto the back of
+    the free list in table order, and leaves the front of the list alone."""
+    order = np.array([5, 2, 7, 0, 1, 3, 4, 6], np.uint32)
+    mgr = airkv.SequenceManager(8, block_size=16, free_order=order)
+    s = mgr.create_sequence()
+    mgr.append_slots(s, 40)                  # blocks 5, 2, 7
+    mgr.truncate(s, 17)                      # keeps 5, 2; releases 7
+    t = mgr.table(s)
+    assert t.physical_blocks == [5, 2] and t.num_tokens == 17
+    assert mgr.allocator.num_free_blocks() == 6
+    # free list now 0 1 3 4 6 7: the next fresh sequence takes 0 first, 7 last
+    o = mgr.create_sequence()
+    assert [mgr.append_token(o) for _ in range(16 * 6)][::16] == [0, 1, 3, 4, 6, 7]
+
+
+def test_truncate_sets_fill_and_appends_continue():
+    mgr = airkv.SequenceManager(4, block_size=16)
+    s = mgr.create_sequence()
+    mgr.append_slots(s, 32)                  # two full blocks
+    mgr.truncate(s, 20)
+    last = mgr.table(s).physical_blocks[-1]
+    assert mgr.allocator.block_info(last) == (4, False)
+    slots = mgr.append_slots(s, 12)          # fills block 1 exactly, no new block
+    assert len(mgr.table(s).physical_blocks) == 2
+    assert slots.tolist() == [last * 16 + p for p in range(4, 16)]
+    assert mgr.allocator.block_info(last) == (16, True)
+    mgr.append_token(s)                      # next token opens a new block
+    assert len(mgr.table(s).physical_blocks) == 3
+
+
+def test_truncate_noop_zero_and_errors():
+    mgr = airkv.SequenceManager(4, block_size=16)
+    s = mgr.create_sequence()
+    mgr.append_slots(s, 10)
+    mgr.truncate(s, 10)
+    mgr.truncate(s, 99)
+    assert mgr.table(s).num_tokens == 10
+    mgr.truncate(s, 0)
+    assert mgr.table(s).physical_blocks == [] and mgr.allocator.num_free_blocks() == 4
+    with pytest.raises(KeyError):
+        mgr.truncate(77, 0)
+    with pytest.raises(airkv.AirKvError):
+        mgr.truncate(s, -1)
+
+
+def test_truncate_into_shared_block_keeps_its_fill():
+    """A block shared with a fork keeps the fill the other sequence gave it."""
+    mgr = airkv.SequenceManager(8, block_size=16)
+    s = mgr.create_sequence()
+    mgr.append_slots(s, 30)
+    c = mgr.fork_sequence(s)
+    mgr.truncate(c, 5)
+    first = mgr.table(s).physical_blocks[0]
+    assert mgr.table(c).physical_blocks == [first]
+    assert mgr.allocator.ref_count(first) == 2
+    assert mgr.allocator.block_info(first) == (16, True)
+    assert mgr.allocator.ref_count(mgr.table(s).physical_blocks[1]) == 1
+
+
+def test_cow_block_any_index():
+    mgr = airkv.SequenceManager(8, block_size=16)
+    s = mgr.create_sequence()
+    mgr.append_slots(s, 40)
+    c = mgr.fork_sequence(s)
+    blocks = mgr.table(s).physical_blocks
+    old, new = mgr.cow_block(c, 1)
+    assert old == blocks[1] and new not in blocks
+    assert mgr.table(c).physical_blocks == [blocks[0], new, blocks[2]]
+    assert mgr.allocator.ref_count(old) == 1 and mgr.allocator.ref_count(new) == 1
+    assert mgr.cow_block(c, 1) == (new, new)            # now private: no copy
+    with pytest.raises(airkv.AirKvError):
+        mgr.cow_block(c, 3)
