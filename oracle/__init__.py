@@ -73,6 +73,13 @@ def lib():
                 "orc_reference_attention_f64": (None, [_P, _P, _P, _i32, _i32, _f64, _P]),
                 "orc_paged_decode": (_i32, [_i32, _i32, _i32, _i32, _i32, _i64, _P, _P, _P, _P,
                                             _P, _i32, _P, _P, _i32, _i32, _f32, _i32, _P]),
+                "orc_key_compress": (None, [_P, _SZ, _P, _P, _P]),
+                "orc_key_decompress": (None, [_P, _f32, _f32, _SZ, _P]),
+                "orc_value_compress": (None, [_P, _SZ, _P, _P, _P]),
+                "orc_value_decompress": (None, [_P, _f32, _f32, _SZ, _P]),
+                "orc_qjl_projection_matrix": (None, [_SZ, _SZ, _u64, _P]),
+                "orc_qjl_compress": (None, [_P, _SZ, _P, _SZ, _P, _P]),
+                "orc_qjl_cos_sim": (_f32, [_P, _P, _SZ]),
             }
             for name, (res, args) in sig.items():
                 fn = getattr(L, name)
@@ -311,3 +318,61 @@ def reference_attention_f64(q, k, v, kv_len, head_dim, scale=None):
 def max_abs_error(a, b) -> float:
     """src/flash_decode.rs:210-212."""
     return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))))
+
+
+# --------------------------------------------------------------------------
+# kv_compress warm-tier codecs (src/kv_compress.rs)
+# --------------------------------------------------------------------------
+
+def key_compress(key):
+    """CompressedKey::compress -> (sign bits uint64[ceil(d/64)], magnitude, mean)."""
+    key = _c(key, np.float32).ravel()
+    bits = np.zeros(max((len(key) + 63) // 64, 1), np.uint64)
+    mag, mean = ctypes.c_float(), ctypes.c_float()
+    lib().orc_key_compress(_ptr(key), len(key), _ptr(bits), ctypes.byref(mag), ctypes.byref(mean))
+    return bits[:(len(key) + 63) // 64], np.float32(mag.value), np.float32(mean.value)
+
+
+def key_decompress(bits, magnitude, mean, dim):
+    bits = _c(bits, np.uint64)
+    out = np.empty(dim, np.float32)
+    lib().orc_key_decompress(_ptr(bits) if bits.size else None, float(magnitude), float(mean), dim,
+                             _ptr(out))
+    return out
+
+
+def value_compress(v):
+    """CompressedValue::compress -> (codes uint8[d], scale, min)."""
+    v = _c(v, np.float32).ravel()
+    q = np.empty(len(v), np.uint8)
+    scale, mn = ctypes.c_float(), ctypes.c_float()
+    lib().orc_value_compress(_ptr(v), len(v), _ptr(q), ctypes.byref(scale), ctypes.byref(mn))
+    return q, np.float32(scale.value), np.float32(mn.value)
+
+
+def value_decompress(q, scale, min_val):
+    q = _c(q, np.uint8).ravel()
+    out = np.empty(len(q), np.float32)
+    lib().orc_value_decompress(_ptr(q), float(scale), float(min_val), len(q), _ptr(out))
+    return out
+
+
+def qjl_projection_matrix(proj_dim, orig_dim, seed):
+    out = np.empty(proj_dim * orig_dim, np.float32)
+    lib().orc_qjl_projection_matrix(proj_dim, orig_dim, seed, _ptr(out))
+    return out
+
+
+def qjl_compress(key, proj, proj_dim):
+    """QjlKey::compress -> (bits uint64[ceil(m/64)], magnitude)."""
+    key = _c(key, np.float32).ravel()
+    proj = _c(proj, np.float32).ravel()
+    assert proj.size == proj_dim * key.size
+    bits = np.zeros((proj_dim + 63) // 64, np.uint64)
+    mag = ctypes.c_float()
+    lib().orc_qjl_compress(_ptr(key), len(key), _ptr(proj), proj_dim, _ptr(bits), ctypes.byref(mag))
+    return bits, np.float32(mag.value)
+
+
+def qjl_cos_sim(a, b, proj_dim):
+    return np.float32(lib().orc_qjl_cos_sim(_ptr(_c(a, np.uint64)), _ptr(_c(b, np.uint64)), proj_dim))

@@ -464,3 +464,136 @@ int orc_paged_decode(int dtype, int block_size, int n_kv_heads, int head_dim, in
     }
     return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* kv_compress warm-tier codecs (src/kv_compress.rs)                         */
+/* ------------------------------------------------------------------------ */
+
+/* Rust f32::min: NaN-ignoring, like rust_max. */
+static inline float rust_min(float a, float b) {
+    if (isnan(a)) return b;
+    if (isnan(b)) return a;
+    return a < b ? a : b;
+}
+
+/* `iter.sum::<f32>()`: a left fold in element order.  Current Rust starts the
+ * fold at -0.0 (the additive identity that keeps the sign of an all -0.0
+ * sum); only empty and all-negative-zero inputs can tell the difference. */
+static float rust_sum_sq(const float *x, size_t n) {
+    float s = -0.0f;
+    for (size_t i = 0; i < n; ++i) s += x[i] * x[i];
+    return s;
+}
+
+/* CompressedKey::compress (src/kv_compress.rs:79-109): mean and L2 norm by
+ * left folds, bit i = key[i] >= mean (a NaN element leaves its bit clear),
+ * packed LSB-first into ceil(dim / 64) words. */
+void orc_key_compress(const float *key, size_t dim, uint64_t *bits, float *magnitude,
+                      float *mean) {
+    float s = -0.0f;
+    for (size_t i = 0; i < dim; ++i) s += key[i];
+    const float m = dim > 0 ? s / (float)dim : 0.0f;
+    for (size_t w = 0; w < (dim + 63) / 64; ++w) bits[w] = 0;
+    for (size_t i = 0; i < dim; ++i)
+        if (key[i] >= m) bits[i / 64] |= 1ull << (i % 64);
+    *magnitude = sqrtf(rust_sum_sq(key, dim));
+    *mean = m;
+}
+
+/* CompressedKey::decompress (:112-127): sign_i * (|k| / sqrt(dim)) + mean,
+ * as a product and a sum (no fused multiply-add in Rust). */
+void orc_key_decompress(const uint64_t *bits, float magnitude, float mean, size_t dim, float *out) {
+    const float scale = dim > 0 ? magnitude / sqrtf((float)dim) : 0.0f;
+    for (size_t i = 0; i < dim; ++i) {
+        const float sign = ((bits[i / 64] >> (i % 64)) & 1u) ? 1.0f : -1.0f;
+        const float p = sign * scale;
+        out[i] = p + mean;
+    }
+}
+
+/* CompressedValue::compress (:187-218): NaN-ignoring min / max folds from
+ * +inf / -inf; scale = range / 255 (or 1.0 when range <= 0);
+ * q = round_half_away((v - min) / scale) clamped to [0, 255]; Rust's `as u8`
+ * sends NaN to 0.  An empty vector has scale 0 and min 0. */
+void orc_value_compress(const float *v, size_t dim, uint8_t *q, float *scale, float *min_val) {
+    if (dim == 0) {
+        *scale = 0.0f;
+        *min_val = 0.0f;
+        return;
+    }
+    float lo = INFINITY, hi = -INFINITY;
+    for (size_t i = 0; i < dim; ++i) {
+        lo = rust_min(lo, v[i]);
+        hi = rust_max(hi, v[i]);
+    }
+    const float range = hi - lo;
+    const float s = range > 0.0f ? range / 255.0f : 1.0f;
+    for (size_t i = 0; i < dim; ++i) {
+        float r = roundf((v[i] - lo) / s);
+        if (r < 0.0f) r = 0.0f;
+        if (r > 255.0f) r = 255.0f;
+        q[i] = isnan(r) ? 0 : (uint8_t)r;
+    }
+    *scale = s;
+    *min_val = lo;
+}
+
+/* CompressedValue::decompress (:221-226): q * scale + min (product, then sum). */
+void orc_value_decompress(const uint8_t *q, float scale, float min_val, size_t dim, float *out) {
+    for (size_t i = 0; i < dim; ++i) {
+        const float p = (float)q[i] * scale;
+        out[i] = p + min_val;
+    }
+}
+
+/* qjl_projection_matrix (:994-1015): the Box-Muller pairs of
+ * orc_box_muller_fill, each value scaled by 1 / sqrt(orig_dim) after the
+ * trigonometric factor: r * cos(theta) * scale, left to right. */
+void orc_qjl_projection_matrix(size_t proj_dim, size_t orig_dim, uint64_t seed, float *out) {
+    const size_t n = proj_dim * orig_dim;
+    uint64_t state = seed + 1;
+    const float two53 = 9007199254740992.0f;
+    const float scale = 1.0f / sqrtf((float)orig_dim);
+    size_t i = 0;
+    while (i < n) {
+        state = state * 6364136223846793005ULL + 1442695040888963407ULL;
+        float u1 = (float)(state >> 11) / two53;
+        state = state * 6364136223846793005ULL + 1442695040888963407ULL;
+        const float u2 = (float)(state >> 11) / two53;
+        u1 = rust_max(u1, 1e-10f);
+        const float r = sqrtf(-2.0f * logf(u1));
+        const float theta = 2.0f * 3.14159265358979323846f * u2;
+        float a = r * cosf(theta);
+        out[i++] = a * scale;
+        if (i < n) {
+            a = r * sinf(theta);
+            out[i++] = a * scale;
+        }
+    }
+}
+
+/* QjlKey::compress (:930-951): |k| by a left fold of squares; bit i set when
+ * the left-folded dot product of row i of R with k is > 0. */
+void orc_qjl_compress(const float *key, size_t dim, const float *proj, size_t proj_dim,
+                      uint64_t *bits, float *magnitude) {
+    for (size_t w = 0; w < (proj_dim + 63) / 64; ++w) bits[w] = 0;
+    for (size_t i = 0; i < proj_dim; ++i) {
+        const float *row = proj + i * dim;
+        float dot = -0.0f;
+        for (size_t j = 0; j < dim; ++j) {
+            const float p = row[j] * key[j];
+            dot += p;
+        }
+        if (dot > 0.0f) bits[i / 64] |= 1ull << (i % 64);
+    }
+    *magnitude = sqrtf(rust_sum_sq(key, dim));
+}
+
+/* QjlKey::approx_cos_sim (:959-968): cos(pi * hamming / m), the product
+ * taken before the division. */
+float orc_qjl_cos_sim(const uint64_t *a, const uint64_t *b, size_t proj_dim) {
+    uint32_t ham = 0;
+    for (size_t w = 0; w < (proj_dim + 63) / 64; ++w) ham += (uint32_t)__builtin_popcountll(a[w] ^ b[w]);
+    const float angle = 3.14159265358979323846f * (float)ham / (float)proj_dim;
+    return cosf(angle);
+}

@@ -87,6 +87,16 @@ int orc_paged_decode(int dtype, int block_size, int n_kv_heads, int head_dim, in
                      int n_q_heads, const int32_t *block_tables, const int32_t *seq_lens,
                      int batch, int max_blocks, float scale, int chunk, float *out);
 
+/* ---- kv_compress warm-tier codecs (src/kv_compress.rs) -------------------- */
+void orc_key_compress(const float *key, size_t dim, uint64_t *bits, float *magnitude, float *mean);
+void orc_key_decompress(const uint64_t *bits, float magnitude, float mean, size_t dim, float *out);
+void orc_value_compress(const float *v, size_t dim, uint8_t *q, float *scale, float *min_val);
+void orc_value_decompress(const uint8_t *q, float scale, float min_val, size_t dim, float *out);
+void orc_qjl_projection_matrix(size_t proj_dim, size_t orig_dim, uint64_t seed, float *out);
+void orc_qjl_compress(const float *key, size_t dim, const float *proj, size_t proj_dim,
+                      uint64_t *bits, float *magnitude);
+float orc_qjl_cos_sim(const uint64_t *a, const uint64_t *b, size_t proj_dim);
+
 #ifdef __cplusplus
 }
 #endif
