@@ -9,9 +9,10 @@ split-K paged decode attention over every cached token.  All inputs are
 resident in HBM before timing starts.
 
 Prints one JSON line: whole-step HBM throughput (`value`, GB/s of
-algorithmic bytes), the decode kernel's roofline fraction (HIP events on the
-launch stream), gather / large-append bandwidths, and the CPU oracle timed
-on a bounded sample of the same workload on this host.
+algorithmic bytes), the decode call's roofline fraction (HIP events on the
+launch stream; HBM traffic from the committed rocprofv3 counter runs),
+gather / large-append bandwidths, decode at the c3 / c4 / c5 configs, and the
+CPU oracle timed on the same workload on this host (all cores and one core).
 """
 import argparse
 import json
@@ -42,6 +43,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-decode", action="store_true",
                     help="skip the gather / append bandwidth legs (for profiling runs)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the c3 / c4 / c5 decode legs")
     return ap.parse_args()
 
 
@@ -77,38 +80,96 @@ def timed_loop(torch, fn, iters, lead_sleep=True):
     return e0.elapsed_time(e1) / iters   # ms
 
 
-def cpu_baseline(pool, w, tables, lens, q_f32, budget_s):
-    """Oracle paged decode (gather + flash_decode, chunk 64, one thread) on
-    whole sequences of the same workload until ~budget_s of CPU time."""
+def cpu_baseline(pool, w, tables, lens, q_f32, budget_s, decode_bytes_of):
+    """The oracle's paged decode (gather + flash_decode with chunk 64 per query
+    head, src/flash_decode.rs:153-173) on whole sequences of the same workload,
+    on this host's cores: first on one thread (every sequence, or about
+    budget_s of work), then on up to 16 threads over every sequence (ctypes
+    releases the GIL, so the C oracle calls run in parallel).  GB/s counts the
+    same algorithmic bytes as the GPU figure."""
+    import concurrent.futures
+
     import numpy as np
 
     import oracle
     cfg = w.cfg
-    bytes_per_tok = cfg.n_kv_heads * cfg.head_dim * 2 * 2
-    done_bytes, done_tok, spent, nseq = 0, 0, 0.0, 0
-    order = list(range(len(lens)))
-    for b in order:
-        L = int(lens[b])
-        nblk = -(-L // cfg.block_size)
-        ids = tables[b, :nblk].astype(np.int32)
-        raw = pool.read_blocks(ids)
-        k, v, _, _ = pool.split_blocks(raw)
-        host = oracle.HostPool(nblk, cfg.block_size, cfg.n_kv_heads, cfg.head_dim, oracle.BF16)
-        host.k[:], host.v[:] = k, v
-        tab = np.arange(nblk, dtype=np.int32).reshape(1, nblk)
-        t0 = time.perf_counter()
-        host.paged_decode(q_f32[b:b + 1], tab, np.array([L], np.int32), chunk=64)
-        spent += time.perf_counter() - t0
-        done_bytes += L * bytes_per_tok + 4 * nblk + cfg.n_q_heads * cfg.head_dim * (2 + 4)
-        done_tok += 1
-        nseq += 1
-        if spent >= budget_s:
+    k, v, _, _ = pool.snapshot()
+    host = oracle.HostPool(pool.num_blocks, cfg.block_size, cfg.n_kv_heads, cfg.head_dim, oracle.BF16)
+    host.k[:], host.v[:] = k, v
+    del k, v
+
+    def one(b):
+        host.paged_decode(q_f32[b:b + 1], tables[b:b + 1], lens[b:b + 1], chunk=64)
+
+    batch = len(lens)
+    done, t0 = 0, time.perf_counter()
+    for b in range(batch):
+        one(b)
+        done += 1
+        if time.perf_counter() - t0 >= budget_s:
             break
-    return {"value": done_bytes / spent / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{nseq} of {len(lens)} sequences of the same workload (all 32 q heads, "
-                      f"{sum(int(lens[b]) for b in order[:nseq])} cached tokens), oracle "
-                      f"gather + flash_decode chunk 64, {spent:.1f} s",
-            "seq_per_s": nseq / spent}
+    t1 = time.perf_counter() - t0
+    v1 = decode_bytes_of(lens[:done], done) / t1 / 1e9
+    threads = max(1, min(16, os.cpu_count() or 1))
+    with concurrent.futures.ThreadPoolExecutor(threads) as ex:
+        t0 = time.perf_counter()
+        list(ex.map(one, range(batch)))
+        tn = time.perf_counter() - t0
+    vn = decode_bytes_of(lens, batch) / tn / 1e9
+    return {"value": vn, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"all {batch} sequences of the final state ({int(np.sum(lens))} cached tokens, "
+                      f"32 q heads each), oracle gather + flash_decode chunk 64 per query head, "
+                      f"{threads} threads over sequences: {tn:.2f} s; one thread: {done} sequences "
+                      f"in {t1:.2f} s",
+            "value_1core": v1, "seq_per_s": batch / tn}
+
+
+def config_decode(torch, name, iters=20):
+    """Decode bandwidth at another BASELINE config's full size (c3 int8, c4
+    fp8, c5 bf16): pool filled by the append kernel, then `iters` timed
+    decode calls.  Reported beside the c2 line, not as `value`."""
+    import numpy as np
+
+    import airkv
+    from airkv import workloads
+    cfg = workloads.CONFIGS[name]
+    lens0 = {"c3": lambda: [8192] * cfg.batch, "c4": lambda: workloads.c4_lengths(cfg.batch),
+             "c5": lambda: workloads.c5_lengths(cfg.batch)}[name]()
+    w = workloads.build_prefill_decode(cfg, lens0, seed=3, decode_steps=1)
+    pool = airkv.KvPool(w.num_blocks, cfg.block_size, cfg.n_kv_heads, cfg.head_dim, cfg.dtype)
+    outl = workloads.outlier_channels(cfg.n_kv_heads, cfg.head_dim, seed=3) if name == "c3" else None
+    gen = workloads.kv_rows(10 ** 12, cfg.n_kv_heads, cfg.head_dim, seed=5, device="cuda",
+                            chunk_rows=32768, outliers=outl)
+    for slots in w.batches:
+        st = torch.from_numpy(slots).cuda()
+        done = 0
+        while done < len(slots):
+            k, v = next(gen)
+            n = min(len(slots) - done, k.shape[0])
+            pool.append(k[:n].contiguous(), v[:n].contiguous(), st[done:done + n].contiguous())
+            done += n
+    tables, lens = w.tables()
+    tt, lt = torch.from_numpy(tables).cuda(), torch.from_numpy(lens).cuda()
+    q = torch.randn(cfg.batch, cfg.n_q_heads, cfg.head_dim, device="cuda").to(torch.bfloat16)
+    out = torch.empty_like(q)
+    ws = pool.new_workspace(cfg.n_q_heads, cfg.batch, tables.shape[1], cfg.max_splits)
+    fn = pool.bind_decode(q, tt, lt, out, ws, max_splits=cfg.max_splits)
+    fn()
+    ms = timed_loop(torch, fn, iters)
+    eb = {airkv.BF16: 2, airkv.INT8: 1, airkv.FP8: 1}[cfg.dtype]
+    per_tok = cfg.n_kv_heads * cfg.head_dim * 2 * eb
+    if cfg.dtype in (airkv.INT8, airkv.FP8):
+        per_tok += cfg.n_kv_heads * (cfg.head_dim // cfg.scale_group) * 4 * 2
+    tok = int(lens.astype(np.int64).sum())
+    pages = int(((lens + cfg.block_size - 1) // cfg.block_size).sum())
+    nbytes = tok * per_tok + 4 * pages + cfg.batch * cfg.n_q_heads * cfg.head_dim * 4
+    assert pool.error_count() == 0
+    res = {"decode_gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "decode_us": round(ms * 1e3, 1),
+           "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4), "cached_tokens": tok,
+           "batch": cfg.batch, "kv_dtype": {airkv.BF16: "bf16", airkv.INT8: "int8", airkv.FP8: "fp8"}[cfg.dtype],
+           "block_size": cfg.block_size, "n_q_heads": cfg.n_q_heads}
+    pool.close()
+    return res
 
 
 def main():
@@ -220,10 +281,20 @@ def main():
         extra["gather_us"] = round(ms_g * 1e3, 1)
         del gk, gv
         # large append: 32768 prefill-like tokens (rewrites existing slots)
-        big = np.concatenate(w.batches[:n_prefill])[:32768]
-        bk = torch.randn(len(big), cfg.n_kv_heads, cfg.head_dim, device=dev)
-        bv = torch.randn_like(bk)
-        big_app = pool.bind_append(bk, bv, torch.from_numpy(big).to(dev))
+        # (two source / slot sets used alternately: 2 x 268 MB of f32 rows
+        # exceed the 256 MB MALL, so no launch reads a cached source)
+        allslots = np.concatenate(w.batches[:n_prefill])
+        sets = []
+        for j in range(2):
+            big = allslots[j * 32768:(j + 1) * 32768]
+            bk = torch.randn(len(big), cfg.n_kv_heads, cfg.head_dim, device=dev)
+            bv = torch.randn_like(bk)
+            sets.append(pool.bind_append(bk, bv, torch.from_numpy(big).to(dev)))
+        flip = [0]
+
+        def big_app():
+            sets[flip[0]]()
+            flip[0] ^= 1
         ms_a = timed_loop(torch, big_app, 20)
         a_bytes = len(big) * cfg.n_kv_heads * cfg.head_dim * 2 * (4 + 2) + 8 * len(big)
         extra["append_gbps"] = round(a_bytes / (ms_a * 1e-3) / 1e9, 1)
@@ -245,11 +316,24 @@ def main():
     del src, dst
     log(f"torch copy {extra['copy_gbps']} GB/s")
 
+    if not args.no_configs and not args.only_decode:
+        extra["other_configs"] = {}
+        for name in ("c3", "c4", "c5"):
+            extra["other_configs"][name] = config_decode(torch, name)
+            log(f"{name} decode {extra['other_configs'][name]}")
+
     cpu = None
     if not args.no_cpu:
         q_last = step_q[-1].float().cpu().numpy()
-        cpu = cpu_baseline(pool, w, tables_np, np.array(lens0) + n_steps, q_last, args.cpu_seconds)
-        log(f"cpu oracle {cpu['value']:.3f} GB/s over {cpu['sample']}")
+        lens_final = (np.array(lens0) + n_steps).astype(np.int32)
+
+        def bytes_of(lens, nseq):
+            lens = np.asarray(lens, np.int64)
+            return (int(lens.sum()) * kv_b + 4 * int(((lens + bs - 1) // bs).sum())
+                    + nseq * cfg.n_q_heads * cfg.head_dim * (2 + 2))
+        cpu = cpu_baseline(pool, w, tables_np, lens_final, q_last, args.cpu_seconds, bytes_of)
+        log(f"cpu oracle {cpu['value']:.3f} GB/s ({cpu['cores']} threads), "
+            f"{cpu['value_1core']:.3f} GB/s (1 thread)")
 
     result = {
         "metric": "paged decode attn HBM GB/s (% of peak); KV append+gather GB/s, 1 MI355X",
