@@ -11,7 +11,7 @@ from ._lib import (AIR_KV_E_HIP, AIR_KV_E_INVALID_ARG, AIR_KV_E_NOT_FOUND, AIR_K
 from .kv_swap import KvSwapManager, pool_callbacks
 from .paged_attention import (BLOCK_SIZE, MAX_BLOCKS, BlockAllocator, BlockTable,
                               SequenceManager, num_blocks_for_tokens)
-from .pool import KvPool
+from .pool import KvPool, wire_int8_quantize
 from .session import PagedSessionCache
 
 __all__ = [
@@ -19,5 +19,5 @@ __all__ = [
     "AIR_KV_E_STATE", "F32", "BF16", "INT8", "FP8", "LAYOUT_HEAD_MAJOR", "LAYOUT_TOKEN_MAJOR",
     "LIB_PATH", "SIGNATURES", "AirKvError", "last_error", "load", "KvSwapManager",
     "pool_callbacks", "BLOCK_SIZE", "MAX_BLOCKS", "BlockAllocator", "BlockTable",
-    "SequenceManager", "num_blocks_for_tokens", "KvPool", "PagedSessionCache",
+    "SequenceManager", "num_blocks_for_tokens", "KvPool", "PagedSessionCache", "wire_int8_quantize",
 ]

@@ -111,6 +111,11 @@ SIGNATURES = {
     "air_kv_session_clear": (_int, [_P]),
     "air_kv_session_truncate_to": (_int, [_P, _i64]),
     "air_kv_session_memory_usage": (_int, [_P, ctypes.POINTER(_SZ)]),
+    "air_kv_block_wire_bytes": (_int, [_P, ctypes.POINTER(_SZ)]),
+    "air_kv_pack_blocks": (_int, [_P, _P, _P, _i32, _P]),
+    "air_kv_unpack_blocks": (_int, [_P, _P, _P, _i32, _P]),
+    "air_kv_wire_int8_quantize": (_int, [_P, _P, _i32, _SZ, _P, _P]),
+    "air_kv_pack_blocks_int8": (_int, [_P, _P, _P, _i32, _P, _P]),
     "air_kv_copy_blocks": (_int, [_P, _P, _P, _P, _i32]),
     "air_kv_read_blocks": (_int, [_P, _P, _pi32, _i32, _P]),
     "air_kv_write_blocks": (_int, [_P, _P, _pi32, _i32, _P]),

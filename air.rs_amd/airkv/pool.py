@@ -246,6 +246,51 @@ class KvPool:
             ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), len(ids),
             data.ctypes.data_as(ctypes.c_void_p)), "air_kv_write_blocks")
 
+    # ---- KvBlock wire format (src/pd_disagg.rs:39-83) ----------------------
+
+    @property
+    def wire_bytes(self):
+        out = ctypes.c_size_t()
+        _lib.check(_lib.load().air_kv_block_wire_bytes(self.handle, ctypes.byref(out)))
+        return out.value
+
+    def pack_blocks(self, ids, out=None, stream=None):
+        """Wire data of blocks `ids` (int32 device tensor) as a uint8 device
+        tensor [n, wire_bytes]: bf16 [block_size][n_kv_heads][head_dim][K|V]."""
+        torch = _torch()
+        _dev(ids, torch.int32, "ids")
+        n = ids.numel()
+        if out is None:
+            out = torch.empty(n, self.wire_bytes, dtype=torch.uint8, device="cuda")
+        _dev(out, torch.uint8, "out", (n, self.wire_bytes))
+        _lib.check(_lib.load().air_kv_pack_blocks(self.handle, _stream_ptr(stream),
+                                                  ctypes.c_void_p(ids.data_ptr()), n,
+                                                  ctypes.c_void_p(out.data_ptr())), "air_kv_pack_blocks")
+        return out
+
+    def unpack_blocks(self, ids, wire, stream=None):
+        torch = _torch()
+        _dev(ids, torch.int32, "ids")
+        n = ids.numel()
+        _dev(wire, torch.uint8, "wire", (n, self.wire_bytes))
+        _lib.check(_lib.load().air_kv_unpack_blocks(self.handle, _stream_ptr(stream),
+                                                    ctypes.c_void_p(ids.data_ptr()), n,
+                                                    ctypes.c_void_p(wire.data_ptr())), "air_kv_unpack_blocks")
+
+    def pack_blocks_int8(self, ids, stream=None):
+        """(codes int8 [n, wire_bytes / 2], scales f32 [n]) device tensors."""
+        torch = _torch()
+        _dev(ids, torch.int32, "ids")
+        n = ids.numel()
+        codes = torch.empty(n, self.wire_bytes // 2, dtype=torch.int8, device="cuda")
+        scales = torch.empty(n, dtype=torch.float32, device="cuda")
+        _lib.check(_lib.load().air_kv_pack_blocks_int8(self.handle, _stream_ptr(stream),
+                                                       ctypes.c_void_p(ids.data_ptr()), n,
+                                                       ctypes.c_void_p(codes.data_ptr()),
+                                                       ctypes.c_void_p(scales.data_ptr())),
+                   "air_kv_pack_blocks_int8")
+        return codes, scales
+
     def split_blocks(self, raw):
         """Split read_blocks output into (k, v, k_scales, v_scales) arrays in
         the device layout [n][n_kv_heads][block_size][...]."""
@@ -273,3 +318,19 @@ class KvPool:
             self.handle, _stream_ptr(stream) if stream is not None else None, ctypes.byref(out),
             1 if reset else 0))
         return out.value
+
+
+def wire_int8_quantize(wire, stream=None):
+    """KvBlock::int8_quantize of every row of `wire` (uint8 device tensor
+    [n_blocks, bytes] of bf16 data) -> (codes int8 [n_blocks, bytes / 2],
+    scales f32 [n_blocks])."""
+    torch = _torch()
+    _dev(wire, torch.uint8, "wire")
+    n, nbytes = wire.shape
+    codes = torch.empty(n, nbytes // 2, dtype=torch.int8, device="cuda")
+    scales = torch.empty(n, dtype=torch.float32, device="cuda")
+    _lib.check(_lib.load().air_kv_wire_int8_quantize(_stream_ptr(stream), ctypes.c_void_p(wire.data_ptr()), n,
+                                                     nbytes // 2, ctypes.c_void_p(codes.data_ptr()),
+                                                     ctypes.c_void_p(scales.data_ptr())),
+               "air_kv_wire_int8_quantize")
+    return codes, scales

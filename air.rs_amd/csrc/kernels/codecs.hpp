@@ -72,6 +72,18 @@ __device__ __forceinline__ int8_t q8_code(float x, float inv) {
     return (int8_t)(int)r;
 }
 
+// KvBlock::int8_quantize's code (src/pd_disagg.rs:78-80): Rust `f32::round`
+// then a saturating `as i8` with no clamp before it, so an infinite product
+// (1 / scale overflows when the block's absmax is subnormal) gives -128 or
+// 127, and NaN gives 0.
+__device__ __forceinline__ int8_t pd_code(float x, float inv) {
+#pragma clang fp contract(off)
+    float r = roundf(x * inv);
+    if (r != r) return 0;
+    r = r < -128.0f ? -128.0f : (r > 127.0f ? 127.0f : r);
+    return (int8_t)(int)r;
+}
+
 // Q8_0 scale from the group's absmax (src/kv_cache.rs:60-62).
 __device__ __forceinline__ float q8_scale(float max_abs) {
 #pragma clang fp contract(off)

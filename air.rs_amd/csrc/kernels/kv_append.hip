@@ -12,6 +12,7 @@
 
 #include "../pool.hpp"
 #include "codecs.hpp"
+#include "page_io.hpp"
 
 namespace airkv {
 namespace {
@@ -32,60 +33,6 @@ struct AppendArgs {
     float *k_scales, *v_scales;
     unsigned long long *errors;
 };
-
-template <int DT>
-__device__ __forceinline__ void store_row_chunk(const float (&x)[8], void *pages, float *scales,
-                                                int64_t elem, int64_t scale_idx, bool lead,
-                                                int lanes_per_group, bool valid) {
-    if constexpr (DT == AIR_KV_F32) {
-        if (valid) {
-            f32x4 *o = reinterpret_cast<f32x4 *>((float *)pages + elem);
-            __builtin_nontemporal_store(f32x4{x[0], x[1], x[2], x[3]}, o);
-            __builtin_nontemporal_store(f32x4{x[4], x[5], x[6], x[7]}, o + 1);
-        }
-    } else if constexpr (DT == AIR_KV_BF16) {
-        if (valid) {
-            u32x4 w;
-            w[0] = (uint32_t)bf16_rne(x[0]) | ((uint32_t)bf16_rne(x[1]) << 16);
-            w[1] = (uint32_t)bf16_rne(x[2]) | ((uint32_t)bf16_rne(x[3]) << 16);
-            w[2] = (uint32_t)bf16_rne(x[4]) | ((uint32_t)bf16_rne(x[5]) << 16);
-            w[3] = (uint32_t)bf16_rne(x[6]) | ((uint32_t)bf16_rne(x[7]) << 16);
-            __builtin_nontemporal_store(w, reinterpret_cast<u32x4 *>((uint16_t *)pages + elem));
-        }
-    } else {
-        // absmax fold from 0.0 with a NaN-ignoring max (src/kv_cache.rs:60,
-        // src/fp8.rs:228-232); max is order independent, so the lane-parallel
-        // reduction equals the reference's sequential fold.
-        float m = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) m = absmax_step(m, x[j]);
-        for (int mask = 1; mask < lanes_per_group; mask <<= 1) m = absmax_step(m, __shfl_xor(m, mask));
-        uint32_t lo = 0, hi = 0;
-        float scale;
-        if constexpr (DT == AIR_KV_INT8) {
-            scale = q8_scale(m);
-            float inv;
-            {
-#pragma clang fp contract(off)
-                inv = 1.0f / scale;
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) lo |= (uint32_t)(uint8_t)q8_code(x[j], inv) << (8 * j);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) hi |= (uint32_t)(uint8_t)q8_code(x[4 + j], inv) << (8 * j);
-        } else {
-            scale = fp8_scale(m);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) lo |= (uint32_t)fp8_code(x[j], scale) << (8 * j);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) hi |= (uint32_t)fp8_code(x[4 + j], scale) << (8 * j);
-        }
-        if (valid) {
-            __builtin_nontemporal_store(u32x2{lo, hi}, reinterpret_cast<u32x2 *>((uint8_t *)pages + elem));
-            if (lead) scales[scale_idx] = scale;
-        }
-    }
-}
 
 template <int DT>
 __global__ __launch_bounds__(kThreads) void kv_append_kernel(AppendArgs a) {

@@ -11,6 +11,11 @@
 
 #include "../pool.hpp"
 #include "codecs.hpp"
+#include "page_io.hpp"
+
+#ifndef AIRKV_GATHER_WGS_PER_CU
+#define AIRKV_GATHER_WGS_PER_CU 8          // build-time tuning knob: resident workgroups per CU
+#endif
 
 namespace airkv {
 namespace {
@@ -34,40 +39,6 @@ struct GatherArgs {
     int32_t layout;
     unsigned long long *errors;
 };
-
-template <int DT>
-__device__ __forceinline__ void load8(const void *pages, const float *scales, int64_t elem,
-                                      int64_t scale_idx, float (&x)[8], u32x4 *raw) {
-    if constexpr (DT == AIR_KV_F32) {
-        const f32x4 *p = reinterpret_cast<const f32x4 *>((const float *)pages + elem);
-        const f32x4 a = __builtin_nontemporal_load(p), b = __builtin_nontemporal_load(p + 1);
-        x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3]; x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
-    } else if constexpr (DT == AIR_KV_BF16) {
-        const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>((const uint16_t *)pages + elem));
-        *raw = w;
-        uint32_t u[4] = {w[0], w[1], w[2], w[3]};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            x[2 * j] = __uint_as_float(u[j] << 16);
-            x[2 * j + 1] = __uint_as_float(u[j] & 0xFFFF0000u);
-        }
-    } else {
-        const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>((const uint8_t *)pages + elem));
-        const float s = scales[scale_idx];
-        uint32_t u[2] = {w[0], w[1]};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            uint32_t byte = (u[j >> 2] >> (8 * (j & 3))) & 0xFFu;
-            float val;
-            if constexpr (DT == AIR_KV_INT8) val = (float)(int32_t)(int8_t)byte;
-            else val = fp8_decode(byte);
-            {
-#pragma clang fp contract(off)
-                x[j] = val * s;   // q as f32 * scale (src/kv_cache.rs:88, src/fp8.rs:263-264)
-            }
-        }
-    }
-}
 
 template <int DT, int OUT>
 __device__ __forceinline__ void store8(void *out, int64_t elem, const float (&x)[8], u32x4 raw) {
@@ -204,7 +175,7 @@ hipError_t launch_gather(const air_kv_pool &p, hipStream_t s, const int32_t *tab
         a.out_k = out_k; a.out_v = out_v;
         a.layout = out_layout;
         a.errors = p.errors;
-        dim3 grid((unsigned)(cus * 8));
+        dim3 grid((unsigned)(cus * AIRKV_GATHER_WGS_PER_CU));
         switch (p.desc.dtype) {
         case AIR_KV_F32: dispatch_out<AIR_KV_F32>(out_dtype, grid, s, a); break;
         case AIR_KV_BF16: dispatch_out<AIR_KV_BF16>(out_dtype, grid, s, a); break;

@@ -1,0 +1,115 @@
+// Moving 8 consecutive head_dim elements of one (token, kv head) row between
+// registers (as f32) and a page of any pool dtype: the shared building block
+// of append, gather and the KvBlock wire kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "air_kv.h"
+#include "codecs.hpp"
+
+namespace airkv {
+
+typedef float pio_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t pio_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t pio_u32x2 __attribute__((ext_vector_type(2)));
+
+// Page -> 8 f32 (INT8/FP8 dequantized as q * scale, src/kv_cache.rs:88 and
+// src/fp8.rs:263-264).  For BF16 pages `raw` receives the 16 source bytes so
+// a bf16 destination can copy them without re-rounding.
+template <int DT>
+__device__ __forceinline__ void load8(const void *pages, const float *scales, int64_t elem,
+                                      int64_t scale_idx, float (&x)[8], pio_u32x4 *raw) {
+    if constexpr (DT == AIR_KV_F32) {
+        const pio_f32x4 *p = reinterpret_cast<const pio_f32x4 *>((const float *)pages + elem);
+        const pio_f32x4 a = __builtin_nontemporal_load(p), b = __builtin_nontemporal_load(p + 1);
+        x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3]; x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
+    } else if constexpr (DT == AIR_KV_BF16) {
+        const pio_u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const pio_u32x4 *>((const uint16_t *)pages + elem));
+        *raw = w;
+        uint32_t u[4] = {w[0], w[1], w[2], w[3]};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            x[2 * j] = __uint_as_float(u[j] << 16);
+            x[2 * j + 1] = __uint_as_float(u[j] & 0xFFFF0000u);
+        }
+    } else {
+        const pio_u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const pio_u32x2 *>((const uint8_t *)pages + elem));
+        const float s = scales[scale_idx];
+        uint32_t u[2] = {w[0], w[1]};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t byte = (u[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+            float val;
+            if constexpr (DT == AIR_KV_INT8) val = (float)(int32_t)(int8_t)byte;
+            else val = fp8_decode(byte);
+            {
+#pragma clang fp contract(off)
+                x[j] = val * s;   // q as f32 * scale (src/kv_cache.rs:88, src/fp8.rs:263-264)
+            }
+        }
+    }
+}
+
+
+// 8 f32 -> page: F32 stored as is, BF16 rounded to nearest even, INT8 / FP8
+// quantized with one scale per scale_group elements; the lanes_per_group
+// consecutive lanes holding one group reduce its absmax with butterfly
+// shuffles (every lane of the group must call this), and the `lead` lane
+// stores the scale.  Nothing is stored when `valid` is false.
+template <int DT>
+__device__ __forceinline__ void store_row_chunk(const float (&x)[8], void *pages, float *scales,
+                                                int64_t elem, int64_t scale_idx, bool lead,
+                                                int lanes_per_group, bool valid) {
+    if constexpr (DT == AIR_KV_F32) {
+        if (valid) {
+            pio_f32x4 *o = reinterpret_cast<pio_f32x4 *>((float *)pages + elem);
+            __builtin_nontemporal_store(pio_f32x4{x[0], x[1], x[2], x[3]}, o);
+            __builtin_nontemporal_store(pio_f32x4{x[4], x[5], x[6], x[7]}, o + 1);
+        }
+    } else if constexpr (DT == AIR_KV_BF16) {
+        if (valid) {
+            pio_u32x4 w;
+            w[0] = (uint32_t)bf16_rne(x[0]) | ((uint32_t)bf16_rne(x[1]) << 16);
+            w[1] = (uint32_t)bf16_rne(x[2]) | ((uint32_t)bf16_rne(x[3]) << 16);
+            w[2] = (uint32_t)bf16_rne(x[4]) | ((uint32_t)bf16_rne(x[5]) << 16);
+            w[3] = (uint32_t)bf16_rne(x[6]) | ((uint32_t)bf16_rne(x[7]) << 16);
+            __builtin_nontemporal_store(w, reinterpret_cast<pio_u32x4 *>((uint16_t *)pages + elem));
+        }
+    } else {
+        // absmax fold from 0.0 with a NaN-ignoring max (src/kv_cache.rs:60,
+        // src/fp8.rs:228-232); max is order independent, so the lane-parallel
+        // reduction equals the reference's sequential fold.
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) m = absmax_step(m, x[j]);
+        for (int mask = 1; mask < lanes_per_group; mask <<= 1) m = absmax_step(m, __shfl_xor(m, mask));
+        uint32_t lo = 0, hi = 0;
+        float scale;
+        if constexpr (DT == AIR_KV_INT8) {
+            scale = q8_scale(m);
+            float inv;
+            {
+#pragma clang fp contract(off)
+                inv = 1.0f / scale;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) lo |= (uint32_t)(uint8_t)q8_code(x[j], inv) << (8 * j);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) hi |= (uint32_t)(uint8_t)q8_code(x[4 + j], inv) << (8 * j);
+        } else {
+            scale = fp8_scale(m);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) lo |= (uint32_t)fp8_code(x[j], scale) << (8 * j);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) hi |= (uint32_t)fp8_code(x[4 + j], scale) << (8 * j);
+        }
+        if (valid) {
+            __builtin_nontemporal_store(pio_u32x2{lo, hi}, reinterpret_cast<pio_u32x2 *>((uint8_t *)pages + elem));
+            if (lead) scales[scale_idx] = scale;
+        }
+    }
+}
+
+}  // namespace airkv

@@ -180,6 +180,51 @@ int air_kv_copy_blocks(air_kv_pool *p, void *stream, const int32_t *src, const i
     return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "air_kv_copy_blocks launch");
 }
 
+int air_kv_block_wire_bytes(const air_kv_pool *p, size_t *bytes) {
+    if (!p || !bytes) return fail(AIR_KV_E_INVALID_ARG, "pool or bytes is NULL");
+    *bytes = airkv::wire_block_bytes(*p);
+    return AIR_KV_OK;
+}
+
+int air_kv_pack_blocks(air_kv_pool *p, void *stream, const int32_t *ids, int32_t n, void *out) {
+    if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
+    if (n < 0) return fail(AIR_KV_E_INVALID_ARG, "n < 0");
+    if (n == 0) return AIR_KV_OK;
+    if (!ids || !out) return fail(AIR_KV_E_INVALID_ARG, "NULL ids or out");
+    hipError_t e = airkv::launch_pack_blocks(*p, (hipStream_t)stream, ids, n, out);
+    return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "air_kv_pack_blocks launch");
+}
+
+int air_kv_pack_blocks_int8(air_kv_pool *p, void *stream, const int32_t *ids, int32_t n,
+                            int8_t *codes, float *scales) {
+    if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
+    if (n < 0) return fail(AIR_KV_E_INVALID_ARG, "n < 0");
+    if (n == 0) return AIR_KV_OK;
+    if (!ids || !codes || !scales) return fail(AIR_KV_E_INVALID_ARG, "NULL ids, codes or scales");
+    hipError_t e = airkv::launch_pack_blocks_int8(*p, (hipStream_t)stream, ids, n, codes, scales);
+    return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "air_kv_pack_blocks_int8 launch");
+}
+
+int air_kv_unpack_blocks(air_kv_pool *p, void *stream, const int32_t *ids, int32_t n, const void *in) {
+    if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
+    if (n < 0) return fail(AIR_KV_E_INVALID_ARG, "n < 0");
+    if (n == 0) return AIR_KV_OK;
+    if (!ids || !in) return fail(AIR_KV_E_INVALID_ARG, "NULL ids or in");
+    hipError_t e = airkv::launch_unpack_blocks(*p, (hipStream_t)stream, ids, n, in);
+    return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "air_kv_unpack_blocks launch");
+}
+
+int air_kv_wire_int8_quantize(void *stream, const void *wire, int32_t n_blocks, size_t elems_per_block,
+                              int8_t *codes, float *scales) {
+    if (n_blocks < 0) return fail(AIR_KV_E_INVALID_ARG, "n_blocks < 0");
+    if (n_blocks == 0 || elems_per_block == 0) return AIR_KV_OK;
+    if (!wire || !codes || !scales) return fail(AIR_KV_E_INVALID_ARG, "NULL wire, codes or scales");
+    if (elems_per_block > (size_t)INT64_MAX / 2) return fail(AIR_KV_E_INVALID_ARG, "block too large");
+    hipError_t e = airkv::launch_wire_int8((hipStream_t)stream, wire, n_blocks, (int64_t)elems_per_block,
+                                           codes, scales);
+    return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "air_kv_wire_int8_quantize launch");
+}
+
 static int check_ids(const air_kv_pool *p, const int32_t *ids, int32_t n) {
     for (int32_t i = 0; i < n; ++i)
         if (ids[i] < 0 || ids[i] >= p->desc.num_blocks)

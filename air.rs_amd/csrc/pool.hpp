@@ -56,5 +56,14 @@ hipError_t launch_decode(const air_kv_pool &pool, hipStream_t s, const DecodePla
                          void *workspace, void *out, int32_t out_dtype);
 hipError_t launch_copy_blocks(const air_kv_pool &pool, hipStream_t s, const int32_t *src,
                               const int32_t *dst, int32_t n);
+size_t wire_block_bytes(const air_kv_pool &pool);
+hipError_t launch_pack_blocks(const air_kv_pool &pool, hipStream_t s, const int32_t *ids, int32_t n,
+                              void *out);
+hipError_t launch_pack_blocks_int8(const air_kv_pool &pool, hipStream_t s, const int32_t *ids,
+                                   int32_t n, int8_t *codes, float *scales);
+hipError_t launch_unpack_blocks(const air_kv_pool &pool, hipStream_t s, const int32_t *ids, int32_t n,
+                                const void *in);
+hipError_t launch_wire_int8(hipStream_t s, const void *wire, int32_t n_blocks, int64_t elems,
+                            int8_t *codes, float *scales);
 
 }  // namespace airkv

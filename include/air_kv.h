@@ -301,6 +301,36 @@ int air_kv_session_truncate_to(air_kv_session *s, int64_t pos);
  * (the paged form of memory_usage, src/kv_cache.rs:388-414). */
 int air_kv_session_memory_usage(const air_kv_session *s, size_t *bytes);
 
+/* ------------------------------------------------------------------------ */
+/* KvBlock wire format (prefill/decode disaggregation)                        */
+/* ------------------------------------------------------------------------ */
+
+/* Bytes of one KvBlock's data (src/pd_disagg.rs:39-49): bf16
+ * [block_size][n_kv_heads][head_dim][2], K at index 0 and V at 1 of the last
+ * axis: 4 * block_size * n_kv_heads * head_dim. */
+int air_kv_block_wire_bytes(const air_kv_pool *pool, size_t *bytes);
+/* Writes the wire data of blocks ids[i] (int32, device) to out + i * wire
+ * bytes (device).  bf16 pools copy their bits, f32 pools round to nearest
+ * even, int8 / fp8 pools dequantize (q * scale) then round.  Ids outside the
+ * pool leave their slot untouched and are counted (air_kv_pool_error_count). */
+int air_kv_pack_blocks(air_kv_pool *pool, void *stream, const int32_t *ids, int32_t n, void *out);
+/* The inverse: wire data (device) into blocks ids[i].  bf16 pools take the
+ * bits, f32 pools widen exactly, int8 / fp8 pools quantize each scale group
+ * of every row exactly as air_kv_append does. */
+int air_kv_unpack_blocks(air_kv_pool *pool, void *stream, const int32_t *ids, int32_t n,
+                         const void *in);
+/* KvBlock::int8_quantize (src/pd_disagg.rs:65-83) of n_blocks wire blocks of
+ * elems_per_block bf16 elements each (device): one f32 scale per block
+ * (absmax / 127, NaN ignored, 1.0 for an all-zero block) and int8 codes
+ * round(x * (1 / scale)) in wire order.  Bit-exact with the reference. */
+int air_kv_wire_int8_quantize(void *stream, const void *wire, int32_t n_blocks,
+                              size_t elems_per_block, int8_t *codes, float *scales);
+/* air_kv_pack_blocks followed by air_kv_wire_int8_quantize in one pass over
+ * the pages (the TcpKvConnector send path, src/pd_disagg.rs:267-275):
+ * codes + i * wire_bytes / 2 and scales[i] for block ids[i]. */
+int air_kv_pack_blocks_int8(air_kv_pool *pool, void *stream, const int32_t *ids, int32_t n,
+                            int8_t *codes, float *scales);
+
 /* Copies whole blocks src[i] -> dst[i] (int32, device): the page copy that
  * BlockAllocator::cow_write leaves to "a real impl" (src/paged_attention.rs:160). */
 int air_kv_copy_blocks(air_kv_pool *pool, void *stream, const int32_t *src_blocks,

@@ -1,0 +1,156 @@
+"""GPU parity of the KvBlock wire kernels (src/pd_disagg.rs:39-83): pack,
+unpack and the int8 transfer quantization, bit-exact against the oracle.
+
+pack: every wire element is bf16_from_f32 of the page element as f32 (bf16
+pages copy their bits; int8 / fp8 pages dequantize q * scale first), laid
+out [block_size][n_kv_heads][head_dim][K|V].  int8: KvBlock::int8_quantize of
+that wire block (oracle.pd_int8_quantize, pinned on the CPU).  unpack: the
+pages that the oracle's append writes for the wire values at the block's
+slots.
+"""
+import numpy as np
+import pytest
+
+import airkv
+import oracle
+from gpu_helpers import assert_bits_equal, log, torch_mod
+
+pytestmark = pytest.mark.gpu
+
+BS, NKV, D = 16, 8, 128
+
+
+def _filled_pool(dtype, nb=24, seed=0):
+    torch = torch_mod()
+    pool = airkv.KvPool(nb, BS, NKV, D, dtype)
+    rng = np.random.default_rng(seed)
+    k = (rng.standard_normal((nb * BS, NKV, D)) * rng.uniform(0.1, 5.0)).astype(np.float32)
+    v = (rng.standard_normal((nb * BS, NKV, D)) * rng.uniform(0.1, 5.0)).astype(np.float32)
+    slots = np.arange(nb * BS, dtype=np.int64)
+    pool.append(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(), torch.from_numpy(slots).cuda())
+    return pool
+
+
+def _page_values(pool, ids):
+    """f32 values of the pages of `ids`, [n][NKV][BS][D] for K and V."""
+    k, v, ks, vs = pool.split_blocks(pool.read_blocks(ids))
+    if pool.dtype == airkv.F32:
+        return k, v
+    if pool.dtype == airkv.BF16:
+        return (oracle.bf16_to_f32(k.reshape(-1)).reshape(k.shape),
+                oracle.bf16_to_f32(v.reshape(-1)).reshape(v.shape))
+    g = pool.scale_group
+
+    def deq(c, s):
+        if pool.dtype == airkv.INT8:
+            x = c.astype(np.int8).astype(np.float32)
+        else:
+            x = oracle.fp8_to_f32(c.reshape(-1)).reshape(c.shape)
+        return (x.reshape(*c.shape[:3], D // g, g) * s[..., None]).astype(np.float32).reshape(c.shape)
+    return deq(k, ks), deq(v, vs)
+
+
+def _expected_wire(pool, ids):
+    k, v = _page_values(pool, ids)                               # [n][h][t][d]
+    kv = np.stack([k.transpose(0, 2, 1, 3), v.transpose(0, 2, 1, 3)], axis=-1)   # [n][t][h][d][2]
+    return oracle.bf16_from_f32(kv.reshape(-1)).reshape(len(ids), -1)
+
+
+@pytest.mark.parametrize("dtype", [airkv.F32, airkv.BF16, airkv.INT8, airkv.FP8])
+def test_pack_blocks_bitexact(dtype):
+    torch = torch_mod()
+    pool = _filled_pool(dtype, seed=int(dtype))
+    ids = np.array([5, 0, 23, 11, 11, 7], np.int32)
+    wire = pool.pack_blocks(torch.from_numpy(ids).cuda())
+    torch.cuda.synchronize()
+    assert pool.wire_bytes == 4 * BS * NKV * D
+    got = wire.cpu().numpy().view(np.uint16).reshape(len(ids), -1)
+    assert_bits_equal(got, _expected_wire(pool, ids), f"pack dtype={dtype}")
+
+
+@pytest.mark.parametrize("dtype", [airkv.F32, airkv.BF16, airkv.INT8, airkv.FP8])
+def test_pack_blocks_int8_bitexact(dtype):
+    """Fused pack + KvBlock::int8_quantize equals the oracle's int8_quantize
+    of the packed wire block: codes and scale."""
+    torch = torch_mod()
+    pool = _filled_pool(dtype, seed=10 + int(dtype))
+    ids = np.array([3, 9, 0, 22], np.int32)
+    codes, scales = pool.pack_blocks_int8(torch.from_numpy(ids).cuda())
+    torch.cuda.synchronize()
+    want_wire = _expected_wire(pool, ids)
+    for i in range(len(ids)):
+        want_q, want_s = oracle.pd_int8_quantize(want_wire[i])
+        assert np.float32(scales[i].item()).view(np.uint32) == np.float32(want_s).view(np.uint32)
+        assert np.array_equal(codes[i].cpu().numpy(), want_q)
+
+
+def test_wire_int8_quantize_special_blocks():
+    """Whole wire buffers with the edge cases of the reference arithmetic:
+    an all-zero block (scale 1.0, codes 0), NaN elements (ignored by the
+    absmax, code 0), infinities (scale inf), subnormal maxima (1/scale
+    overflows), values at exact .5 ties of x * inv, and random blocks."""
+    torch = torch_mod()
+    n, e = 7, 4096
+    rng = np.random.default_rng(5)
+    f = (rng.standard_normal((n, e)) * 3).astype(np.float32)
+    f[0] = 0.0
+    f[1, ::97] = np.nan
+    f[2, 17] = np.inf
+    f[3] = f[3] * np.float32(1e-40)                  # subnormal range
+    f[4] = np.float32(127.0) * np.linspace(-1, 1, e, dtype=np.float32)   # ties after * inv
+    bits = oracle.bf16_from_f32(f.reshape(-1)).reshape(n, e)
+    wire = torch.from_numpy(bits.view(np.uint8).copy()).cuda()
+    codes, scales = airkv.wire_int8_quantize(wire)
+    torch.cuda.synchronize()
+    for i in range(n):
+        want_q, want_s = oracle.pd_int8_quantize(bits[i])
+        got_s = np.float32(scales[i].item())
+        assert got_s.view(np.uint32) == np.float32(want_s).view(np.uint32), i
+        assert np.array_equal(codes[i].cpu().numpy(), want_q), i
+    assert scales[0].item() == 1.0 and int(codes[0].abs().max()) == 0
+
+
+@pytest.mark.parametrize("dtype", [airkv.F32, airkv.BF16, airkv.INT8, airkv.FP8])
+def test_unpack_blocks_matches_oracle_append(dtype):
+    """unpack writes the pages the oracle's append writes for the wire
+    values (as f32) at the block's slots; other blocks stay untouched."""
+    torch = torch_mod()
+    nb = 12
+    pool = airkv.KvPool(nb, BS, NKV, D, dtype)
+    host = oracle.HostPool(nb, BS, NKV, D, dtype)
+    ids = np.array([4, 10, 0], np.int32)
+    rng = np.random.default_rng(20 + int(dtype))
+    vals = (rng.standard_normal((len(ids), BS, NKV, D, 2)) * 2).astype(np.float32)
+    wire_bits = oracle.bf16_from_f32(vals.reshape(-1)).reshape(len(ids), -1)
+    pool.unpack_blocks(torch.from_numpy(ids).cuda(),
+                       torch.from_numpy(wire_bits.view(np.uint8).reshape(len(ids), -1).copy()).cuda())
+    torch.cuda.synchronize()
+    wf = oracle.bf16_to_f32(wire_bits.reshape(-1)).reshape(len(ids), BS, NKV, D, 2)
+    k = wf[..., 0].reshape(-1, NKV, D)
+    v = wf[..., 1].reshape(-1, NKV, D)
+    slots = (ids[:, None].astype(np.int64) * BS + np.arange(BS)[None, :]).reshape(-1)
+    assert host.append(k, v, slots) == 0
+    gk, gv, gks, gvs = pool.snapshot()
+    assert_bits_equal(gk, host.k, "unpack K pages")
+    assert_bits_equal(gv, host.v, "unpack V pages")
+    if host.k_scales is not None:
+        assert_bits_equal(gks, host.k_scales, "unpack K scales")
+        assert_bits_equal(gvs, host.v_scales, "unpack V scales")
+
+
+def test_bf16_roundtrip_and_bad_ids():
+    """bf16 pools: pack then unpack into other blocks reproduces the pages
+    bit for bit; ids outside the pool are skipped and counted."""
+    torch = torch_mod()
+    pool = _filled_pool(airkv.BF16, nb=16, seed=3)
+    src = torch.tensor([1, 2, 3], dtype=torch.int32, device="cuda")
+    dst = torch.tensor([13, 14, 15], dtype=torch.int32, device="cuda")
+    pool.unpack_blocks(dst, pool.pack_blocks(src))
+    k, v, _, _ = pool.snapshot()
+    assert np.array_equal(k[[13, 14, 15]], k[[1, 2, 3]]) and np.array_equal(v[[13, 14, 15]], v[[1, 2, 3]])
+    pool.error_count(reset=True)
+    out = pool.pack_blocks(torch.tensor([0, 99, -1], dtype=torch.int32, device="cuda"))
+    pool.unpack_blocks(torch.tensor([77], dtype=torch.int32, device="cuda"), out[:1].contiguous())
+    torch.cuda.synchronize()
+    assert pool.error_count() == 3
+    log("wire bad ids counted")

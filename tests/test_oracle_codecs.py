@@ -320,6 +320,17 @@ def test_pd_int8_quantize_whole_buffer():
     assert s == 1.0 and not q.any()
 
 
+def test_pd_int8_quantize_saturates_like_rust_cast():
+    """With a subnormal block maximum, 1/scale overflows to +inf and every
+    nonzero product is +-inf: Rust's saturating `as i8` gives 127 / -128 (no
+    clamp to +-127 as in Q8_0), zero gives NaN and so 0."""
+    x = np.array([3e-40, -3e-40, 1e-40, -2e-40, 0.0], np.float32)
+    bits = oracle.bf16_from_f32(x)
+    q, s = oracle.pd_int8_quantize(bits)
+    assert np.isinf(np.float32(1.0) / s)
+    assert q.tolist() == [127, -128, 127, -128, 0]
+
+
 # ---------------------------------------------------------------------------
 # generators
 # ---------------------------------------------------------------------------
