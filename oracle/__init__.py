@@ -73,6 +73,10 @@ def lib():
                 "orc_reference_attention_f64": (None, [_P, _P, _P, _i32, _i32, _f64, _P]),
                 "orc_paged_decode": (_i32, [_i32, _i32, _i32, _i32, _i32, _i64, _P, _P, _P, _P,
                                             _P, _i32, _P, _P, _i32, _i32, _f32, _i32, _P]),
+                "orc_blockwise_attention_head": (None, [_P, _P, _P, _i32, _i32, _i32, _f32, _i32,
+                                                        _i32, _i32, _P]),
+                "orc_paged_prefill": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _i64, _P, _P, _P, _P,
+                                             _P, _i32, _P, _P, _P, _i32, _i32, _f32, _i32, _P]),
                 "orc_key_compress": (None, [_P, _SZ, _P, _P, _P]),
                 "orc_key_decompress": (None, [_P, _f32, _f32, _SZ, _P]),
                 "orc_value_compress": (None, [_P, _SZ, _P, _P, _P]),
@@ -239,6 +243,27 @@ class HostPool:
                                   out_dtype, out_layout)
         return ok, ov, offs, bad
 
+    def paged_prefill(self, q, cu_q, block_tables, seq_lens, scale=None, kv_block=512):
+        """Causal attention of each sequence's newest cu_q[b+1] - cu_q[b]
+        tokens over its pages (blockwise_attention_head with q_offset =
+        seq_len - q_len).  q: [total_q][n_q][d] f32."""
+        q = _c(q, np.float32)
+        total, n_q, d = q.shape
+        tables = _c(block_tables, np.int32)
+        lens = _c(seq_lens, np.int32)
+        cu = _c(cu_q, np.int32)
+        if scale is None:
+            scale = np.float32(1.0) / np.sqrt(np.float32(d))
+        out = np.empty_like(q)
+        rc = lib().orc_paged_prefill(self.dtype, self.block_size, self.n_kv_heads, self.head_dim,
+                                     self.group, n_q // self.n_kv_heads, self.num_blocks, _ptr(self.k),
+                                     _ptr(self.v), _ptr(self.k_scales), _ptr(self.v_scales), _ptr(q), n_q,
+                                     _ptr(cu), _ptr(tables), _ptr(lens), len(lens), tables.shape[1],
+                                     float(scale), kv_block, _ptr(out))
+        if rc:
+            raise ValueError("oracle paged_prefill rejected its inputs")
+        return out
+
     def paged_decode(self, q, block_tables, seq_lens, scale=None, chunk=64):
         q = _c(q, np.float32)
         batch, n_q, d = q.shape
@@ -376,3 +401,15 @@ def qjl_compress(key, proj, proj_dim):
 
 def qjl_cos_sim(a, b, proj_dim):
     return np.float32(lib().orc_qjl_cos_sim(_ptr(_c(a, np.uint64)), _ptr(_c(b, np.uint64)), proj_dim))
+
+
+# --------------------------------------------------------------------------
+# blockwise causal attention (src/chunked_attn.rs)
+# --------------------------------------------------------------------------
+
+def blockwise_attention_head(q, k, v, seq_q, seq_kv, head_dim, scale, block_size, causal, q_offset):
+    q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    out = np.empty(seq_q * head_dim, np.float32)
+    lib().orc_blockwise_attention_head(_ptr(q), _ptr(k), _ptr(v), seq_q, seq_kv, head_dim, float(scale),
+                                       block_size, 1 if causal else 0, q_offset, _ptr(out))
+    return out

@@ -597,3 +597,116 @@ float orc_qjl_cos_sim(const uint64_t *a, const uint64_t *b, size_t proj_dim) {
     const float angle = 3.14159265358979323846f * (float)ham / (float)proj_dim;
     return cosf(angle);
 }
+
+/* ------------------------------------------------------------------------ */
+/* Blockwise (chunked, causal) attention (src/chunked_attn.rs)               */
+/* ------------------------------------------------------------------------ */
+
+/* blockwise_attention_head (src/chunked_attn.rs:114-213) for one head:
+ * q [seq_q][d], k / v [seq_kv][d]; query qi sits at absolute position
+ * q_offset + qi and, when causal, sees keys 0..=that position.  Per KV block
+ * of block_size keys: scores (left-folded dot product, then * scale), block
+ * max, running-max update (exp(m_old - m_new) rescale of acc and l), block
+ * probabilities exp(s - m_new) summed left to right, acc += p * v row by row;
+ * finally acc / max(l, 1e-8).  Each f32 operation rounds once, in the
+ * reference's order (the libm expf is glibc's, which Rust's f32::exp calls
+ * on Linux). */
+void orc_blockwise_attention_head(const float *q, const float *k, const float *v, int seq_q,
+                                  int seq_kv, int head_dim, float scale, int block_size,
+                                  int causal, int q_offset, float *out) {
+    float *l = (float *)malloc(sizeof(float) * (size_t)(seq_q > 0 ? seq_q : 1));
+    float *m = (float *)malloc(sizeof(float) * (size_t)(seq_q > 0 ? seq_q : 1));
+    int bs = block_size < seq_kv ? block_size : seq_kv;
+    if (bs < 1) bs = 1;
+    float *s_row = (float *)malloc(sizeof(float) * (size_t)bs);
+    float *p_row = (float *)malloc(sizeof(float) * (size_t)bs);
+    for (int i = 0; i < seq_q; ++i) {
+        l[i] = 0.0f;
+        m[i] = -INFINITY;
+        for (int j = 0; j < head_dim; ++j) out[(size_t)i * head_dim + j] = 0.0f;
+    }
+    const int n_blocks = (seq_kv + bs - 1) / bs;
+    for (int kb = 0; kb < n_blocks; ++kb) {
+        const int ks = kb * bs;
+        const int ke = ks + bs < seq_kv ? ks + bs : seq_kv;
+        const int blk = ke - ks;
+        for (int qi = 0; qi < seq_q; ++qi) {
+            const int qpos = q_offset + qi;
+            const float *qr = q + (size_t)qi * head_dim;
+            for (int kj = 0; kj < blk; ++kj) {
+                if (causal && ks + kj > qpos) { s_row[kj] = -INFINITY; continue; }
+                const float *kr = k + (size_t)(ks + kj) * head_dim;
+                float dot = -0.0f;
+                for (int j = 0; j < head_dim; ++j) { const float p = qr[j] * kr[j]; dot += p; }
+                s_row[kj] = dot * scale;
+            }
+            float mb = -INFINITY;
+            for (int kj = 0; kj < blk; ++kj) mb = rust_max(mb, s_row[kj]);
+            const float m_new = rust_max(m[qi], mb);
+            const float e_old = expf(m[qi] - m_new);
+            float *o = out + (size_t)qi * head_dim;
+            for (int j = 0; j < head_dim; ++j) o[j] *= e_old;
+            l[qi] *= e_old;
+            float bl = 0.0f;
+            for (int kj = 0; kj < blk; ++kj) { p_row[kj] = expf(s_row[kj] - m_new); bl += p_row[kj]; }
+            for (int kj = 0; kj < blk; ++kj) {
+                const float *vr = v + (size_t)(ks + kj) * head_dim;
+                for (int j = 0; j < head_dim; ++j) { const float t = p_row[kj] * vr[j]; o[j] += t; }
+            }
+            l[qi] += bl;
+            m[qi] = m_new;
+        }
+    }
+    for (int qi = 0; qi < seq_q; ++qi) {
+        const float den = rust_max(l[qi], 1e-8f);
+        for (int j = 0; j < head_dim; ++j) out[(size_t)qi * head_dim + j] /= den;
+    }
+    free(l); free(m); free(s_row); free(p_row);
+}
+
+/* Paged prefill over a pool (device layout): for each sequence b, its
+ * q_len = cu_q[b+1] - cu_q[b] newest tokens (already in the cache, whose
+ * length is seq_lens[b]) attend causally over all seq_lens[b] tokens, i.e.
+ * blockwise_attention_head with q_offset = seq_lens[b] - q_len, per query
+ * head h on kv head h / group (the mask of src/ops.rs:762-790).  q / out:
+ * [total_q][n_q_heads][head_dim] f32.  Returns 0, or -1 on a bad table entry
+ * or a q_len above seq_len. */
+int orc_paged_prefill(int dtype, int block_size, int n_kv_heads, int head_dim, int scale_group,
+                      int group, int64_t num_blocks, const void *k_pages, const void *v_pages,
+                      const float *k_scales, const float *v_scales, const float *q, int n_q_heads,
+                      const int32_t *cu_q, const int32_t *block_tables, const int32_t *seq_lens,
+                      int batch, int max_blocks, float scale, int kv_block, float *out) {
+    for (int b = 0; b < batch; ++b) {
+        const int len = seq_lens[b], nq = cu_q[b + 1] - cu_q[b];
+        if (len < 0 || len > max_blocks * block_size || nq < 0 || nq > len) return -1;
+        if (nq == 0) continue;
+        for (int t = 0; t < len; ++t) {
+            const int32_t blk = block_tables[(size_t)b * max_blocks + t / block_size];
+            if (blk < 0 || blk >= num_blocks) return -1;
+        }
+        float *kc = (float *)malloc(sizeof(float) * (size_t)len * head_dim);
+        float *vc = (float *)malloc(sizeof(float) * (size_t)len * head_dim);
+        float *qh = (float *)malloc(sizeof(float) * (size_t)nq * head_dim);
+        float *oh = (float *)malloc(sizeof(float) * (size_t)nq * head_dim);
+        for (int h = 0; h < n_q_heads; ++h) {
+            const int kvh = h / group;
+            for (int t = 0; t < len; ++t) {
+                const int32_t blk = block_tables[(size_t)b * max_blocks + t / block_size];
+                const size_t row = ((size_t)blk * n_kv_heads + kvh) * block_size + t % block_size;
+                for (int j = 0; j < head_dim; ++j) {
+                    kc[(size_t)t * head_dim + j] = pool_value(dtype, k_pages, k_scales, head_dim, scale_group, row, j);
+                    vc[(size_t)t * head_dim + j] = pool_value(dtype, v_pages, v_scales, head_dim, scale_group, row, j);
+                }
+            }
+            for (int r = 0; r < nq; ++r)
+                memcpy(qh + (size_t)r * head_dim, q + ((size_t)(cu_q[b] + r) * n_q_heads + h) * head_dim,
+                       sizeof(float) * head_dim);
+            orc_blockwise_attention_head(qh, kc, vc, nq, len, head_dim, scale, kv_block, 1, len - nq, oh);
+            for (int r = 0; r < nq; ++r)
+                memcpy(out + ((size_t)(cu_q[b] + r) * n_q_heads + h) * head_dim, oh + (size_t)r * head_dim,
+                       sizeof(float) * head_dim);
+        }
+        free(kc); free(vc); free(qh); free(oh);
+    }
+    return 0;
+}

@@ -97,6 +97,16 @@ void orc_qjl_compress(const float *key, size_t dim, const float *proj, size_t pr
                       uint64_t *bits, float *magnitude);
 float orc_qjl_cos_sim(const uint64_t *a, const uint64_t *b, size_t proj_dim);
 
+/* ---- blockwise causal attention (src/chunked_attn.rs) --------------------- */
+void orc_blockwise_attention_head(const float *q, const float *k, const float *v, int seq_q,
+                                  int seq_kv, int head_dim, float scale, int block_size,
+                                  int causal, int q_offset, float *out);
+int orc_paged_prefill(int dtype, int block_size, int n_kv_heads, int head_dim, int scale_group,
+                      int group, int64_t num_blocks, const void *k_pages, const void *v_pages,
+                      const float *k_scales, const float *v_scales, const float *q, int n_q_heads,
+                      const int32_t *cu_q, const int32_t *block_tables, const int32_t *seq_lens,
+                      int batch, int max_blocks, float scale, int kv_block, float *out);
+
 #ifdef __cplusplus
 }
 #endif

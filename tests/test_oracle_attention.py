@@ -131,3 +131,101 @@ def test_chunk_normalised_partials_and_merge_weights():
 def test_reduce_rejects_zero_chunks():
     with pytest.raises(ValueError):
         oracle.reduce_chunks(np.zeros((0, 4)), [], [], 4)
+
+
+# ---- blockwise causal attention (src/chunked_attn.rs:114-213) ---------------
+
+def _make_qkv(seq_q, seq_kv, head_dim):
+    """make_qkv of src/chunked_attn.rs tests: sin / cos ramps (f64 then f32)."""
+    q = np.sin(np.arange(seq_q * head_dim, dtype=np.float64) * 0.314).astype(np.float32)
+    k = q.copy()
+    v = (np.cos(np.arange(seq_kv * head_dim, dtype=np.float64) * 0.271).astype(np.float32)
+         * np.float32(0.5))
+    return q, k, v
+
+
+def test_reference_blockwise_shape_finite_and_causal_ones():
+    q, k, v = _make_qkv(4, 4, 4)
+    out = oracle.blockwise_attention_head(q, k, v, 4, 4, 4, 0.5, 2, True, 0)
+    assert out.shape == (16,) and np.all(np.isfinite(out))
+    ones = np.ones(16, np.float32)
+    out = oracle.blockwise_attention_head(ones, ones, ones, 4, 4, 4, 1.0, 2, True, 0)
+    assert np.all(np.abs(out - 1.0) < 1e-4)
+
+
+def test_reference_blockwise_matches_full_for_small_seq():
+    q, k, v = _make_qkv(3, 3, 4)
+    full = oracle.blockwise_attention_head(q, k, v, 3, 3, 4, 1.0, 3, True, 0)
+    chunked = oracle.blockwise_attention_head(q, k, v, 3, 3, 4, 1.0, 1, True, 0)
+    assert np.max(np.abs(full - chunked)) < 1e-4
+
+
+@pytest.mark.parametrize("seq_q,seq_kv,block", [(1, 70, 16), (9, 70, 7), (33, 33, 512), (5, 200, 64)])
+def test_blockwise_rows_are_reference_attention_over_their_prefix(seq_q, seq_kv, block):
+    """Causal with q_offset = seq_kv - seq_q: query row i is the plain softmax
+    attention of that query over keys 0..=q_offset + i (orc_reference_attention,
+    pinned by the flash_decode tests), and a float64 masked softmax agrees."""
+    rng = np.random.default_rng(seq_q * 100 + seq_kv)
+    d = 64
+    q = rng.standard_normal(seq_q * d).astype(np.float32)
+    k = rng.standard_normal(seq_kv * d).astype(np.float32)
+    v = rng.standard_normal(seq_kv * d).astype(np.float32)
+    scale = np.float32(1.0) / np.sqrt(np.float32(d))
+    off = seq_kv - seq_q
+    out = oracle.blockwise_attention_head(q, k, v, seq_q, seq_kv, d, scale, block, True, off).reshape(seq_q, d)
+    Q, K, V = (x.astype(np.float64).reshape(-1, d) for x in (q, k, v))
+    for i in range(seq_q):
+        n = off + i + 1
+        want = oracle.reference_attention(q[i * d:(i + 1) * d], k[:n * d], v[:n * d], n, d, scale)
+        assert np.max(np.abs(out[i] - want)) < 2e-6
+        s = K[:n] @ Q[i] * float(scale)
+        p = np.exp(s - s.max())
+        assert np.max(np.abs(out[i] - (p / p.sum()) @ V[:n])) < 2e-6
+
+
+def test_blockwise_block_size_and_noncausal():
+    rng = np.random.default_rng(9)
+    d, sq, skv = 32, 6, 50
+    q, k, v = (rng.standard_normal(n * d).astype(np.float32) for n in (sq, skv, skv))
+    outs = [oracle.blockwise_attention_head(q, k, v, sq, skv, d, 0.2, b, True, skv - sq) for b in (1, 3, 16, 512)]
+    for o in outs[1:]:
+        assert np.max(np.abs(o - outs[0])) < 1e-5
+    nc = oracle.blockwise_attention_head(q, k, v, sq, skv, d, 0.2, 16, False, 0).reshape(sq, d)
+    for i in range(sq):
+        want = oracle.reference_attention(q[i * d:(i + 1) * d], k, v, skv, d, 0.2)
+        assert np.max(np.abs(nc[i] - want)) < 2e-6
+
+
+def test_paged_prefill_matches_dense_blockwise():
+    """The paged wrapper on a shuffled f32 pool equals the dense function on
+    the gathered K/V, per query head on kv head h // group."""
+    rng = np.random.default_rng(4)
+    bs, nkv, d, group = 16, 2, 32, 2
+    lens = np.array([40, 17, 33], np.int32)
+    qlens = np.array([5, 17, 1], np.int32)
+    nb = 16
+    pool = oracle.HostPool(nb, bs, nkv, d, oracle.F32)
+    perm = rng.permutation(nb).astype(np.int32)
+    tables = np.full((3, 3), -1, np.int32)
+    used = 0
+    dense_k, dense_v = [], []
+    for b, L in enumerate(lens):
+        nblk = -(-L // bs)
+        tables[b, :nblk] = perm[used:used + nblk]
+        used += nblk
+        kk = rng.standard_normal((L, nkv, d)).astype(np.float32)
+        vv = rng.standard_normal((L, nkv, d)).astype(np.float32)
+        slots = np.array([tables[b, t // bs] * bs + t % bs for t in range(L)], np.int64)
+        assert pool.append(kk, vv, slots) == 0
+        dense_k.append(kk)
+        dense_v.append(vv)
+    cu = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
+    q = rng.standard_normal((cu[-1], nkv * group, d)).astype(np.float32)
+    got = pool.paged_prefill(q, cu, tables, lens, scale=0.25, kv_block=8)
+    for b in range(3):
+        for h in range(nkv * group):
+            kh = h // group
+            qh = q[cu[b]:cu[b + 1], h].reshape(-1)
+            want = oracle.blockwise_attention_head(qh, dense_k[b][:, kh].reshape(-1), dense_v[b][:, kh].reshape(-1),
+                                                   qlens[b], lens[b], d, 0.25, 8, True, lens[b] - qlens[b])
+            assert np.array_equal(got[cu[b]:cu[b + 1], h].reshape(-1), want)
