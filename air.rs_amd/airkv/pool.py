@@ -187,6 +187,56 @@ class KvPool:
                 _lib.check(rc, "air_paged_decode")
         return launch
 
+    def _prefill_args(self, q, cu_q, block_tables, seq_lens, out, max_q_len, scale, stream):
+        torch = _torch()
+        total_q, n_q, d = q.shape
+        if d != self.head_dim:
+            raise ValueError("q head_dim differs from the pool")
+        if n_q % self.n_kv_heads:
+            raise ValueError("n_q_heads must be a multiple of n_kv_heads")
+        if q.dtype not in (torch.float32, torch.bfloat16) or out.dtype not in (torch.float32,
+                                                                               torch.bfloat16):
+            raise TypeError("q and out must be float32 or bfloat16")
+        _dev(q, q.dtype, "q")
+        _dev(out, out.dtype, "out", (total_q, n_q, d))
+        _dev(block_tables, torch.int32, "block_tables")
+        batch = block_tables.shape[0]
+        _dev(seq_lens, torch.int32, "seq_lens", (batch,))
+        _dev(cu_q, torch.int32, "cu_q", (batch + 1,))
+        if max_q_len is None:
+            max_q_len = int((cu_q[1:] - cu_q[:-1]).max().item()) if batch else 0
+        if scale is None:
+            scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+        qdt = F32 if q.dtype == torch.float32 else BF16
+        odt = F32 if out.dtype == torch.float32 else BF16
+        return (self.handle, _stream_ptr(stream), ctypes.c_void_p(q.data_ptr()), qdt, n_q,
+                ctypes.c_void_p(cu_q.data_ptr()), total_q, max_q_len,
+                ctypes.c_void_p(block_tables.data_ptr()), ctypes.c_void_p(seq_lens.data_ptr()), batch,
+                block_tables.shape[1], scale, ctypes.c_void_p(out.data_ptr()), odt)
+
+    def paged_prefill(self, q, cu_q, block_tables, seq_lens, out, max_q_len=None, scale=None,
+                      stream=None):
+        """Causal attention of each sequence's newest cu_q[b+1] - cu_q[b]
+        tokens over its pages (air_paged_prefill).  q / out: [total_q][n_q][d];
+        cu_q int32 [batch + 1]; max_q_len defaults to the largest q_len (read
+        back from cu_q, which synchronises)."""
+        args = self._prefill_args(q, cu_q, block_tables, seq_lens, out, max_q_len, scale, stream)
+        _lib.check(_lib.load().air_paged_prefill(*args), "air_paged_prefill")
+        return out
+
+    def bind_prefill(self, q, cu_q, block_tables, seq_lens, out, max_q_len=None, scale=None,
+                     stream=None):
+        """Validate once, return a zero-argument prefill launcher."""
+        args = self._prefill_args(q, cu_q, block_tables, seq_lens, out, max_q_len, scale, stream)
+        fn = _lib.load().air_paged_prefill
+        _lib.check(fn(*args), "air_paged_prefill")
+
+        def launch():
+            rc = fn(*args)
+            if rc:
+                _lib.check(rc, "air_paged_prefill")
+        return launch
+
     def bind_append(self, k, v, slot_mapping, stream=None):
         """Validate once, return a zero-argument append launcher."""
         self.append(k, v, slot_mapping, stream)

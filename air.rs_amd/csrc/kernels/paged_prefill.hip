@@ -1,0 +1,439 @@
+// Paged prefill attention (chunked, causal) on the matrix cores.
+//
+// For each sequence b, its q_len = cu_q[b + 1] - cu_q[b] newest tokens, whose
+// K/V are already in the pages, attend causally over the sequence's seq_len
+// cached tokens: query r sits at absolute position seq_len - q_len + r and
+// sees keys 0 ..= that position.  This is blockwise_attention_head with
+// q_offset = seq_len - q_len (src/chunked_attn.rs:114-213) per query head on
+// kv head h / group (:240-243), i.e. the causal prefill branch of
+// ops::attention with the mask of src/ops.rs:762-790, over paged storage.
+//
+// Work: a workgroup of four waves owns one (sequence, kv head) and four
+// consecutive work items of it, item = token block * group + head of the
+// group, a token block being 32 query rows.  With group 4 the four waves are
+// the four query heads of one token block, so every K/V tile staged in LDS
+// serves the whole GQA group.  Workgroups take their items heaviest first
+// (the last token blocks see the most keys).
+//
+// Per 32-key tile, per wave (32 query rows):
+//   S^T = K . Q^T   v_mfma_f32_32x32x16_bf16, M = 32 keys, N = 32 queries,
+//                   K = head_dim in 8 steps of 16.  K is read from LDS in the
+//                   A-operand layout (lane: key lane % 32, 8 contiguous
+//                   head_dim elements at 16*step + 8*(lane / 32)); Q^T stays in
+//                   registers in the matching B layout.  f32 queries are split
+//                   into hi + lo bf16 halves and take two products per step.
+//   online softmax in the log2 domain, one query per lane pair (lanes l and
+//                   l + 32 hold 16 keys each); the running max is raised only
+//                   when a tile exceeds it by 2^8, so probabilities stay below
+//                   256 and most tiles skip rescaling the accumulators.
+//   O^T += V^T . P^T  v_mfma_f32_32x32x16_bf16, M = 32 head_dim rows (four
+//                   tiles), N = 32 queries, K = 16 keys per step.  P^T is used
+//                   where the S^T product left it: its B-operand keys are
+//                   those of the C layout, keys (8*(i/4) + 4*(lane/32) + i%4)
+//                   for registers i = 8*step .. +8.  V is stored to LDS
+//                   transposed, V^T[d][c], with the key of column c = c with
+//                   bits 2 and 3 swapped, so a lane's eight keys of one step
+//                   are one contiguous 16-byte read.  P is split into hi + lo
+//                   bf16 halves (~16 mantissa bits): bf16 probabilities alone
+//                   leave ~1e-3 relative error at these lengths.
+//
+// K/V tiles are double-buffered in LDS: the global loads of tile t + 1 are
+// issued before tile t is computed and written to the other buffer after it,
+// with one barrier per tile.  Keys past the sequence and out-of-pool table
+// entries are staged as zeros (stale page bytes may hold non-finite values).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "../host/status.hpp"
+#include "../pool.hpp"
+#include "codecs.hpp"
+#include "prefill_common.hpp"
+
+namespace airkv {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kRows = 32;                   // query rows per wave
+constexpr int kKeys = 32;                   // keys per tile
+constexpr int D = 128;                      // head_dim
+constexpr int KPITCH = D * 2 + 16;          // bytes per K row in LDS (bank-spread 16-byte reads)
+constexpr int VPITCH = kKeys * 2 + 16;      // bytes per V^T row in LDS
+constexpr int KBUF = kKeys * KPITCH;
+constexpr int VBUF = D * VPITCH;
+constexpr int STAGE = KBUF + VBUF;
+
+#ifndef AIRKV_PREFILL_WAVES_PER_EU
+#define AIRKV_PREFILL_WAVES_PER_EU 2        // register budget: waves per SIMD
+#endif
+
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// bf16 bits (round to nearest even) of a finite f32.
+__device__ __forceinline__ uint32_t bf16_bits(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ void split_bf16(float x, uint32_t &hi, uint32_t &lo) {
+    hi = bf16_bits(x);
+    lo = bf16_bits(x - __uint_as_float(hi << 16));
+}
+
+// LDS column of key k inside a V^T row: bits 2 and 3 swapped (an involution).
+__device__ __forceinline__ int vcol_of_key(int k) {
+    return (k & 0x13) | ((k & 4) << 1) | ((k & 8) >> 1);
+}
+
+// Eight cache elements of one row as bf16 (16 bytes).  bf16 pages are raw
+// bits; int8 / fp8 pages are dequantized to the reference's f32 value
+// (q as f32 * scale, src/kv_cache.rs:88; to_f32(code) * scale,
+// src/fp8.rs:263-264) with one rounding, then rounded to bf16.  The fp8
+// conversion is the hardware's OCP E4M3, which agrees with the reference
+// decoder on every code its encoder emits.
+template <int DT> struct Raw8;
+template <> struct Raw8<AIR_KV_BF16> { u32x4 w; };
+template <> struct Raw8<AIR_KV_INT8> { u32x2 w; float s; };
+template <> struct Raw8<AIR_KV_FP8> { u32x2 w; float s; };
+
+template <int DT>
+__device__ __forceinline__ void load_raw(const void *pages, const float *scales, int64_t row,
+                                         int col, int n_sc, int scale_group, bool live,
+                                         Raw8<DT> &r) {
+    // `live` false: no load (the key is past the sequence or its block is
+    // outside the pool); the zeros stage a zero row.
+    if constexpr (DT == AIR_KV_BF16) {
+        r.w = u32x4{0, 0, 0, 0};
+        if (live) r.w = *reinterpret_cast<const u32x4 *>((const uint16_t *)pages + row * D + col);
+    } else {
+        r.w = u32x2{0, 0};
+        r.s = 0.0f;
+        if (live) {
+            r.w = *reinterpret_cast<const u32x2 *>((const uint8_t *)pages + row * D + col);
+            r.s = scales[row * n_sc + col / scale_group];
+        }
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ u32x4 to_bf16x8(const Raw8<DT> &r) {
+    if constexpr (DT == AIR_KV_BF16) {
+        return r.w;
+    } else {
+        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+        u32x4 o;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t w = r.w[h];
+            f32x2 lo, hi;
+            if constexpr (DT == AIR_KV_INT8) {
+                const uint32_t u = w ^ 0x80808080u;   // q + 128 as an unsigned byte
+                const float off = -128.0f * r.s;     // exact: fma gives q * s with one rounding
+                lo = f32x2{__builtin_fmaf((float)(u & 0xFFu), r.s, off),
+                           __builtin_fmaf((float)((u >> 8) & 0xFFu), r.s, off)};
+                hi = f32x2{__builtin_fmaf((float)((u >> 16) & 0xFFu), r.s, off),
+                           __builtin_fmaf((float)(u >> 24), r.s, off)};
+            } else {
+                lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false) * r.s;
+                hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true) * r.s;
+            }
+            o[2 * h] = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2));
+            o[2 * h + 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2));
+        }
+        return o;
+    }
+}
+
+__device__ __forceinline__ void store_out4(const PrefillArgs &a, int64_t idx, f32x4 v) {
+    if (a.out_dtype == AIR_KV_F32) {
+        *reinterpret_cast<f32x4 *>((float *)a.out + idx) = v;
+    } else {
+        const u32x2 w = {(uint32_t)bf16_rne(v[0]) | ((uint32_t)bf16_rne(v[1]) << 16),
+                         (uint32_t)bf16_rne(v[2]) | ((uint32_t)bf16_rne(v[3]) << 16)};
+        *reinterpret_cast<u32x2 *>((uint16_t *)a.out + idx) = w;
+    }
+}
+
+template <int BS, bool QF32, int DT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AIRKV_PREFILL_WAVES_PER_EU)))
+void prefill_kernel(PrefillArgs a) {
+    __shared__ __align__(16) uint8_t smem[2 * STAGE];
+    const int b = blockIdx.x, kh = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = a.group;
+    const int64_t max_len = (int64_t)a.max_blocks * BS;
+    const int32_t q0 = a.cu_q[b], q1 = a.cu_q[b + 1];
+    const int64_t len = a.lens[b];
+    const int qlen = q1 - q0;
+    const bool rows_ok = q0 >= 0 && q1 >= q0 && q1 <= a.total_q;
+    const bool seq_ok = rows_ok && len >= 0 && len <= max_len && qlen <= len;
+    const int32_t *tbl = a.tables + (int64_t)b * a.max_blocks;
+
+    if (blockIdx.z == 0 && kh == 0) {
+        // Each invalid sequence and each out-of-pool table entry within its
+        // length is counted once.
+        if (!seq_ok) {
+            if (tid == 0) atomicAdd(a.errors, 1ull);
+        } else if (qlen > 0) {
+            for (int64_t j = tid; j < (len + BS - 1) / BS; j += kThreads) {
+                const int32_t blk = tbl[j];
+                if (blk < 0 || blk >= a.num_blocks) atomicAdd(a.errors, 1ull);
+            }
+        }
+    }
+    if (!seq_ok) {
+        // rows of a sequence whose lengths are inconsistent become zeros
+        if (rows_ok && blockIdx.z == 0) {
+            const int64_t n = (int64_t)qlen * G * D;
+            for (int64_t i = tid; i < n; i += kThreads) {
+                const int64_t r = i / (G * D), e = i % (G * D);
+                const int64_t idx = ((int64_t)(q0 + r) * a.n_q_heads + kh * G) * D + e;
+                if (a.out_dtype == AIR_KV_F32) ((float *)a.out)[idx] = 0.0f;
+                else ((uint16_t *)a.out)[idx] = 0;
+            }
+        }
+        return;
+    }
+    if (qlen <= 0) return;
+
+    const int q_offset = (int)(len - qlen);
+    const int ntb = (qlen + kRows - 1) / kRows;
+    const int n_items = ntb * G;
+    const int n_wg = (n_items + kWaves - 1) / kWaves;
+    const int r32 = lane & 31, hh = lane >> 5;
+
+    // Staging roles.  K: thread covers 8-element chunks tid and tid + 256 of
+    // the tile's 32 x 16 chunks (row = chunk / 16).  V: thread covers keys
+    // 2p and 2p + 1 (p = tid % 16) at head_dim 8*dc .. +8 (dc = tid / 16), so
+    // it writes key pairs as packed dwords of V^T.
+    const int vp = tid & 15, vdc = tid >> 4;
+    const int n_sc = DT == AIR_KV_BF16 ? 0 : D / a.scale_group;
+    const char *kp = (const char *)a.k_pages;
+    const char *vpg = (const char *)a.v_pages;
+
+    Raw8<DT> rk[2], rv[2];
+    auto load_tile = [&](int t, int kend) {
+        const int kt = t * kKeys;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int c = tid + kThreads * i;
+            const int key = kt + (c >> 4);
+            int32_t blk = key < kend ? tbl[key / BS] : -1;
+            const bool live = blk >= 0 && blk < a.num_blocks;
+            const int64_t row = ((int64_t)(live ? blk : 0) * a.n_kv_heads + kh) * BS + key % BS;
+            load_raw<DT>(kp, a.k_scales, row, (c & 15) * 8, n_sc, a.scale_group, live, rk[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int key = kt + 2 * vp + i;
+            int32_t blk = key < kend ? tbl[key / BS] : -1;
+            const bool live = blk >= 0 && blk < a.num_blocks;
+            const int64_t row = ((int64_t)(live ? blk : 0) * a.n_kv_heads + kh) * BS + key % BS;
+            load_raw<DT>(vpg, a.v_scales, row, vdc * 8, n_sc, a.scale_group, live, rv[i]);
+        }
+    };
+    auto stage_tile = [&](int buf) {
+        uint8_t *ks = smem + buf * STAGE;
+        uint8_t *vs = ks + KBUF;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int c = tid + kThreads * i;
+            *reinterpret_cast<u32x4 *>(ks + (c >> 4) * KPITCH + (c & 15) * 16) = to_bf16x8<DT>(rk[i]);
+        }
+        const u32x4 v0 = to_bf16x8<DT>(rv[0]), v1 = to_bf16x8<DT>(rv[1]);
+        const int cp = vcol_of_key(2 * vp) >> 1;          // dword column of the key pair
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t e0 = (j & 1) ? v0[j >> 1] >> 16 : v0[j >> 1] & 0xFFFFu;
+            const uint32_t e1 = (j & 1) ? v1[j >> 1] >> 16 : v1[j >> 1] & 0xFFFFu;
+            *reinterpret_cast<uint32_t *>(vs + (vdc * 8 + j) * VPITCH + cp * 4) = e0 | (e1 << 16);
+        }
+    };
+
+    for (int w = blockIdx.z; w < n_wg; w += gridDim.z) {
+        const int wi = n_wg - 1 - w;                   // heaviest work first
+        const int item = wi * kWaves + wave;
+        const bool wvalid = item < n_items;
+        const int tb = (wvalid ? item : n_items - 1) / G;
+        const int g = (wvalid ? item : n_items - 1) % G;
+        const int h = kh * G + g;
+        const int r0 = tb * kRows;
+        const int last_item = (wi * kWaves + kWaves - 1 < n_items ? wi * kWaves + kWaves - 1 : n_items - 1);
+        const int tb_last = last_item / G;
+        const int rows_last = (tb_last + 1) * kRows < qlen ? (tb_last + 1) * kRows : qlen;
+        const int kend = q_offset + rows_last;          // keys the workgroup needs (<= len)
+        const int rows_w = r0 + kRows < qlen ? r0 + kRows : qlen;
+        const int kend_w = q_offset + rows_w;           // keys this wave needs
+        const int nt = (kend + kKeys - 1) / kKeys;
+
+        // Q^T as the B operand: lane holds query row r0 + lane % 32 (clamped
+        // to the last row; rows past q_len are computed and not stored),
+        // head_dim 16*ks + 8*(lane / 32) .. +8.
+        const int qrow = r0 + r32 < qlen ? r0 + r32 : qlen - 1;
+        const int qpos = q_offset + qrow;
+        u32x4 qhi[D / 16], qlo[D / 16];
+        {
+            const int64_t qbase = ((int64_t)(q0 + qrow) * a.n_q_heads + h) * D + 8 * hh;
+#pragma unroll
+            for (int ks = 0; ks < D / 16; ++ks) {
+                if constexpr (QF32) {
+                    const f32x4 *qp = reinterpret_cast<const f32x4 *>((const float *)a.q + qbase + 16 * ks);
+                    const f32x4 x0 = qp[0], x1 = qp[1];
+                    const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+                    uint32_t hv[8], lv[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) split_bf16(x[j], hv[j], lv[j]);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        qhi[ks][j] = hv[2 * j] | (hv[2 * j + 1] << 16);
+                        qlo[ks][j] = lv[2 * j] | (lv[2 * j + 1] << 16);
+                    }
+                } else {
+                    qhi[ks] = *reinterpret_cast<const u32x4 *>((const uint16_t *)a.q + qbase + 16 * ks);
+                    qlo[ks] = u32x4{0, 0, 0, 0};
+                }
+            }
+        }
+
+        f32x16 acc[D / 32];
+#pragma unroll
+        for (int n = 0; n < D / 32; ++n)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[n][i] = 0.0f;
+        float m_run = -INFINITY, l_run = 0.0f;
+
+        auto compute_tile = [&](int t, int buf) {
+            const uint8_t *ks_ = smem + buf * STAGE;
+            const uint8_t *vs_ = ks_ + KBUF;
+            const int kt = t * kKeys;
+            f32x16 s;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < D / 16; ++ks) {
+                const u32x4 ka = *reinterpret_cast<const u32x4 *>(ks_ + r32 * KPITCH + (16 * ks + 8 * hh) * 2);
+                s = mfma32(ka, qhi[ks], s);
+                if constexpr (QF32) s = mfma32(ka, qlo[ks], s);
+            }
+            // lane holds S[key kt + 8*(i/4) + 4*hh + i%4][query r32]
+            float sc[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key = kt + 8 * (i >> 2) + 4 * hh + (i & 3);
+                sc[i] = key <= qpos ? s[i] * a.scale_log2 : -INFINITY;
+            }
+            float mt = sc[0];
+#pragma unroll
+            for (int i = 1; i < 16; ++i) mt = fmaxf(mt, sc[i]);
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            if (__ballot(mt > m_run + 8.0f) != 0ull) {
+                const float m_new = fmaxf(m_run, mt);
+                const float alpha = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - m_new);
+                l_run *= alpha;
+#pragma unroll
+                for (int n = 0; n < D / 32; ++n) acc[n] *= alpha;
+                m_run = m_new;
+            }
+            float p[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) p[i] = (sc[i] == -INFINITY) ? 0.0f : exp2f(sc[i] - m_run);
+            float ls = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) ls += p[i];
+            l_run += ls;
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                uint32_t hv[8], lv[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) split_bf16(p[8 * st + j], hv[j], lv[j]);
+                const u32x4 phi = {hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16),
+                                   hv[6] | (hv[7] << 16)};
+                const u32x4 plo = {lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16), lv[4] | (lv[5] << 16),
+                                   lv[6] | (lv[7] << 16)};
+#pragma unroll
+                for (int n = 0; n < D / 32; ++n) {
+                    const u32x4 va = *reinterpret_cast<const u32x4 *>(vs_ + (32 * n + r32) * VPITCH +
+                                                                      (16 * st + 8 * hh) * 2);
+                    acc[n] = mfma32(va, phi, acc[n]);
+                    acc[n] = mfma32(va, plo, acc[n]);
+                }
+            }
+        };
+
+        load_tile(0, kend);
+        stage_tile(0);
+        __syncthreads();
+        for (int t = 0; t < nt; ++t) {
+            if (t + 1 < nt) load_tile(t + 1, kend);
+            if (wvalid && t * kKeys < kend_w) compute_tile(t, t & 1);
+            if (t + 1 < nt) stage_tile((t + 1) & 1);
+            __syncthreads();
+        }
+
+        if (wvalid && r0 + r32 < qlen) {
+            float l = l_run + __shfl_xor(l_run, 32);
+            const float inv = 1.0f / l;
+            const int64_t orow = ((int64_t)(q0 + r0 + r32) * a.n_q_heads + h) * D + 4 * hh;
+#pragma unroll
+            for (int n = 0; n < D / 32; ++n)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4)
+                    store_out4(a, orow + 32 * n + 8 * i4,
+                               f32x4{acc[n][4 * i4], acc[n][4 * i4 + 1], acc[n][4 * i4 + 2],
+                                     acc[n][4 * i4 + 3]} * inv);
+        }
+    }
+}
+
+template <int BS, int DT>
+hipError_t launch_dt(const PrefillArgs &a, hipStream_t s, dim3 grid) {
+    if (a.q_dtype == AIR_KV_F32)
+        hipLaunchKernelGGL((prefill_kernel<BS, true, DT>), grid, dim3(kThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL((prefill_kernel<BS, false, DT>), grid, dim3(kThreads), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int BS>
+hipError_t launch_bs(const PrefillArgs &a, int dtype, hipStream_t s, dim3 grid) {
+    switch (dtype) {
+    case AIR_KV_BF16: return launch_dt<BS, AIR_KV_BF16>(a, s, grid);
+    case AIR_KV_INT8: return launch_dt<BS, AIR_KV_INT8>(a, s, grid);
+    default: return launch_dt<BS, AIR_KV_FP8>(a, s, grid);
+    }
+}
+
+}  // namespace
+
+bool prefill_supported(int dtype, int head_dim, int block_size, int scale_group) {
+    if (head_dim != D || (block_size != 16 && block_size != 32)) return false;
+    if (dtype == AIR_KV_BF16) return true;
+    // 1-byte pages: a thread's 8 contiguous codes must share one scale
+    return (dtype == AIR_KV_INT8 || dtype == AIR_KV_FP8) && scale_group >= 8;
+}
+
+hipError_t launch_prefill(const PrefillArgs &a, int dtype, int block_size, int32_t max_q_len,
+                          hipStream_t s) {
+    // grid: x = sequence, y = kv head, z = workgroups per (sequence, kv head)
+    // sized for max_q_len; the kernel strides over z, so a sequence longer
+    // than max_q_len is still covered completely.
+    const int64_t ntb = ((int64_t)(max_q_len > 0 ? max_q_len : 1) + kRows - 1) / kRows;
+    int64_t nz = (ntb * a.group + kWaves - 1) / kWaves;
+    nz = nz > 65535 ? 65535 : nz;
+    const dim3 grid((unsigned)a.batch, (unsigned)a.n_kv_heads, (unsigned)nz);
+    return block_size == 16 ? launch_bs<16>(a, dtype, s, grid) : launch_bs<32>(a, dtype, s, grid);
+}
+
+}  // namespace airkv

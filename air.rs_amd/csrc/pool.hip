@@ -6,6 +6,7 @@
 #include <vector>
 
 #include "host/status.hpp"
+#include "kernels/prefill_common.hpp"
 #include "pool.hpp"
 
 using airkv::fail;
@@ -169,6 +170,45 @@ int air_paged_decode(air_kv_pool *p, void *stream, const void *q, int32_t q_dtyp
                                         block_tables, seq_lens, batch, max_blocks, scale, workspace,
                                         out, out_dtype);
     return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "air_paged_decode launch");
+}
+
+int air_paged_prefill(air_kv_pool *p, void *stream, const void *q, int32_t q_dtype, int32_t n_q_heads,
+                      const int32_t *cu_q, int32_t total_q, int32_t max_q_len,
+                      const int32_t *block_tables, const int32_t *seq_lens, int32_t batch,
+                      int32_t max_blocks, float scale, void *out, int32_t out_dtype) {
+    if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
+    const air_kv_pool_desc &d = p->desc;
+    if (!airkv::prefill_supported(d.dtype, d.head_dim, d.block_size, d.scale_group))
+        return fail(AIR_KV_E_INVALID_ARG,
+                    "paged prefill needs a BF16, INT8 or FP8 pool with head_dim 128 (pool dtype %d, head_dim %d)",
+                    d.dtype, d.head_dim);
+    if (n_q_heads <= 0 || n_q_heads % d.n_kv_heads)
+        return fail(AIR_KV_E_INVALID_ARG, "n_q_heads %d is not a multiple of n_kv_heads %d", n_q_heads,
+                    d.n_kv_heads);
+    if (batch < 0 || total_q < 0 || max_q_len < 0 || max_blocks < 0)
+        return fail(AIR_KV_E_INVALID_ARG, "negative batch, total_q, max_q_len or max_blocks");
+    if (batch == 0 || total_q == 0) return AIR_KV_OK;
+    if (!q || !cu_q || !block_tables || !seq_lens || !out)
+        return fail(AIR_KV_E_INVALID_ARG, "NULL prefill buffer");
+    if (q_dtype != AIR_KV_F32 && q_dtype != AIR_KV_BF16)
+        return fail(AIR_KV_E_INVALID_ARG, "q_dtype must be F32 or BF16");
+    if (out_dtype != AIR_KV_F32 && out_dtype != AIR_KV_BF16)
+        return fail(AIR_KV_E_INVALID_ARG, "out_dtype must be F32 or BF16");
+    if (!(scale == scale)) return fail(AIR_KV_E_INVALID_ARG, "scale is NaN");
+    if ((int64_t)max_blocks * d.block_size > INT32_MAX)
+        return fail(AIR_KV_E_INVALID_ARG, "max_blocks * block_size exceeds int32");
+    airkv::PrefillArgs a;
+    a.q = q; a.q_dtype = q_dtype; a.n_q_heads = n_q_heads;
+    a.cu_q = cu_q; a.tables = block_tables; a.lens = seq_lens;
+    a.batch = batch; a.max_blocks = max_blocks; a.total_q = total_q;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    a.n_kv_heads = d.n_kv_heads; a.group = n_q_heads / d.n_kv_heads; a.scale_group = d.scale_group;
+    a.num_blocks = d.num_blocks;
+    a.k_pages = p->k_pages; a.v_pages = p->v_pages; a.k_scales = p->k_scales; a.v_scales = p->v_scales;
+    a.out = out; a.out_dtype = out_dtype;
+    a.errors = p->errors;
+    hipError_t e = airkv::launch_prefill(a, d.dtype, d.block_size, max_q_len, (hipStream_t)stream);
+    return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "air_paged_prefill launch");
 }
 
 int air_kv_copy_blocks(air_kv_pool *p, void *stream, const int32_t *src, const int32_t *dst, int32_t n) {

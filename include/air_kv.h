@@ -253,6 +253,31 @@ int air_paged_decode(air_kv_pool *pool, void *stream, const void *q, int32_t q_d
                      int32_t batch, int32_t max_blocks, float scale, int32_t max_splits,
                      void *workspace, size_t ws_bytes, void *out, int32_t out_dtype);
 
+/* Paged prefill attention (chunked, causal): sequence b's q_len = cu_q[b + 1]
+ * - cu_q[b] newest tokens, whose K/V are already appended, attend over its
+ * seq_lens[b] cached tokens; query row r (0-based within the sequence) sits at
+ * position seq_lens[b] - q_len + r and sees keys 0 ..= that position:
+ *   out[cu_q[b] + r][h] = softmax over those keys of q . K[h / group]^T * scale, . V
+ * This is blockwise_attention_head with q_offset = seq_len - q_len
+ * (src/chunked_attn.rs:114-213) for every query head, GQA kv head h / group
+ * (:240-243) -- the causal prefill branch of ops::attention (src/ops.rs:333-357,
+ * mask :762-790) over paged storage, for the 512-token prefill chunks of
+ * src/generator.rs:46.  q / out: [total_q][n_q_heads][head_dim] as q_dtype /
+ * out_dtype (AIR_KV_F32 or AIR_KV_BF16); cu_q: int32 [batch + 1] (device).
+ * max_q_len sizes the launch (an upper bound of the q_len values; a larger
+ * q_len is still computed in full).  Supports BF16, INT8 and FP8 pools with
+ * head_dim 128 (quantized pages are dequantized q * scale in registers); other
+ * pools return AIR_KV_E_INVALID_ARG.  A sequence whose rows do not lie in
+ * [0, total_q], whose seq_len is outside [0, max_blocks * block_size] or
+ * whose q_len exceeds its seq_len is counted (air_kv_pool_error_count) and its
+ * rows (when they lie in [0, total_q]) are zero-filled; out-of-pool table
+ * entries within a sequence's length are counted and read as zero keys and
+ * values.  No workspace; rows of different sequences must not overlap. */
+int air_paged_prefill(air_kv_pool *pool, void *stream, const void *q, int32_t q_dtype,
+                      int32_t n_q_heads, const int32_t *cu_q, int32_t total_q, int32_t max_q_len,
+                      const int32_t *block_tables, const int32_t *seq_lens, int32_t batch,
+                      int32_t max_blocks, float scale, void *out, int32_t out_dtype);
+
 /* ------------------------------------------------------------------------ */
 /* SessionKvCache over pages                                                 */
 /* ------------------------------------------------------------------------ */

@@ -1,0 +1,221 @@
+"""GPU parity: paged prefill attention (chunked, causal) against the oracle's
+blockwise_attention_head per query head with q_offset = seq_len - q_len
+(src/chunked_attn.rs:114-213), through the C ABI.
+
+Tolerances (relative to max |reference|): 1e-3 for bf16 caches, 2e-2 for
+int8 / fp8 caches, the oracle running on the same dequantized cache.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import airkv
+from airkv import workloads
+from gpu_helpers import device_pool_for, host_pool_for, log, rel_err, run_appends, torch_mod
+
+pytestmark = pytest.mark.gpu
+
+TOL = {airkv.BF16: 1e-3, airkv.INT8: 2e-2, airkv.FP8: 2e-2}
+
+
+def _setup(cfg, ctx_lens, seed, outliers=None):
+    w = workloads.build_prefill_decode(cfg, ctx_lens, seed, decode_steps=0)
+    k, v = next(workloads.kv_rows(w.n_rows, cfg.n_kv_heads, cfg.head_dim, seed=seed + 100,
+                                  outliers=outliers, chunk_rows=1 << 24))
+    pool, host = device_pool_for(w), host_pool_for(w)
+    run_appends(w, k, v, pool, host)
+    tables, lens = w.tables()
+    return pool, host, tables, lens
+
+
+def _prefill_case(cfg, ctx_lens, q_lens, seed, q_bf16=True, out_bf16=False, max_q_len=None,
+                  outliers=None, kv_block=512):
+    torch = torch_mod()
+    pool, host, tables, lens = _setup(cfg, ctx_lens, seed, outliers)
+    cu = np.zeros(len(q_lens) + 1, np.int32)
+    cu[1:] = np.cumsum(q_lens)
+    total = int(cu[-1])
+    rng = np.random.default_rng(seed + 7)
+    q = rng.standard_normal((total, cfg.n_q_heads, cfg.head_dim)).astype(np.float32)
+    qt = torch.from_numpy(q).cuda()
+    if q_bf16:
+        qt = qt.to(torch.bfloat16)
+        q = qt.float().cpu().numpy()
+    out = torch.full(q.shape, float("nan"), dtype=torch.bfloat16 if out_bf16 else torch.float32,
+                     device="cuda")
+    pool.paged_prefill(qt, torch.from_numpy(cu).cuda(), torch.from_numpy(tables).cuda(),
+                       torch.from_numpy(lens).cuda(), out, max_q_len=max_q_len)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    want = host.paged_prefill(q, cu, tables, lens, kv_block=kv_block)
+    assert pool.error_count() == 0
+    assert np.all(np.isfinite(got))
+    return got, want
+
+
+@pytest.mark.parametrize("dtype", [airkv.BF16, airkv.INT8, airkv.FP8])
+@pytest.mark.parametrize("group", [1, 2, 4, 8])
+def test_prefill_matches_oracle_small(dtype, group):
+    """Chunks of 1, 31, 32, 33 and 100 rows over prefixes of 0 .. 300 tokens
+    (a whole-sequence prefill, partial token blocks, a single row)."""
+    log(f"prefill small dtype={dtype} group={group}")
+    nkv = 1 if group == 8 else 2
+    cfg = workloads.Config("small", nkv * group, nkv, 128, 16, dtype, 5)
+    q_lens = [1, 31, 32, 33, 100]
+    ctx = [1, 31 + 17, 32 + 300, 33, 100 + 45]
+    got, want = _prefill_case(cfg, ctx, q_lens, seed=60 + group)
+    err = rel_err(got, want)
+    log(f"  rel err {err:.2e}")
+    assert err <= TOL[dtype]
+
+
+@pytest.mark.parametrize("bs", [16, 32])
+def test_prefill_f32_queries_bf16_out(bs):
+    cfg = workloads.Config("q32", 8, 2, 128, bs, airkv.BF16, 3)
+    got, want = _prefill_case(cfg, [70, 129, 250], [70, 64, 97], seed=71, q_bf16=False,
+                              out_bf16=True)
+    err = rel_err(got, want)
+    log(f"prefill f32 q / bf16 out bs={bs}: rel err {err:.2e}")
+    assert err <= 1e-2          # bf16 output rounding (2^-9) dominates
+    got, want = _prefill_case(cfg, [70, 129, 250], [70, 64, 97], seed=71, q_bf16=False)
+    err = rel_err(got, want)
+    log(f"prefill f32 q / f32 out bs={bs}: rel err {err:.2e}")
+    assert err <= 1e-3
+
+
+def test_prefill_max_q_len_below_actual_still_complete():
+    cfg = workloads.Config("mq", 8, 2, 128, 16, airkv.BF16, 2)
+    got, want = _prefill_case(cfg, [300, 200], [300, 150], seed=73, max_q_len=40)
+    assert rel_err(got, want) <= 1e-3
+
+
+def test_prefill_c5_chunks_scaled():
+    """configs[4] prefill geometry: 512-token chunks (bs 32, 32 q / 8 kv,
+    bf16) over prefixes from the lognormal context mix; two sequences and a
+    reduced head count keep the scalar oracle within seconds."""
+    cfg = workloads.Config("c5p", 8, 2, 128, 32, airkv.BF16, 2)
+    prefix = workloads.c5_lengths(2, seed=5)
+    got, want = _prefill_case(cfg, [p + 512 for p in prefix], [512, 512], seed=75)
+    err = rel_err(got, want)
+    log(f"prefill c5 chunks (prefix {prefix}): rel err {err:.2e}")
+    assert err <= 1e-3
+
+
+def test_prefill_c3_int8_outliers():
+    cfg = workloads.Config("c3p", 16, 2, 128, 16, airkv.INT8, 2)
+    out_ch = workloads.outlier_channels(2, 128)
+    got, want = _prefill_case(cfg, [400, 257], [128, 257], seed=77, outliers=out_ch)
+    err = rel_err(got, want)
+    log(f"prefill int8 outliers: rel err {err:.2e}")
+    assert err <= 2e-2
+
+
+def test_prefill_full_c5_shape_vs_torch_fp32():
+    """The full configs[4] head geometry (32 q / 8 kv, d 128, bs 32) with
+    eight 512-token chunks, against a float32 torch attention over the
+    gathered cache (causal mask of src/ops.rs:762-790)."""
+    torch = torch_mod()
+    cfg = workloads.Config("c5full", 32, 8, 128, 32, airkv.BF16, 8)
+    prefix = workloads.c5_lengths(8, seed=9)
+    ctx = [p + 512 for p in prefix]
+    w = workloads.build_prefill_decode(cfg, ctx, 91, decode_steps=0)
+    rows = workloads.kv_rows(w.n_rows, 8, 128, seed=92, device="cuda", chunk_rows=1 << 24)
+    k, v = next(rows)
+    pool = device_pool_for(w)
+    off = 0
+    for slots in w.batches:
+        n = len(slots)
+        pool.append(k[off:off + n].contiguous(), v[off:off + n].contiguous(),
+                    torch.from_numpy(slots).cuda())
+        off += n
+    tables, lens = w.tables()
+    cu = np.arange(9, dtype=np.int32) * 512
+    g = torch.Generator(device="cuda")
+    g.manual_seed(93)
+    q = torch.randn((8 * 512, 32, 128), generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty((8 * 512, 32, 128), device="cuda")
+    tt, lt = torch.from_numpy(tables).cuda(), torch.from_numpy(lens).cuda()
+    pool.paged_prefill(q, torch.from_numpy(cu).cuda(), tt, lt, out, max_q_len=512)
+    # dense K/V of every sequence, token-major [t][h][d], f32
+    offs = np.zeros(9, np.int64)
+    offs[1:] = np.cumsum(np.array(lens, np.int64) * 8 * 128)
+    gk = torch.empty(int(offs[-1]), device="cuda")
+    gv = torch.empty_like(gk)
+    pool.gather(tt, lt, torch.from_numpy(offs[:-1]).cuda(), gk, gv, out_dtype=airkv.F32,
+                layout=airkv.LAYOUT_TOKEN_MAJOR)
+    assert pool.error_count() == 0
+    worst = 0.0
+    for b in range(8):
+        L = int(lens[b])
+        kb = gk[offs[b]:offs[b + 1]].view(L, 8, 128).permute(1, 0, 2).contiguous()   # [kv][L][d]
+        vb = gv[offs[b]:offs[b + 1]].view(L, 8, 128).permute(1, 0, 2).contiguous()
+        qb = q[512 * b:512 * (b + 1)].float().permute(1, 0, 2).contiguous()          # [32][512][d]
+        kr = kb.repeat_interleave(4, dim=0)
+        vr = vb.repeat_interleave(4, dim=0)
+        s = torch.bmm(qb, kr.transpose(1, 2).contiguous()) / np.sqrt(128.0)
+        qpos = torch.arange(L - 512, L, device="cuda")[:, None]
+        kpos = torch.arange(L, device="cuda")[None, :]
+        s = s.masked_fill(kpos > qpos, float("-inf"))
+        ref = torch.bmm(torch.softmax(s, dim=-1), vr).permute(1, 0, 2)               # [512][32][d]
+        got = out[512 * b:512 * (b + 1)]
+        e = float((got - ref).abs().max() / ref.abs().max())
+        worst = max(worst, e)
+    log(f"prefill full c5 shape vs torch fp32: worst rel err {worst:.2e}")
+    assert worst <= 1e-3
+
+
+def test_prefill_invalid_sequences_counted_and_zeroed():
+    """A chunk longer than its sequence and an out-of-range seq_len are
+    counted and their rows zero-filled; the valid sequence is unaffected; an
+    out-of-pool table entry inside a sequence is counted."""
+    torch = torch_mod()
+    cfg = workloads.Config("bad", 8, 2, 128, 16, airkv.BF16, 3)
+    pool, host, tables, lens = _setup(cfg, [40, 50, 60], seed=79)
+    q_lens = [10, 60, 5]                 # sequence 1: q_len 60 > seq_len 50
+    lens_bad = lens.copy()
+    lens_bad[2] = tables.shape[1] * 16 + 1   # beyond the table
+    cu = np.zeros(4, np.int32)
+    cu[1:] = np.cumsum(q_lens)
+    q = torch.randn((int(cu[-1]), 8, 128), device="cuda").to(torch.bfloat16)
+    out = torch.full((int(cu[-1]), 8, 128), 7.0, device="cuda")
+    pool.error_count(reset=True)
+    pool.paged_prefill(q, torch.from_numpy(cu).cuda(), torch.from_numpy(tables).cuda(),
+                       torch.from_numpy(lens_bad).cuda(), out)
+    torch.cuda.synchronize()
+    assert pool.error_count(reset=True) == 2
+    got = out.cpu().numpy()
+    assert np.all(got[10:] == 0.0)
+    want = host.paged_prefill(q.float().cpu().numpy()[:10], cu[:2], tables[:1], lens[:1])
+    assert rel_err(got[:10], want) <= 1e-3
+    # an out-of-pool block id inside sequence 0's length
+    t2 = tables.copy()
+    t2[0, 1] = 1 << 30
+    cu1 = np.array([0, 10], np.int32)
+    out1 = torch.zeros((10, 8, 128), device="cuda")
+    pool.paged_prefill(q[:10].contiguous(), torch.from_numpy(cu1).cuda(), torch.from_numpy(t2[:1]).cuda(),
+                       torch.from_numpy(lens[:1]).cuda(), out1)
+    assert pool.error_count(reset=True) == 1
+    assert torch.isfinite(out1).all()
+
+
+def test_prefill_rejects_unsupported_pools_and_args():
+    torch = torch_mod()
+    L = airkv.load()
+    p32 = airkv.KvPool(8, 16, 2, 128, airkv.F32)
+    q = torch.zeros((4, 8, 128), device="cuda")
+    cu = torch.tensor([0, 4], dtype=torch.int32, device="cuda")
+    tb = torch.zeros((1, 1), dtype=torch.int32, device="cuda")
+    ln = torch.tensor([4], dtype=torch.int32, device="cuda")
+    with pytest.raises(airkv.AirKvError):
+        p32.paged_prefill(q, cu, tb, ln, torch.empty_like(q))
+    pb = airkv.KvPool(8, 16, 2, 64, airkv.BF16)
+    with pytest.raises(airkv.AirKvError):
+        pb.paged_prefill(torch.zeros((4, 8, 64), device="cuda"), cu, tb, ln,
+                         torch.zeros((4, 8, 64), device="cuda"))
+    pb = airkv.KvPool(8, 16, 2, 128, airkv.BF16)
+    rc = L.air_paged_prefill(pb.handle, None, ctypes.c_void_p(q.data_ptr()), airkv.F32, 7,
+                             ctypes.c_void_p(cu.data_ptr()), 4, 4, ctypes.c_void_p(tb.data_ptr()),
+                             ctypes.c_void_p(ln.data_ptr()), 1, 1, 0.1, ctypes.c_void_p(q.data_ptr()),
+                             airkv.F32)
+    assert rc == airkv.AIR_KV_E_INVALID_ARG
