@@ -91,6 +91,18 @@ __device__ __forceinline__ void split_bf16(float x, uint32_t &hi, uint32_t &lo) 
     lo = bf16_bits(x - __uint_as_float(hi << 16));
 }
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// (x, y) = hi + lo with both halves bf16 pairs (hardware round to nearest
+// even): hi carries 8 significant bits, lo the next 8.
+__device__ __forceinline__ void split_pair(float x, float y, uint32_t &hi, uint32_t &lo) {
+    const f32x2 v = {x, y};
+    const bf16x2 h = __builtin_convertvector(v, bf16x2);
+    const f32x2 r = v - __builtin_convertvector(h, f32x2);
+    hi = __builtin_bit_cast(uint32_t, h);
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2));
+}
+
 // LDS column of key k inside a V^T row: bits 2 and 3 swapped (an involution).
 __device__ __forceinline__ int vcol_of_key(int k) {
     return (k & 0x13) | ((k & 4) << 1) | ((k & 8) >> 1);
@@ -107,22 +119,17 @@ template <> struct Raw8<AIR_KV_BF16> { u32x4 w; };
 template <> struct Raw8<AIR_KV_INT8> { u32x2 w; float s; };
 template <> struct Raw8<AIR_KV_FP8> { u32x2 w; float s; };
 
+// Unconditional load: the row is always inside the pool.  Whether the key is
+// live (inside the sequence, block inside the pool) is applied when the tile
+// is staged, so no wait for the load sits before the current tile's compute.
 template <int DT>
 __device__ __forceinline__ void load_raw(const void *pages, const float *scales, int64_t row,
-                                         int col, int n_sc, int scale_group, bool live,
-                                         Raw8<DT> &r) {
-    // `live` false: no load (the key is past the sequence or its block is
-    // outside the pool); the zeros stage a zero row.
+                                         int col, int n_sc, int scale_group, Raw8<DT> &r) {
     if constexpr (DT == AIR_KV_BF16) {
-        r.w = u32x4{0, 0, 0, 0};
-        if (live) r.w = *reinterpret_cast<const u32x4 *>((const uint16_t *)pages + row * D + col);
+        r.w = *reinterpret_cast<const u32x4 *>((const uint16_t *)pages + row * D + col);
     } else {
-        r.w = u32x2{0, 0};
-        r.s = 0.0f;
-        if (live) {
-            r.w = *reinterpret_cast<const u32x2 *>((const uint8_t *)pages + row * D + col);
-            r.s = scales[row * n_sc + col / scale_group];
-        }
+        r.w = *reinterpret_cast<const u32x2 *>((const uint8_t *)pages + row * D + col);
+        r.s = scales[row * n_sc + col / scale_group];
     }
 }
 
@@ -131,7 +138,6 @@ __device__ __forceinline__ u32x4 to_bf16x8(const Raw8<DT> &r) {
     if constexpr (DT == AIR_KV_BF16) {
         return r.w;
     } else {
-        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
         u32x4 o;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -152,16 +158,6 @@ __device__ __forceinline__ u32x4 to_bf16x8(const Raw8<DT> &r) {
             o[2 * h + 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2));
         }
         return o;
-    }
-}
-
-__device__ __forceinline__ void store_out4(const PrefillArgs &a, int64_t idx, f32x4 v) {
-    if (a.out_dtype == AIR_KV_F32) {
-        *reinterpret_cast<f32x4 *>((float *)a.out + idx) = v;
-    } else {
-        const u32x2 w = {(uint32_t)bf16_rne(v[0]) | ((uint32_t)bf16_rne(v[1]) << 16),
-                         (uint32_t)bf16_rne(v[2]) | ((uint32_t)bf16_rne(v[3]) << 16)};
-        *reinterpret_cast<u32x2 *>((uint16_t *)a.out + idx) = w;
     }
 }
 
@@ -214,8 +210,8 @@ void prefill_kernel(PrefillArgs a) {
     const int n_wg = (n_items + kWaves - 1) / kWaves;
     const int r32 = lane & 31, hh = lane >> 5;
 
-    // Staging roles.  K: thread covers 8-element chunks tid and tid + 256 of
-    // the tile's 32 x 16 chunks (row = chunk / 16).  V: thread covers keys
+    // Staging roles.  K: thread covers head_dim 8*(tid % 16) .. +8 of key rows
+    // tid / 16 and 16 + tid / 16.  V: thread covers keys
     // 2p and 2p + 1 (p = tid % 16) at head_dim 8*dc .. +8 (dc = tid / 16), so
     // it writes key pairs as packed dwords of V^T.
     const int vp = tid & 15, vdc = tid >> 4;
@@ -224,42 +220,63 @@ void prefill_kernel(PrefillArgs a) {
     const char *vpg = (const char *)a.v_pages;
 
     Raw8<DT> rk[2], rv[2];
+    bool klive[2], vlive[2];
+    // The pages of tile t are 32 / BS consecutive table entries, the same for
+    // the whole workgroup.  They are fetched one tile ahead of the page loads
+    // (nb0, nb1 hold the next tile's ids), so a page load never waits on its
+    // table entry.  kend <= len keeps every index inside the table row.
+    // Both entries are loaded unconditionally from indices clamped to the
+    // last page in use (a branch here would make the compiler wait for every
+    // load in flight).
+    int32_t nb0 = 0, nb1 = 0;
+    auto fetch_ids = [&](int t, int kend) {
+        const int last = (kend - 1) / BS;
+        const int j0 = (t * kKeys) / BS;
+        nb0 = tbl[j0 < last ? j0 : last];
+        if constexpr (BS == 16) nb1 = tbl[j0 + 1 < last ? j0 + 1 : last];
+        else nb1 = nb0;
+    };
+    // Stale page bytes may hold non-finite values: keys past the sequence and
+    // blocks outside the pool are staged as zeros (the loads themselves read
+    // block 0 for them).
     auto load_tile = [&](int t, int kend) {
         const int kt = t * kKeys;
+        const int32_t b0 = __builtin_amdgcn_readfirstlane(nb0), b1 = __builtin_amdgcn_readfirstlane(nb1);
+        const bool ok0 = b0 >= 0 && b0 < a.num_blocks, ok1 = b1 >= 0 && b1 < a.num_blocks;
+        const int64_t base0 = ((int64_t)(ok0 ? b0 : 0) * a.n_kv_heads + kh) * BS;
+        const int64_t base1 = ((int64_t)(ok1 ? b1 : 0) * a.n_kv_heads + kh) * BS;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const int c = tid + kThreads * i;
-            const int key = kt + (c >> 4);
-            int32_t blk = key < kend ? tbl[key / BS] : -1;
-            const bool live = blk >= 0 && blk < a.num_blocks;
-            const int64_t row = ((int64_t)(live ? blk : 0) * a.n_kv_heads + kh) * BS + key % BS;
-            load_raw<DT>(kp, a.k_scales, row, (c & 15) * 8, n_sc, a.scale_group, live, rk[i]);
+            const int r = (tid >> 4) + 16 * i;           // key row of the tile
+            const bool second = BS == 16 && i == 1;      // row in the tile's second page
+            klive[i] = kt + r < kend && (second ? ok1 : ok0);
+            const int64_t row = (second ? base1 : base0) + (BS == 16 ? (tid >> 4) : r);
+            load_raw<DT>(kp, a.k_scales, row, (tid & 15) * 8, n_sc, a.scale_group, rk[i]);
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const int key = kt + 2 * vp + i;
-            int32_t blk = key < kend ? tbl[key / BS] : -1;
-            const bool live = blk >= 0 && blk < a.num_blocks;
-            const int64_t row = ((int64_t)(live ? blk : 0) * a.n_kv_heads + kh) * BS + key % BS;
-            load_raw<DT>(vpg, a.v_scales, row, vdc * 8, n_sc, a.scale_group, live, rv[i]);
+            const int r = 2 * vp + i;
+            const bool second = BS == 16 && r >= 16;
+            vlive[i] = kt + r < kend && (second ? ok1 : ok0);
+            const int64_t row = (second ? base1 : base0) + r % BS;
+            load_raw<DT>(vpg, a.v_scales, row, vdc * 8, n_sc, a.scale_group, rv[i]);
         }
     };
     auto stage_tile = [&](int buf) {
         uint8_t *ks = smem + buf * STAGE;
         uint8_t *vs = ks + KBUF;
+        const u32x4 zero = {0, 0, 0, 0};
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int c = tid + kThreads * i;
-            *reinterpret_cast<u32x4 *>(ks + (c >> 4) * KPITCH + (c & 15) * 16) = to_bf16x8<DT>(rk[i]);
-        }
-        const u32x4 v0 = to_bf16x8<DT>(rv[0]), v1 = to_bf16x8<DT>(rv[1]);
+        for (int i = 0; i < 2; ++i)
+            *reinterpret_cast<u32x4 *>(ks + ((tid >> 4) + 16 * i) * KPITCH + (tid & 15) * 16) =
+                klive[i] ? to_bf16x8<DT>(rk[i]) : zero;
+        const u32x4 v0 = vlive[0] ? to_bf16x8<DT>(rv[0]) : zero;
+        const u32x4 v1 = vlive[1] ? to_bf16x8<DT>(rv[1]) : zero;
         const int cp = vcol_of_key(2 * vp) >> 1;          // dword column of the key pair
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t e0 = (j & 1) ? v0[j >> 1] >> 16 : v0[j >> 1] & 0xFFFFu;
-            const uint32_t e1 = (j & 1) ? v1[j >> 1] >> 16 : v1[j >> 1] & 0xFFFFu;
-            *reinterpret_cast<uint32_t *>(vs + (vdc * 8 + j) * VPITCH + cp * 4) = e0 | (e1 << 16);
-        }
+        for (int j = 0; j < 8; ++j)       // bf16 j of both keys as one dword: (key 2p, key 2p + 1)
+            *reinterpret_cast<uint32_t *>(vs + (vdc * 8 + j) * VPITCH + cp * 4) =
+                __builtin_amdgcn_perm(v1[j >> 1], v0[j >> 1], (j & 1) ? 0x07060302u : 0x05040100u);
     };
 
     for (int w = blockIdx.z; w < n_wg; w += gridDim.z) {
@@ -340,7 +357,7 @@ void prefill_kernel(PrefillArgs a) {
             mt = fmaxf(mt, __shfl_xor(mt, 32));
             if (__ballot(mt > m_run + 8.0f) != 0ull) {
                 const float m_new = fmaxf(m_run, mt);
-                const float alpha = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - m_new);
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);   // 0 on the first tile
                 l_run *= alpha;
 #pragma unroll
                 for (int n = 0; n < D / 32; ++n) acc[n] *= alpha;
@@ -348,20 +365,17 @@ void prefill_kernel(PrefillArgs a) {
             }
             float p[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) p[i] = (sc[i] == -INFINITY) ? 0.0f : exp2f(sc[i] - m_run);
+            for (int i = 0; i < 16; ++i) p[i] = __builtin_amdgcn_exp2f(sc[i] - m_run);   // masked: 0
             float ls = 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; ++i) ls += p[i];
             l_run += ls;
 #pragma unroll
             for (int st = 0; st < 2; ++st) {
-                uint32_t hv[8], lv[8];
+                uint32_t hv[4], lv[4];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) split_bf16(p[8 * st + j], hv[j], lv[j]);
-                const u32x4 phi = {hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16),
-                                   hv[6] | (hv[7] << 16)};
-                const u32x4 plo = {lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16), lv[4] | (lv[5] << 16),
-                                   lv[6] | (lv[7] << 16)};
+                for (int j = 0; j < 4; ++j) split_pair(p[8 * st + 2 * j], p[8 * st + 2 * j + 1], hv[j], lv[j]);
+                const u32x4 phi = {hv[0], hv[1], hv[2], hv[3]}, plo = {lv[0], lv[1], lv[2], lv[3]};
 #pragma unroll
                 for (int n = 0; n < D / 32; ++n) {
                     const u32x4 va = *reinterpret_cast<const u32x4 *>(vs_ + (32 * n + r32) * VPITCH +
@@ -372,27 +386,44 @@ void prefill_kernel(PrefillArgs a) {
             }
         };
 
+        fetch_ids(0, kend);
         load_tile(0, kend);
+        fetch_ids(1, kend);
         stage_tile(0);
         __syncthreads();
         for (int t = 0; t < nt; ++t) {
-            if (t + 1 < nt) load_tile(t + 1, kend);
+            if (t + 1 < nt) {
+                load_tile(t + 1, kend);
+                fetch_ids(t + 2, kend);
+            }
             if (wvalid && t * kKeys < kend_w) compute_tile(t, t & 1);
             if (t + 1 < nt) stage_tile((t + 1) & 1);
             __syncthreads();
         }
 
         if (wvalid && r0 + r32 < qlen) {
-            float l = l_run + __shfl_xor(l_run, 32);
+            const float l = l_run + __shfl_xor(l_run, 32);
             const float inv = 1.0f / l;
             const int64_t orow = ((int64_t)(q0 + r0 + r32) * a.n_q_heads + h) * D + 4 * hh;
+            if (a.out_dtype == AIR_KV_F32) {
 #pragma unroll
-            for (int n = 0; n < D / 32; ++n)
+                for (int n = 0; n < D / 32; ++n)
 #pragma unroll
-                for (int i4 = 0; i4 < 4; ++i4)
-                    store_out4(a, orow + 32 * n + 8 * i4,
-                               f32x4{acc[n][4 * i4], acc[n][4 * i4 + 1], acc[n][4 * i4 + 2],
-                                     acc[n][4 * i4 + 3]} * inv);
+                    for (int i4 = 0; i4 < 4; ++i4)
+                        *reinterpret_cast<f32x4 *>((float *)a.out + orow + 32 * n + 8 * i4) =
+                            f32x4{acc[n][4 * i4], acc[n][4 * i4 + 1], acc[n][4 * i4 + 2], acc[n][4 * i4 + 3]} * inv;
+            } else {
+#pragma unroll
+                for (int n = 0; n < D / 32; ++n)
+#pragma unroll
+                    for (int i4 = 0; i4 < 4; ++i4) {
+                        const f32x2 x = f32x2{acc[n][4 * i4], acc[n][4 * i4 + 1]} * inv;
+                        const f32x2 y = f32x2{acc[n][4 * i4 + 2], acc[n][4 * i4 + 3]} * inv;
+                        *reinterpret_cast<u32x2 *>((uint16_t *)a.out + orow + 32 * n + 8 * i4) =
+                            u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2)),
+                                  __builtin_bit_cast(uint32_t, __builtin_convertvector(y, bf16x2))};
+                    }
+            }
         }
     }
 }
