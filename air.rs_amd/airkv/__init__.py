@@ -8,6 +8,7 @@ not touch the GPU.
 from ._lib import (AIR_KV_E_HIP, AIR_KV_E_INVALID_ARG, AIR_KV_E_NOT_FOUND, AIR_KV_E_OOM,
                    AIR_KV_E_STATE, AIR_KV_OK, BF16, F32, FP8, INT8, LAYOUT_HEAD_MAJOR,
                    LAYOUT_TOKEN_MAJOR, LIB_PATH, SIGNATURES, AirKvError, last_error, load)
+from . import kv_compress
 from .kv_swap import KvSwapManager, pool_callbacks
 from .paged_attention import (BLOCK_SIZE, MAX_BLOCKS, BlockAllocator, BlockTable,
                               SequenceManager, num_blocks_for_tokens)
@@ -20,4 +21,5 @@ __all__ = [
     "LIB_PATH", "SIGNATURES", "AirKvError", "last_error", "load", "KvSwapManager",
     "pool_callbacks", "BLOCK_SIZE", "MAX_BLOCKS", "BlockAllocator", "BlockTable",
     "SequenceManager", "num_blocks_for_tokens", "KvPool", "PagedSessionCache", "wire_int8_quantize",
+    "kv_compress",
 ]

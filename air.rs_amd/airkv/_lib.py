@@ -118,6 +118,14 @@ SIGNATURES = {
     "air_kv_unpack_blocks": (_int, [_P, _P, _P, _i32, _P]),
     "air_kv_wire_int8_quantize": (_int, [_P, _P, _i32, _SZ, _P, _P]),
     "air_kv_pack_blocks_int8": (_int, [_P, _P, _P, _i32, _P, _P]),
+    "air_kv_key_compress": (_int, [_P, _P, _i32, _i64, _i32, _P, _P, _P]),
+    "air_kv_key_decompress": (_int, [_P, _P, _P, _P, _i64, _i32, _P]),
+    "air_kv_value_compress": (_int, [_P, _P, _i32, _i64, _i32, _P, _P, _P]),
+    "air_kv_value_decompress": (_int, [_P, _P, _P, _P, _i64, _i32, _P]),
+    "air_kv_qjl_compress": (_int, [_P, _P, _i32, _i64, _i32, _P, _i32, _P, _P]),
+    "air_kv_qjl_scores": (_int, [_P, _P, _P, _i64, _i32, _P, ctypes.c_float, _P, _P]),
+    "air_kv_compress_blocks": (_int, [_P, _P, _P, _i32, _P, _P, _P, _P, _P, _P]),
+    "air_kv_qjl_compress_blocks": (_int, [_P, _P, _P, _i32, _P, _i32, _P, _P]),
     "air_kv_copy_blocks": (_int, [_P, _P, _P, _P, _i32]),
     "air_kv_read_blocks": (_int, [_P, _P, _pi32, _i32, _P]),
     "air_kv_write_blocks": (_int, [_P, _P, _pi32, _i32, _P]),

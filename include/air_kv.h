@@ -356,6 +356,64 @@ int air_kv_wire_int8_quantize(void *stream, const void *wire, int32_t n_blocks,
 int air_kv_pack_blocks_int8(air_kv_pool *pool, void *stream, const int32_t *ids, int32_t n,
                             int8_t *codes, float *scales);
 
+/* ------------------------------------------------------------------------ */
+/* kv_compress warm-tier codecs (src/kv_compress.rs)                          */
+/* ------------------------------------------------------------------------ */
+
+/* Batched codecs over rows of `dim` elements (dim 32, 64 or 128; rows are
+ * device [n_rows][dim] arrays of rows_dtype AIR_KV_F32 or AIR_KV_BF16, 16-byte
+ * aligned).  Every output is bit-exact with the reference's scalar code: one
+ * row per lane folds its elements left to right, as the reference's
+ * iterators do, and products and sums round separately.  All device
+ * pointers; asynchronous on `stream`. */
+
+/* CompressedKey::compress (src/kv_compress.rs:79-109) of each row:
+ * bits[r][w] (ceil(dim / 64) words, bit i = row[i] >= mean, LSB first),
+ * magnitude[r] = |row| (sqrt of the left fold of squares), mean[r]. */
+int air_kv_key_compress(void *stream, const void *rows, int32_t rows_dtype, int64_t n_rows,
+                        int32_t dim, uint64_t *bits, float *magnitude, float *mean);
+/* CompressedKey::decompress (:112-127): out[r][i] = (+-1) * (magnitude /
+ * sqrt(dim)) + mean, f32 (any dim >= 1). */
+int air_kv_key_decompress(void *stream, const uint64_t *bits, const float *magnitude,
+                          const float *mean, int64_t n_rows, int32_t dim, float *out);
+/* CompressedValue::compress (:187-218): codes[r][i] = round((v - min) /
+ * scale) clamped to [0, 255] (NaN -> 0), scale = (max - min) / 255 or 1.0,
+ * NaN-ignoring min / max folds.  codes must be 16-byte aligned. */
+int air_kv_value_compress(void *stream, const void *rows, int32_t rows_dtype, int64_t n_rows,
+                          int32_t dim, uint8_t *codes, float *scale, float *min_val);
+/* CompressedValue::decompress (:221-226): out = q * scale + min, f32. */
+int air_kv_value_decompress(void *stream, const uint8_t *codes, const float *scale,
+                            const float *min_val, int64_t n_rows, int32_t dim, float *out);
+/* QjlKey::compress (:930-951) with the row-major [proj_dim][dim] f32 matrix
+ * `proj` (qjl_projection_matrix, :989-1017, is built by the caller):
+ * bit i of row r = (proj[i] . row > 0), magnitude[r] = |row|.  proj_dim
+ * 1..512; bits[r] holds ceil(proj_dim / 64) words. */
+int air_kv_qjl_compress(void *stream, const void *rows, int32_t rows_dtype, int64_t n_rows,
+                        int32_t dim, const float *proj, int32_t proj_dim, uint64_t *bits,
+                        float *magnitude);
+/* QjlKey::approx_cos_sim / approx_dot (:959-975) of one query (query_bits,
+ * device, ceil(proj_dim / 64) words) against n_keys keys: cos_sim[k] =
+ * cos(pi * hamming / proj_dim) (the cosine evaluated by the host's libm, as
+ * the reference's f32::cos), dot[k] = cos_sim[k] * key_magnitude[k] *
+ * query_magnitude.  Either output may be NULL. */
+int air_kv_qjl_scores(void *stream, const uint64_t *key_bits, const float *key_magnitude,
+                      int64_t n_keys, int32_t proj_dim, const uint64_t *query_bits,
+                      float query_magnitude, float *cos_sim, float *dot);
+/* Warm-tier compression of whole pool blocks, CompressedKvEntry::compress
+ * (:283-292) of every (head, token) row: the K rows of blocks ids[0..n) with
+ * CompressedKey::compress and the V rows with CompressedValue::compress.
+ * Rows are ordered [i][head][token] (n * n_kv_heads * block_size rows);
+ * quantized pools are dequantized (q * scale) first.  Ids outside the pool
+ * give zero outputs and are counted (air_kv_pool_error_count).  Pools with
+ * head_dim 32, 64 or 128. */
+int air_kv_compress_blocks(air_kv_pool *pool, void *stream, const int32_t *ids, int32_t n,
+                           uint64_t *key_bits, float *key_magnitude, float *key_mean,
+                           uint8_t *value_codes, float *value_scale, float *value_min);
+/* QjlKey::compress of the K rows of pool blocks (same row order). */
+int air_kv_qjl_compress_blocks(air_kv_pool *pool, void *stream, const int32_t *ids, int32_t n,
+                               const float *proj, int32_t proj_dim, uint64_t *bits,
+                               float *magnitude);
+
 /* Copies whole blocks src[i] -> dst[i] (int32, device): the page copy that
  * BlockAllocator::cow_write leaves to "a real impl" (src/paged_attention.rs:160). */
 int air_kv_copy_blocks(air_kv_pool *pool, void *stream, const int32_t *src_blocks,

@@ -80,6 +80,23 @@ def assert_bits_equal(a, b, what):
         raise AssertionError(f"{what}: {bad.size} bytes differ, first at byte {bad[0]}")
 
 
+def assert_floats_bit_equal(a, b, what):
+    """f32 arrays equal bit for bit, except that any NaN matches any NaN: the
+    sign and payload of a NaN produced by arithmetic are unspecified by IEEE
+    754 and by Rust (its float docs call NaN bit patterns non-deterministic),
+    so only NaN-ness is part of the contract."""
+    a = np.array(a, np.float32, copy=True)
+    b = np.array(b, np.float32, copy=True)
+    assert a.shape == b.shape, (what, a.shape, b.shape)
+    na, nb = np.isnan(a), np.isnan(b)
+    if not np.array_equal(na, nb):
+        bad = np.nonzero(na != nb)[0]
+        raise AssertionError(f"{what}: NaN positions differ, first at {bad[0]}")
+    a[na] = 0.0
+    b[nb] = 0.0
+    assert_bits_equal(a, b, what)
+
+
 def rel_err(got, want):
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
