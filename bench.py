@@ -11,8 +11,10 @@ resident in HBM before timing starts.
 Prints one JSON line: whole-step HBM throughput (`value`, GB/s of
 algorithmic bytes), the decode call's roofline fraction (HIP events on the
 launch stream; HBM traffic from the committed rocprofv3 counter runs),
-gather / large-append bandwidths, decode at the c3 / c4 / c5 configs, and the
-CPU oracle timed on the same workload on this host (all cores and one core).
+gather / large-append bandwidths, decode at the c3 / c4 / c5 configs, paged
+prefill at the c5 chunk geometry (TFLOP/s), warm-tier block compression
+(GB/s), and the CPU oracle timed on the same workload on this host (all cores
+and one core).
 """
 import argparse
 import json
@@ -172,6 +174,78 @@ def config_decode(torch, name, iters=20):
     return res
 
 
+def prefill_leg(torch, iters=20):
+    """Paged prefill at the configs[4] geometry: eight 512-token chunks (32 q /
+    8 kv heads, d 128, bs 32, bf16 pages and queries) over prefixes drawn
+    from the lognormal context mix.  Algorithmic flops count QK^T and PV over
+    the causal keys only: 4 * d per (query row, head, key)."""
+    import numpy as np
+
+    import airkv
+    from airkv import workloads
+    cfg = workloads.Config("c5-prefill", 32, 8, 128, 32, airkv.BF16, 8)
+    chunk = 512
+    prefix = workloads.c5_lengths(cfg.batch, seed=5)
+    w = workloads.build_prefill_decode(cfg, [p + chunk for p in prefix], seed=5, decode_steps=0)
+    pool = airkv.KvPool(w.num_blocks, cfg.block_size, cfg.n_kv_heads, cfg.head_dim, cfg.dtype)
+    gen = workloads.kv_rows(10 ** 12, cfg.n_kv_heads, cfg.head_dim, seed=6, device="cuda", chunk_rows=32768)
+    for slots in w.batches:
+        st = torch.from_numpy(slots).cuda()
+        done = 0
+        while done < len(slots):
+            k, v = next(gen)
+            n = min(len(slots) - done, k.shape[0])
+            pool.append(k[:n].contiguous(), v[:n].contiguous(), st[done:done + n].contiguous())
+            done += n
+    tables, lens = w.tables()
+    cu = torch.arange(cfg.batch + 1, dtype=torch.int32, device="cuda") * chunk
+    q = torch.randn(cfg.batch * chunk, cfg.n_q_heads, cfg.head_dim, device="cuda").to(torch.bfloat16)
+    out = torch.empty_like(q)
+    fn = pool.bind_prefill(q, cu, torch.from_numpy(tables).cuda(), torch.from_numpy(lens).cuda(), out,
+                           max_q_len=chunk)
+    ms = timed_loop(torch, fn, iters)
+    keys = sum(sum(int(L) - chunk + r + 1 for r in range(chunk)) for L in lens)
+    flops = keys * cfg.n_q_heads * 4 * cfg.head_dim
+    tf = flops / (ms * 1e-3) / 1e12
+    assert pool.error_count() == 0
+    pool.close()
+    return {"tflops": round(tf, 1), "us": round(ms * 1e3, 1), "frac_of_bf16_mfma": round(tf / 2500.0, 4),
+            "prefix_tokens": [int(x) for x in prefix], "chunk": chunk, "q_rows": cfg.batch * chunk,
+            "flops": int(flops)}
+
+
+def compress_leg(torch, iters=10):
+    """Warm-tier compression of 8192 bf16 blocks (bs 16, 8 kv heads, d 128:
+    1M K rows and 1M V rows) with air_kv_compress_blocks.  Algorithmic bytes:
+    the pages read (512 B per K and V row) plus the outputs written (16 B bits
+    + 8 B per key row, 128 B codes + 8 B per value row) and 4 B per id."""
+    import numpy as np
+
+    import airkv
+    from airkv import kv_compress as kc
+    nb = 8192
+    pool = airkv.KvPool(nb + 64, 16, 8, 128, airkv.BF16)
+    k = torch.randn(nb * 16, 8, 128, device="cuda")
+    slots = torch.arange(nb * 16, dtype=torch.int64, device="cuda")
+    pool.append(k, torch.randn_like(k), slots)
+    del k
+    ids = torch.from_numpy(np.random.default_rng(7).permutation(nb).astype(np.int32)).cuda()
+    kc.compress_blocks(pool, ids)
+    outs = kc.compress_blocks(pool, ids)
+    L = airkv.load()
+    import ctypes
+    args = (pool.handle, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream), ctypes.c_void_p(ids.data_ptr()),
+            nb, *[ctypes.c_void_p(outs[n].data_ptr()) for n in
+                  ("key_bits", "key_magnitude", "key_mean", "value_codes", "value_scale", "value_min")])
+    ms = timed_loop(torch, lambda: L.air_kv_compress_blocks(*args), iters)
+    rows = nb * 16 * 8
+    nbytes = rows * (2 * 256 + 16 + 8 + 128 + 8) + 4 * nb
+    assert pool.error_count() == 0
+    pool.close()
+    return {"gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "us": round(ms * 1e3, 1), "rows": rows,
+            "blocks": nb, "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -321,6 +395,10 @@ def main():
         for name in ("c3", "c4", "c5"):
             extra["other_configs"][name] = config_decode(torch, name)
             log(f"{name} decode {extra['other_configs'][name]}")
+        extra["prefill_c5"] = prefill_leg(torch)
+        log(f"prefill {extra['prefill_c5']['tflops']} TFLOP/s")
+        extra["kv_compress_blocks"] = compress_leg(torch)
+        log(f"compress blocks {extra['kv_compress_blocks']['gbps']} GB/s")
 
     cpu = None
     if not args.no_cpu:
