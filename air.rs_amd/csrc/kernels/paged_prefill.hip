@@ -37,9 +37,10 @@
 //                   bf16 halves (~16 mantissa bits): bf16 probabilities alone
 //                   leave ~1e-3 relative error at these lengths.
 //
-// K/V tiles are double-buffered in LDS: the global loads of tile t + 1 are
-// issued before tile t is computed and written to the other buffer after it,
-// with one barrier per tile.  Keys past the sequence and out-of-pool table
+// K/V tiles are double-buffered in LDS and two tiles ahead in registers: the
+// global loads of tile t + 2 are issued before tile t is computed, and tile
+// t + 1 is written to the other LDS buffer after it, with one barrier per
+// tile.  Keys past the sequence and out-of-pool table
 // entries are staged as zeros (stale page bytes may hold non-finite values).
 #include <hip/hip_runtime.h>
 
@@ -119,17 +120,28 @@ template <> struct Raw8<AIR_KV_BF16> { u32x4 w; };
 template <> struct Raw8<AIR_KV_INT8> { u32x2 w; float s; };
 template <> struct Raw8<AIR_KV_FP8> { u32x2 w; float s; };
 
-// Unconditional load: the row is always inside the pool.  Whether the key is
-// live (inside the sequence, block inside the pool) is applied when the tile
-// is staged, so no wait for the load sits before the current tile's compute.
+// Buffer descriptor word 3 for raw (untyped) buffer access on gfx9-class GPUs.
+constexpr int kBufferWord3 = 0x00020000;
+
+// One page slab (block_size rows of one kv head) as a buffer resource.  The
+// tile's page bases are uniform, so the descriptors live in scalar registers
+// and each thread's offsets inside a page stay constant across tiles.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const void *base, int64_t byte_off, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)((const char *)base + byte_off), (short)0, bytes,
+                                             kBufferWord3);
+}
+
+// Unconditional load of 8 elements at byte offset `off` of a page (the page
+// is always inside the pool: out-of-pool ids read block 0 and are zeroed
+// when staged), plus the group scale for 1-byte pages.
 template <int DT>
-__device__ __forceinline__ void load_raw(const void *pages, const float *scales, int64_t row,
-                                         int col, int n_sc, int scale_group, Raw8<DT> &r) {
+__device__ __forceinline__ void load_raw(__amdgpu_buffer_rsrc_t pg, __amdgpu_buffer_rsrc_t sc, int off,
+                                         int soff, Raw8<DT> &r) {
     if constexpr (DT == AIR_KV_BF16) {
-        r.w = *reinterpret_cast<const u32x4 *>((const uint16_t *)pages + row * D + col);
+        r.w = __builtin_amdgcn_raw_buffer_load_b128(pg, off, 0, 0);
     } else {
-        r.w = *reinterpret_cast<const u32x2 *>((const uint8_t *)pages + row * D + col);
-        r.s = scales[row * n_sc + col / scale_group];
+        r.w = __builtin_amdgcn_raw_buffer_load_b64(pg, off, 0, 0);
+        r.s = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(sc, soff, 0, 0));
     }
 }
 
@@ -216,18 +228,22 @@ void prefill_kernel(PrefillArgs a) {
     // it writes key pairs as packed dwords of V^T.
     const int vp = tid & 15, vdc = tid >> 4;
     const int n_sc = DT == AIR_KV_BF16 ? 0 : D / a.scale_group;
-    const char *kp = (const char *)a.k_pages;
-    const char *vpg = (const char *)a.v_pages;
 
-    Raw8<DT> rk[2], rv[2];
-    bool klive[2], vlive[2];
+    // One tile's loaded rows (this thread's two K chunks and two V chunks)
+    // and the tile's uniform facts: first key, and whether each page is
+    // inside the pool.
+    struct TileRegs {
+        Raw8<DT> k[2], v[2];
+        int kt;
+        bool ok0, ok1;
+    };
     // The pages of tile t are 32 / BS consecutive table entries, the same for
     // the whole workgroup.  They are fetched one tile ahead of the page loads
-    // (nb0, nb1 hold the next tile's ids), so a page load never waits on its
-    // table entry.  kend <= len keeps every index inside the table row.
-    // Both entries are loaded unconditionally from indices clamped to the
-    // last page in use (a branch here would make the compiler wait for every
-    // load in flight).
+    // (nb0, nb1 hold the ids of the next tile to load), so a page load never
+    // waits on its table entry.  kend <= len keeps every index inside the
+    // table row.  Both entries are loaded unconditionally from indices
+    // clamped to the last page in use (a branch here would make the compiler
+    // wait for every load in flight).
     int32_t nb0 = 0, nb1 = 0;
     auto fetch_ids = [&](int t, int kend) {
         const int last = (kend - 1) / BS;
@@ -236,42 +252,70 @@ void prefill_kernel(PrefillArgs a) {
         if constexpr (BS == 16) nb1 = tbl[j0 + 1 < last ? j0 + 1 : last];
         else nb1 = nb0;
     };
-    // Stale page bytes may hold non-finite values: keys past the sequence and
-    // blocks outside the pool are staged as zeros (the loads themselves read
-    // block 0 for them).
-    auto load_tile = [&](int t, int kend) {
-        const int kt = t * kKeys;
+    // Per-thread byte offsets inside a page (constant across tiles).  K chunk
+    // i: key row (tid / 16) + 16 i of the tile; V chunk i: key 2 vp + i.
+    constexpr int EB = DT == AIR_KV_BF16 ? 2 : 1;
+    constexpr int PAGE_BYTES = BS * D * EB;
+    int k_off[2], v_off[2], ks_off[2], vs_off[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int kr = ((tid >> 4) + 16 * i) % BS, vr = (2 * vp + i) % BS;
+        k_off[i] = (kr * D + (tid & 15) * 8) * EB;
+        v_off[i] = (vr * D + vdc * 8) * EB;
+        ks_off[i] = (kr * n_sc + ((tid & 15) * 8) / (n_sc ? a.scale_group : 1)) * 4;
+        vs_off[i] = (vr * n_sc + (vdc * 8) / (n_sc ? a.scale_group : 1)) * 4;
+    }
+    auto load_tile = [&](int t, TileRegs &R) {
         const int32_t b0 = __builtin_amdgcn_readfirstlane(nb0), b1 = __builtin_amdgcn_readfirstlane(nb1);
-        const bool ok0 = b0 >= 0 && b0 < a.num_blocks, ok1 = b1 >= 0 && b1 < a.num_blocks;
-        const int64_t base0 = ((int64_t)(ok0 ? b0 : 0) * a.n_kv_heads + kh) * BS;
-        const int64_t base1 = ((int64_t)(ok1 ? b1 : 0) * a.n_kv_heads + kh) * BS;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int r = (tid >> 4) + 16 * i;           // key row of the tile
-            const bool second = BS == 16 && i == 1;      // row in the tile's second page
-            klive[i] = kt + r < kend && (second ? ok1 : ok0);
-            const int64_t row = (second ? base1 : base0) + (BS == 16 ? (tid >> 4) : r);
-            load_raw<DT>(kp, a.k_scales, row, (tid & 15) * 8, n_sc, a.scale_group, rk[i]);
+        R.kt = t * kKeys;
+        R.ok0 = b0 >= 0 && b0 < a.num_blocks;
+        R.ok1 = b1 >= 0 && b1 < a.num_blocks;
+        const int64_t row0 = ((int64_t)(R.ok0 ? b0 : 0) * a.n_kv_heads + kh) * BS;
+        const int64_t row1 = ((int64_t)(R.ok1 ? b1 : 0) * a.n_kv_heads + kh) * BS;
+        const __amdgpu_buffer_rsrc_t k0 = page_rsrc(a.k_pages, row0 * D * EB, PAGE_BYTES);
+        const __amdgpu_buffer_rsrc_t v0 = page_rsrc(a.v_pages, row0 * D * EB, PAGE_BYTES);
+        const __amdgpu_buffer_rsrc_t k1 = page_rsrc(a.k_pages, row1 * D * EB, PAGE_BYTES);
+        const __amdgpu_buffer_rsrc_t v1 = page_rsrc(a.v_pages, row1 * D * EB, PAGE_BYTES);
+        __amdgpu_buffer_rsrc_t ks0 = k0, vs0 = v0, ks1 = k1, vs1 = v1;
+        if constexpr (DT != AIR_KV_BF16) {
+            ks0 = page_rsrc(a.k_scales, row0 * n_sc * 4, BS * n_sc * 4);
+            vs0 = page_rsrc(a.v_scales, row0 * n_sc * 4, BS * n_sc * 4);
+            ks1 = page_rsrc(a.k_scales, row1 * n_sc * 4, BS * n_sc * 4);
+            vs1 = page_rsrc(a.v_scales, row1 * n_sc * 4, BS * n_sc * 4);
         }
+        // BS 16: K chunk i and V keys >= 16 lie in the tile's second page
+        load_raw<DT>(k0, ks0, k_off[0], ks_off[0], R.k[0]);
+        if constexpr (BS == 16) load_raw<DT>(k1, ks1, k_off[1], ks_off[1], R.k[1]);
+        else load_raw<DT>(k0, ks0, k_off[1], ks_off[1], R.k[1]);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const int r = 2 * vp + i;
-            const bool second = BS == 16 && r >= 16;
-            vlive[i] = kt + r < kend && (second ? ok1 : ok0);
-            const int64_t row = (second ? base1 : base0) + r % BS;
-            load_raw<DT>(vpg, a.v_scales, row, vdc * 8, n_sc, a.scale_group, rv[i]);
+            if (BS == 16 && vp >= 8) load_raw<DT>(v1, vs1, v_off[i], vs_off[i], R.v[i]);
+            else load_raw<DT>(v0, vs0, v_off[i], vs_off[i], R.v[i]);
         }
     };
-    auto stage_tile = [&](int buf) {
+    // Stale page bytes may hold non-finite values: keys past the sequence and
+    // rows of out-of-pool blocks are staged as zeros.  Only the tiles that
+    // hold such keys (uniform test) pay for the selects.
+    auto stage_tile = [&](int buf, const TileRegs &R, int kend) {
         uint8_t *ks = smem + buf * STAGE;
         uint8_t *vs = ks + KBUF;
         const u32x4 zero = {0, 0, 0, 0};
+        u32x4 kx[2] = {to_bf16x8<DT>(R.k[0]), to_bf16x8<DT>(R.k[1])};
+        u32x4 v0 = to_bf16x8<DT>(R.v[0]), v1 = to_bf16x8<DT>(R.v[1]);
+        if (!(R.ok0 && R.ok1 && R.kt + kKeys <= kend)) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int r = (tid >> 4) + 16 * i;
+                const bool okp = (BS == 16 && i == 1) ? R.ok1 : R.ok0;
+                kx[i] = (R.kt + r < kend && okp) ? kx[i] : zero;
+            }
+            const bool okv = (BS == 16 && vp >= 8) ? R.ok1 : R.ok0;
+            v0 = (R.kt + 2 * vp < kend && okv) ? v0 : zero;
+            v1 = (R.kt + 2 * vp + 1 < kend && okv) ? v1 : zero;
+        }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            *reinterpret_cast<u32x4 *>(ks + ((tid >> 4) + 16 * i) * KPITCH + (tid & 15) * 16) =
-                klive[i] ? to_bf16x8<DT>(rk[i]) : zero;
-        const u32x4 v0 = vlive[0] ? to_bf16x8<DT>(rv[0]) : zero;
-        const u32x4 v1 = vlive[1] ? to_bf16x8<DT>(rv[1]) : zero;
+            *reinterpret_cast<u32x4 *>(ks + ((tid >> 4) + 16 * i) * KPITCH + (tid & 15) * 16) = kx[i];
         const int cp = vcol_of_key(2 * vp) >> 1;          // dword column of the key pair
 #pragma unroll
         for (int j = 0; j < 8; ++j)       // bf16 j of both keys as one dword: (key 2p, key 2p + 1)
@@ -322,6 +366,15 @@ void prefill_kernel(PrefillArgs a) {
                     qlo[ks] = u32x4{0, 0, 0, 0};
                 }
             }
+            // Consume Q here, once per work item: otherwise the compiler
+            // cannot tell inside the tile loop that these loads have landed
+            // and waits on the vector-memory counter there, i.e. on the page
+            // loads issued for later tiles.
+#pragma unroll
+            for (int ks = 0; ks < D / 16; ++ks) {
+                asm volatile("" ::"v"(qhi[ks]));
+                if constexpr (QF32) asm volatile("" ::"v"(qlo[ks]));
+            }
         }
 
         f32x16 acc[D / 32];
@@ -344,17 +397,23 @@ void prefill_kernel(PrefillArgs a) {
                 s = mfma32(ka, qhi[ks], s);
                 if constexpr (QF32) s = mfma32(ka, qlo[ks], s);
             }
-            // lane holds S[key kt + 8*(i/4) + 4*hh + i%4][query r32]
+            // lane holds S[key kt + 8*(i/4) + 4*hh + i%4][query r32].  Only
+            // tiles that cross the causal diagonal of the wave's first row
+            // need the mask (a uniform test).  The scale (> 0) is applied
+            // after the max and inside the exponent's fma.
+            const bool diag = kt + kKeys - 1 > q_offset + r0;
+            const int kq = qpos - kt - 4 * hh;       // key i is visible when 8*(i/4) + i%4 <= kq
             float sc[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int key = kt + 8 * (i >> 2) + 4 * hh + (i & 3);
-                sc[i] = key <= qpos ? s[i] * a.scale_log2 : -INFINITY;
-            }
-            float mt = sc[0];
+            for (int i = 0; i < 16; ++i) sc[i] = s[i];
+            if (diag) {
 #pragma unroll
-            for (int i = 1; i < 16; ++i) mt = fmaxf(mt, sc[i]);
-            mt = fmaxf(mt, __shfl_xor(mt, 32));
+                for (int i = 0; i < 16; ++i) sc[i] = 8 * (i >> 2) + (i & 3) <= kq ? sc[i] : -INFINITY;
+            }
+            float mt = fmaxf(sc[0], sc[1]);
+#pragma unroll
+            for (int i = 2; i < 16; ++i) mt = fmaxf(mt, sc[i]);
+            mt = fmaxf(mt, __shfl_xor(mt, 32)) * a.scale_log2;
             if (__ballot(mt > m_run + 8.0f) != 0ull) {
                 const float m_new = fmaxf(m_run, mt);
                 const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);   // 0 on the first tile
@@ -365,7 +424,8 @@ void prefill_kernel(PrefillArgs a) {
             }
             float p[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) p[i] = __builtin_amdgcn_exp2f(sc[i] - m_run);   // masked: 0
+            for (int i = 0; i < 16; ++i)   // masked: exp2(-inf) = 0
+                p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], a.scale_log2, -m_run));
             float ls = 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; ++i) ls += p[i];
@@ -386,18 +446,34 @@ void prefill_kernel(PrefillArgs a) {
             }
         };
 
+        // Two register sets hold the next two tiles: the loads of tile t + 2
+        // are issued before tile t is computed, and tile t + 1 (loaded a tile
+        // earlier) is staged after it, so every load has about two tiles of
+        // compute to land.  The loop is unrolled by two so both sets stay in
+        // fixed registers; even tiles use LDS buffer 0, odd tiles buffer 1.
+        TileRegs ra, rb;
         fetch_ids(0, kend);
-        load_tile(0, kend);
+        load_tile(0, ra);
         fetch_ids(1, kend);
-        stage_tile(0);
+        if (nt > 1) load_tile(1, rb);
+        fetch_ids(2, kend);
+        stage_tile(0, ra, kend);
         __syncthreads();
-        for (int t = 0; t < nt; ++t) {
-            if (t + 1 < nt) {
-                load_tile(t + 1, kend);
-                fetch_ids(t + 2, kend);
+        for (int t = 0; t < nt; t += 2) {
+            if (t + 2 < nt) {
+                load_tile(t + 2, ra);
+                fetch_ids(t + 3, kend);
             }
-            if (wvalid && t * kKeys < kend_w) compute_tile(t, t & 1);
-            if (t + 1 < nt) stage_tile((t + 1) & 1);
+            if (wvalid && t * kKeys < kend_w) compute_tile(t, 0);
+            if (t + 1 < nt) stage_tile(1, rb, kend);
+            __syncthreads();
+            if (t + 1 >= nt) break;
+            if (t + 3 < nt) {
+                load_tile(t + 3, rb);
+                fetch_ids(t + 4, kend);
+            }
+            if (wvalid && (t + 1) * kKeys < kend_w) compute_tile(t + 1, 1);
+            if (t + 2 < nt) stage_tile(0, ra, kend);
             __syncthreads();
         }
 

@@ -1,6 +1,7 @@
 // extern "C" entry points for the device pool (air_kv.h, "Device side").
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -194,7 +195,8 @@ int air_paged_prefill(air_kv_pool *p, void *stream, const void *q, int32_t q_dty
         return fail(AIR_KV_E_INVALID_ARG, "q_dtype must be F32 or BF16");
     if (out_dtype != AIR_KV_F32 && out_dtype != AIR_KV_BF16)
         return fail(AIR_KV_E_INVALID_ARG, "out_dtype must be F32 or BF16");
-    if (!(scale == scale)) return fail(AIR_KV_E_INVALID_ARG, "scale is NaN");
+    if (!(scale > 0.0f && scale < INFINITY))
+        return fail(AIR_KV_E_INVALID_ARG, "prefill scale must be finite and > 0");
     if ((int64_t)max_blocks * d.block_size > INT32_MAX)
         return fail(AIR_KV_E_INVALID_ARG, "max_blocks * block_size exceeds int32");
     airkv::PrefillArgs a;

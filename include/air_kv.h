@@ -265,7 +265,8 @@ int air_paged_decode(air_kv_pool *pool, void *stream, const void *q, int32_t q_d
  * src/generator.rs:46.  q / out: [total_q][n_q_heads][head_dim] as q_dtype /
  * out_dtype (AIR_KV_F32 or AIR_KV_BF16); cu_q: int32 [batch + 1] (device).
  * max_q_len sizes the launch (an upper bound of the q_len values; a larger
- * q_len is still computed in full).  Supports BF16, INT8 and FP8 pools with
+ * q_len is still computed in full).  scale must be finite and > 0 (the
+ * reference's is 1/sqrt(head_dim)).  Supports BF16, INT8 and FP8 pools with
  * head_dim 128 (quantized pages are dequantized q * scale in registers); other
  * pools return AIR_KV_E_INVALID_ARG.  A sequence whose rows do not lie in
  * [0, total_q], whose seq_len is outside [0, max_blocks * block_size] or

@@ -219,3 +219,7 @@ def test_prefill_rejects_unsupported_pools_and_args():
                              ctypes.c_void_p(ln.data_ptr()), 1, 1, 0.1, ctypes.c_void_p(q.data_ptr()),
                              airkv.F32)
     assert rc == airkv.AIR_KV_E_INVALID_ARG
+    # the scale must be finite and > 0
+    for bad in (0.0, -0.5, float("inf")):
+        with pytest.raises(airkv.AirKvError):
+            pb.paged_prefill(q, cu, tb, ln, torch.empty_like(q), scale=bad)
