@@ -218,15 +218,24 @@ constexpr int waves_per_simd(int dt) {
     return dt == AIR_KV_BF16 ? AIRKV_DECODE_WAVES_PER_EU : AIRKV_DECODE_QWAVES_PER_EU;
 }
 
+// f32 queries on 1-byte pages carry the hi + lo query halves as well and do
+// not fit the 3-wave register budget: they are built for 2 waves per SIMD.
+constexpr int kernel_waves_per_simd(int dt, bool qf32) {
+    return (qf32 && dt != AIR_KV_BF16) ? 2 : waves_per_simd(dt);
+}
+
 template <int D, int BS, bool QF32, int DT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(waves_per_simd(DT))))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kernel_waves_per_simd(DT, QF32))))
 void decode_mfma_kernel(DecodeArgs a) {
     static_assert(D == 128, "lane mappings assume head_dim 128");
     constexpr bool QUANT = DT != AIR_KV_BF16;
     constexpr int EB = QUANT ? 1 : 2;         // bytes per cache element
     constexpr int KSTEPS = D / 32;            // QK k-steps
     constexpr int DTILES = D / 16;            // PV output tiles along head_dim
-    constexpr int PITCH = D + 4;              // LDS row pitch in bf16 elements
+    // LDS row pitch in bf16 elements: 288 bytes = 72 dwords, 8 mod 64, so the
+    // four rows x four 8-byte column chunks of one transposing read land on
+    // distinct banks.
+    constexpr int PITCH = D + 16;
     constexpr int VTILE = 16 * PITCH;         // bf16 elements per wave's V tile
     static_assert(BS % 16 == 0, "a 16-token tile must not straddle pages");
     __shared__ int32_t s_pre[kMaxBatch + 1];
@@ -484,13 +493,18 @@ void decode_mfma_kernel(DecodeArgs a) {
                 dst[1] = u32x2{x[2], x[3]};
             }
         }
-        // O^T[d][h] += V^T[d][t] P^T[t][h]; A lane holds V[t = 4*g4 + jj][d = 16n + r16]
-        const uint16_t *col = sv + (4 * g4) * PITCH + r16;
+        // O^T[d][h] += V^T[d][t] P^T[t][h]; the A lane holds V[t = 4*g4 + jj][d =
+        // 16n + r16], jj = 0..3.  V stays row-major in LDS and a transposing
+        // read builds the operand: within each 16-lane group, lane j receives
+        // element j % 4 of the 8 bytes addressed by lanes 4k + j / 4 (k =
+        // 0..3), so lane 16*g4 + s points at V[4*g4 + s/4][16n + 4*(s%4)].
+        const uint16_t *col = sv + (4 * g4 + (r16 >> 2)) * PITCH + 4 * (r16 & 3);
 #pragma unroll
         for (int n = 0; n < DTILES; ++n) {
-            const uint16_t *c = col + 16 * n;
-            const u32x2 av = {(uint32_t)c[0] | ((uint32_t)c[PITCH] << 16),
-                              (uint32_t)c[2 * PITCH] | ((uint32_t)c[3 * PITCH] << 16)};
+            typedef short s16x4 __attribute__((ext_vector_type(4)));
+            const s16x4 t4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4 *)(col + 16 * n));
+            const u32x2 av = __builtin_bit_cast(u32x2, t4);
             acc[n] = mfma_pv(av, p_hi, acc[n]);
             if constexpr (!QUANT) acc[n] = mfma_pv(av, p_lo, acc[n]);
         }
