@@ -232,10 +232,12 @@ void decode_mfma_kernel(DecodeArgs a) {
     constexpr int EB = QUANT ? 1 : 2;         // bytes per cache element
     constexpr int KSTEPS = D / 32;            // QK k-steps
     constexpr int DTILES = D / 16;            // PV output tiles along head_dim
-    // LDS row pitch in bf16 elements: 288 bytes = 72 dwords, 8 mod 64, so the
-    // four rows x four 8-byte column chunks of one transposing read land on
-    // distinct banks.
-    constexpr int PITCH = D + 16;
+    // V tile layout in LDS: row pitch 320 bytes, and the 8-byte column chunks
+    // of row r stored at chunk ^ (r & 7).  With it the transposing reads and
+    // both store patterns (1-byte and bf16 pages) touch every bank once per
+    // cycle (a 288-byte pitch without the swizzle left the 1-byte stores
+    // 4-way conflicted).
+    constexpr int PITCH = D + 32;
     constexpr int VTILE = 16 * PITCH;         // bf16 elements per wave's V tile
     static_assert(BS % 16 == 0, "a 16-token tile must not straddle pages");
     __shared__ int32_t s_pre[kMaxBatch + 1];
@@ -476,11 +478,11 @@ void decode_mfma_kernel(DecodeArgs a) {
         if constexpr (QUANT) {
             const float vsc = __uint_as_float(t.vs);
             const bool live = vrow < nv;
-            u32x2 *dst = reinterpret_cast<u32x2 *>(sv + vrow * PITCH + vcol);
+            u32x2 *dst = reinterpret_cast<u32x2 *>(sv + vrow * PITCH);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const u32x2 x = dequant4<DT>(t.v[i >> 2][i & 3], vsc);
-                dst[i] = live ? x : u32x2{0, 0};
+                dst[(vcol / 4 + i) ^ (vrow & 7)] = live ? x : u32x2{0, 0};
             }
         } else {
 #pragma unroll
@@ -488,22 +490,24 @@ void decode_mfma_kernel(DecodeArgs a) {
                 const int row = v * 4 + vrow;
                 u32x4 x = t.v[v];
                 if (row >= nv) x = u32x4{0, 0, 0, 0};
-                u32x2 *dst = reinterpret_cast<u32x2 *>(sv + row * PITCH + vcol);
-                dst[0] = u32x2{x[0], x[1]};
-                dst[1] = u32x2{x[2], x[3]};
+                u32x2 *dst = reinterpret_cast<u32x2 *>(sv + row * PITCH);
+                dst[(vcol / 4) ^ (row & 7)] = u32x2{x[0], x[1]};
+                dst[(vcol / 4 + 1) ^ (row & 7)] = u32x2{x[2], x[3]};
             }
         }
         // O^T[d][h] += V^T[d][t] P^T[t][h]; the A lane holds V[t = 4*g4 + jj][d =
         // 16n + r16], jj = 0..3.  V stays row-major in LDS and a transposing
         // read builds the operand: within each 16-lane group, lane j receives
         // element j % 4 of the 8 bytes addressed by lanes 4k + j / 4 (k =
-        // 0..3), so lane 16*g4 + s points at V[4*g4 + s/4][16n + 4*(s%4)].
-        const uint16_t *col = sv + (4 * g4 + (r16 >> 2)) * PITCH + 4 * (r16 & 3);
+        // 0..3), so lane 16*g4 + s points at V[4*g4 + s/4][16n + 4*(s%4)]
+        // (chunk 4n + s%4 of that row, swizzled as stored).
+        const int vr = 4 * g4 + (r16 >> 2);
+        const uint16_t *vrow_p = sv + vr * PITCH;
 #pragma unroll
         for (int n = 0; n < DTILES; ++n) {
             typedef short s16x4 __attribute__((ext_vector_type(4)));
             const s16x4 t4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) s16x4 *)(col + 16 * n));
+                (__attribute__((address_space(3))) s16x4 *)(vrow_p + 4 * ((4 * n + (r16 & 3)) ^ (vr & 7))));
             const u32x2 av = __builtin_bit_cast(u32x2, t4);
             acc[n] = mfma_pv(av, p_hi, acc[n]);
             if constexpr (!QUANT) acc[n] = mfma_pv(av, p_lo, acc[n]);
