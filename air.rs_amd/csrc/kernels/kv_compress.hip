@@ -9,11 +9,11 @@
 // The reference folds each vector left to right (Iterator::sum, f32::min /
 // max folds, a dot product per projected row), and the fold order fixes the
 // rounding of the mean, the norm and every projection.  So one lane owns one
-// row and runs the folds in that order; rows reach the lanes through LDS:
-// a wave stages 64 rows x 32 columns with coalesced loads (any pool dtype,
-// dequantized by the shared page loader), then each lane reads its row back
-// (row pitch 33 floats: conflict-free) and keeps it in registers.  Products
-// and sums round separately (no contraction), as Rust's do.
+// row and runs the folds in that order.  It loads its whole row itself (any
+// pool dtype, dequantized by the shared page loader) with back-to-back
+// 16-byte pieces, so every cache line is fetched once, and keeps it in
+// registers.  Products and sums round separately (no contraction), as
+// Rust's do.
 //
 // Rows come either from a dense [n_rows][dim] array or from pool blocks: row
 // r of a block list is row r % (n_kv_heads * block_size) of the K or V slab
@@ -31,21 +31,16 @@ namespace airkv {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
-constexpr int kPitch = 33;          // floats per staged row (32 columns + 1: bank spread)
 constexpr int kProjRows = 32;       // projection rows staged in LDS at a time
 
-__device__ __forceinline__ float rust_min(float a, float b) {
-    if (a != a) return b;
-    if (b != b) return a;
-    return a < b ? a : b;
-}
-
-__device__ __forceinline__ float rust_max(float a, float b) {
-    if (a != a) return b;
-    if (b != b) return a;
-    return a > b ? a : b;
-}
+// One step of the NaN-ignoring folds `value.iter().fold(INF, f32::min)` and
+// `fold(-INF, f32::max)` as the oracle states them (a < b ? a : b, the
+// other operand on NaN).  The accumulator starts at +-inf and only ever
+// takes non-NaN values, so each step is one unordered compare and a select:
+// keep the accumulator when it wins strictly or x is NaN, else take x (on a
+// tie, x, as `a < b ? a : b` returns b).
+__device__ __forceinline__ float fold_min(float acc, float x) { return !(acc >= x) ? acc : x; }
+__device__ __forceinline__ float fold_max(float acc, float x) { return !(acc <= x) ? acc : x; }
 
 // Element offset of row r and whether its block is inside the pool.
 __device__ __forceinline__ bool row_elem(const RowSource &s, int64_t r, int dim, int64_t &elem) {
@@ -60,42 +55,51 @@ __device__ __forceinline__ bool row_elem(const RowSource &s, int64_t r, int dim,
     return ok;
 }
 
-// The wave's 64 rows row0 .. row0 + 63 into registers: lane l gets row row0 + l
-// in x.  Rows past n_rows and rows of out-of-pool blocks read as zeros; `live`
-// tells the lane whether its row is real.  Every thread of the workgroup calls
-// this the same number of times (it contains barriers).
+// Row r into registers (its own lane): D / 8 pieces of 8 elements, read
+// back to back by the same lane.  Plain (cacheable) loads: the lanes of a
+// wave read 64 different rows, so each 128-byte line is needed by several
+// consecutive loads of one lane and must stay in cache between them (a
+// streaming load would fetch it again).  INT8 / FP8 rows are dequantized as
+// q * scale with one rounding (src/kv_cache.rs:88, src/fp8.rs:263-264).
+// Rows of out-of-pool blocks read as zeros and `live` is false for them.
 template <int DT, int D>
-__device__ void stage_rows(const RowSource &s, int64_t row0, int64_t n_rows, float *lds,
-                           float (&x)[D], bool &live) {
-    const int lane = threadIdx.x & 63;
-    float *w_lds = lds + (threadIdx.x >> 6) * 64 * kPitch;
-    {
-        int64_t e;
-        live = row0 + lane < n_rows && row_elem(s, row0 + lane, D, e);
-    }
+__device__ __forceinline__ void load_row(const RowSource &s, int64_t r, float (&x)[D], bool &live) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    int64_t e;
+    live = row_elem(s, r, D, e);
 #pragma unroll
-    for (int c = 0; c < D / 32; ++c) {
+    for (int c = 0; c < D / 8; ++c) {
+        const int64_t el = e + 8 * c;
+        float v[8];
+        if constexpr (DT == AIR_KV_F32) {
+            const f32x4 *p = reinterpret_cast<const f32x4 *>((const float *)s.base + el);
+            const f32x4 a = p[0], b = p[1];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int g = lane + 64 * i;          // 8-column group g % 4 of row g / 4
-            const int rr = g >> 2, c8 = g & 3;
-            float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-            const int64_t r = row0 + rr;
-            if (r < n_rows) {
-                int64_t e;
-                if (row_elem(s, r, D, e)) {
-                    const int64_t el = e + 32 * c + 8 * c8;
-                    pio_u32x4 raw;
-                    load8<DT>(s.base, s.scales, el, s.scale_group ? el / s.scale_group : 0, v, &raw);
+            for (int j = 0; j < 4; ++j) { v[j] = a[j]; v[4 + j] = b[j]; }
+        } else if constexpr (DT == AIR_KV_BF16) {
+            const u32x4 w = *reinterpret_cast<const u32x4 *>((const uint16_t *)s.base + el);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[2 * j] = __uint_as_float(w[j] << 16);
+                v[2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+            }
+        } else {
+            const u32x2 w = *reinterpret_cast<const u32x2 *>((const uint8_t *)s.base + el);
+            const float sc = s.scales[el / s.scale_group];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t byte = (w[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+                const float val = DT == AIR_KV_INT8 ? (float)(int32_t)(int8_t)byte : fp8_decode(byte);
+                {
+#pragma clang fp contract(off)
+                    v[j] = val * sc;
                 }
             }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) w_lds[rr * kPitch + 8 * c8 + j] = v[j];
         }
-        __syncthreads();
 #pragma unroll
-        for (int j = 0; j < 32; ++j) x[32 * c + j] = w_lds[lane * kPitch + j];
-        __syncthreads();
+        for (int j = 0; j < 8; ++j) x[8 * c + j] = live ? v[j] : 0.0f;
     }
 }
 
@@ -114,16 +118,12 @@ __device__ __forceinline__ float l2_norm(const float (&x)[D]) {
 
 template <int DT, int D>
 __global__ __launch_bounds__(kThreads) void key_compress_kernel(CompressArgs a) {
-    __shared__ float lds[kWaves * 64 * kPitch];
     constexpr int W = (D + 63) / 64;
-    const int lane = threadIdx.x & 63;
-    for (int64_t base = (int64_t)blockIdx.x * kThreads; base < a.n_rows; base += (int64_t)gridDim.x * kThreads) {
-        const int64_t row0 = base + (threadIdx.x & ~63);
+    for (int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x; r < a.n_rows;
+         r += (int64_t)gridDim.x * kThreads) {
         float x[D];
         bool live;
-        stage_rows<DT, D>(a.src, row0, a.n_rows, lds, x, live);
-        const int64_t r = row0 + lane;
-        if (r >= a.n_rows) continue;
+        load_row<DT, D>(a.src, r, x, live);
         if (!live && a.errors && (r % a.src.rows_per_block) == 0) atomicAdd(a.errors, 1ull);
         float mean, mag;
         uint64_t bits[W];
@@ -153,22 +153,18 @@ __global__ __launch_bounds__(kThreads) void key_compress_kernel(CompressArgs a) 
 
 template <int DT, int D>
 __global__ __launch_bounds__(kThreads) void value_compress_kernel(CompressArgs a) {
-    __shared__ float lds[kWaves * 64 * kPitch];
-    const int lane = threadIdx.x & 63;
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    for (int64_t base = (int64_t)blockIdx.x * kThreads; base < a.n_rows; base += (int64_t)gridDim.x * kThreads) {
-        const int64_t row0 = base + (threadIdx.x & ~63);
+    for (int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x; r < a.n_rows;
+         r += (int64_t)gridDim.x * kThreads) {
         float x[D];
         bool live;
-        stage_rows<DT, D>(a.src, row0, a.n_rows, lds, x, live);
-        const int64_t r = row0 + lane;
-        if (r >= a.n_rows) continue;
+        load_row<DT, D>(a.src, r, x, live);
         if (!live && a.errors && (r % a.src.rows_per_block) == 0) atomicAdd(a.errors, 1ull);
         float lo = INFINITY, hi = -INFINITY;
 #pragma unroll
         for (int j = 0; j < D; ++j) {                  // (:198-199)
-            lo = rust_min(lo, x[j]);
-            hi = rust_max(hi, x[j]);
+            lo = fold_min(lo, x[j]);
+            hi = fold_max(hi, x[j]);
         }
         float scale;
         uint32_t q[D / 4];
@@ -176,18 +172,52 @@ __global__ __launch_bounds__(kThreads) void value_compress_kernel(CompressArgs a
 #pragma clang fp contract(off)
             const float range = hi - lo;
             scale = range > 0.0f ? range / 255.0f : 1.0f;   // (:201-202)
+            // round((v - min) / scale) (:204-209).  The quotient is the
+            // correctly rounded IEEE one either way: with y = RN(1 / scale)
+            // and q0 = RN(d * y) within an ulp, one correction q0 + (d - q0 *
+            // scale) * y, the remainder exact by fma, is RN(d / scale)
+            // (Markstein).  That needs scale and 1 / scale normal and no
+            // overflow (quotients here are at most ~255; ones that underflow
+            // round to code 0 either way); other rows (a subnormal or
+            // infinite scale, i.e. tiny or non-finite data) divide exactly.
+            const float y = 1.0f / scale;
+            auto codes = [&](auto quotient) {
 #pragma unroll
-            for (int j4 = 0; j4 < D / 4; ++j4) {
-                uint32_t w = 0;
+                for (int j4 = 0; j4 < D / 4; ++j4) {
+                    uint32_t w = 0;
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    float t = roundf((x[4 * j4 + k] - lo) / scale);   // (:204-209)
-                    t = t < 0.0f ? 0.0f : t;
-                    t = t > 255.0f ? 255.0f : t;
-                    const uint32_t c = (t != t) ? 0u : (uint32_t)t;   // `as u8`: NaN -> 0
-                    w |= c << (8 * k);
+                    for (int k = 0; k < 4; ++k) {
+                        float t = roundf(quotient(x[4 * j4 + k] - lo));
+                        t = t < 0.0f ? 0.0f : t;
+                        t = t > 255.0f ? 255.0f : t;
+                        const uint32_t c = (t != t) ? 0u : (uint32_t)t;   // `as u8`: NaN -> 0
+                        w |= c << (8 * k);
+                    }
+                    q[j4] = w;
                 }
-                q[j4] = w;
+            };
+            if (__builtin_isnormal(scale) && __builtin_isnormal(y)) {
+                // d = v - min >= 0 (or NaN) here, so round half away from zero
+                // is trunc + (fraction >= 0.5), and only the upper clamp and
+                // NaN need handling
+#pragma unroll
+                for (int j4 = 0; j4 < D / 4; ++j4) {
+                    uint32_t w = 0;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const float d = x[4 * j4 + k] - lo;
+                        const float q0 = d * y;
+                        const float rem = __builtin_fmaf(-q0, scale, d);
+                        const float quo = __builtin_fmaf(rem, y, q0);
+                        const float t = __builtin_truncf(quo);
+                        float r = t + (quo - t >= 0.5f ? 1.0f : 0.0f);
+                        r = r <= 255.0f ? r : (r == r ? 255.0f : 0.0f);
+                        w |= (uint32_t)r << (8 * k);
+                    }
+                    q[j4] = w;
+                }
+            } else {
+                codes([&](float d) { return d / scale; });
             }
         }
         if (!live) { scale = 0.0f; lo = 0.0f; for (int j = 0; j < D / 4; ++j) q[j] = 0; }
@@ -201,21 +231,25 @@ __global__ __launch_bounds__(kThreads) void value_compress_kernel(CompressArgs a
 
 template <int DT, int D>
 __global__ __launch_bounds__(kThreads) void qjl_compress_kernel(CompressArgs a) {
-    __shared__ float lds[kWaves * 64 * kPitch];
     __shared__ __align__(16) float proj[kProjRows * D];
-    const int lane = threadIdx.x & 63;
     const int m = a.proj_dim, W = (m + 63) / 64;
+    // every thread runs the same number of iterations (the projection rows
+    // are staged with barriers); rows past n_rows compute on zeros and store
+    // nothing
     for (int64_t base = (int64_t)blockIdx.x * kThreads; base < a.n_rows; base += (int64_t)gridDim.x * kThreads) {
-        const int64_t row0 = base + (threadIdx.x & ~63);
-        float x[D];
-        bool live;
-        stage_rows<DT, D>(a.src, row0, a.n_rows, lds, x, live);
-        const int64_t r = row0 + lane;
+        const int64_t r = base + threadIdx.x;
         const bool own = r < a.n_rows;
+        float x[D];
+        bool live = false;
+        if (own) load_row<DT, D>(a.src, r, x, live);
+        else
+#pragma unroll
+            for (int j = 0; j < D; ++j) x[j] = 0.0f;
         if (own && !live && a.errors && (r % a.src.rows_per_block) == 0) atomicAdd(a.errors, 1ull);
         uint64_t word = 0;
         for (int i0 = 0; i0 < m; i0 += kProjRows) {
             // rows i0 .. i0 + 31 of R (zeros past m)
+            __syncthreads();
             for (int e = threadIdx.x; e < kProjRows * D; e += kThreads) {
                 const int i = i0 + e / D;
                 proj[e] = i < m ? a.proj[(int64_t)i * D + e % D] : 0.0f;
@@ -238,7 +272,6 @@ __global__ __launch_bounds__(kThreads) void qjl_compress_kernel(CompressArgs a) 
                     word = 0;
                 }
             }
-            __syncthreads();
         }
         if (own) a.f0[r] = live ? l2_norm<D>(x) : 0.0f;
     }

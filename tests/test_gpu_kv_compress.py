@@ -46,6 +46,14 @@ def _rows(n, d, seed):
     rng = np.random.default_rng(seed)
     x = rng.standard_normal((n, d)).astype(np.float32)
     x[: n // 4] *= np.float32(37.0)
+    # magnitudes from 1e-38 to 1e36 (subnormal and huge scales), offsets far
+    # larger than the spread (tiny ranges), and exact integer grids whose
+    # quotients land on .5 ties
+    mags = (10.0 ** rng.uniform(-38, 36, size=n // 4)).astype(np.float32)
+    x[n // 4: n // 2] *= mags[:, None]
+    x[n // 2: n // 2 + n // 8] += np.float32(1000.0)
+    a, b = n // 2 + n // 8, n // 2 + n // 4
+    x[a:b] = rng.integers(-300, 300, size=(b - a, d)).astype(np.float32) * np.float32(0.5)
     return np.concatenate([_edge_rows(d), x])
 
 
