@@ -12,8 +12,8 @@
 // consecutive work items of it, item = token block * group + head of the
 // group, a token block being 32 query rows.  With group 4 the four waves are
 // the four query heads of one token block, so every K/V tile staged in LDS
-// serves the whole GQA group.  Workgroups take their items heaviest first
-// (the last token blocks see the most keys).
+// serves the whole GQA group.  Workgroups start in decreasing order of the
+// keys their heaviest wave needs (prefill_slot below).
 //
 // Per 32-key tile, per wave (32 query rows):
 //   S^T = K . Q^T   v_mfma_f32_32x32x16_bf16, M = 32 keys, N = 32 queries,
@@ -30,18 +30,25 @@
 //                   tiles), N = 32 queries, K = 16 keys per step.  P^T is used
 //                   where the S^T product left it: its B-operand keys are
 //                   those of the C layout, keys (8*(i/4) + 4*(lane/32) + i%4)
-//                   for registers i = 8*step .. +8.  V is stored to LDS
-//                   transposed, V^T[d][c], with the key of column c = c with
-//                   bits 2 and 3 swapped, so a lane's eight keys of one step
-//                   are one contiguous 16-byte read.  P is split into hi + lo
+//                   for registers i = 8*step .. +8.  P is split into hi + lo
 //                   bf16 halves (~16 mantissa bits): bf16 probabilities alone
 //                   leave ~1e-3 relative error at these lengths.
 //
-// K/V tiles are double-buffered in LDS and two tiles ahead in registers: the
-// global loads of tile t + 2 are issued before tile t is computed, and tile
-// t + 1 is written to the other LDS buffer after it, with one barrier per
-// tile.  Keys past the sequence and out-of-pool table
-// entries are staged as zeros (stale page bytes may hold non-finite values).
+// bf16 pages (prefill_bf16_kernel): K and V tiles are staged row-major in
+// three LDS stages, 16-byte chunks XOR-swizzled by row; the V^T operand comes
+// from two transposing reads (ds_read_b64_tr_b16) per 16 keys.  The loop is
+// software-pipelined: the S^T product of tile t + 1 is issued before the
+// softmax and PV products of tile t, tile t + 2 is written to LDS after them,
+// and the page loads of tile t + 3 are in flight in registers, with one
+// barrier per tile.
+//
+// 1-byte pages (prefill_kernel): codes are dequantized to bf16 on the way to
+// LDS; V is stored transposed, V^T[d][c] with the key of column c = c with
+// bits 2 and 3 swapped, so a lane's eight keys of one step are one contiguous
+// 16-byte read.  Two LDS buffers, page loads two tiles ahead in registers.
+//
+// Keys past the sequence and out-of-pool table entries are staged as zeros
+// (stale page bytes may hold non-finite values).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -173,25 +180,139 @@ __device__ __forceinline__ u32x4 to_bf16x8(const Raw8<DT> &r) {
     }
 }
 
-template <int BS, bool QF32, int DT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AIRKV_PREFILL_WAVES_PER_EU)))
-void prefill_kernel(PrefillArgs a) {
-    __shared__ __align__(16) uint8_t smem[2 * STAGE];
-    const int b = blockIdx.x, kh = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+// Dispatch order.  The grid is one-dimensional: n_kv_heads workgroups for
+// each of the batch * nz (sequence, slot) items, and the hardware starts
+// workgroups in index order.  Slot z of sequence b serves that sequence's
+// work group n_wg - 1 - z (and every nz-th one below it), whose heaviest wave
+// needs the keys up to its last query row.  Grid row r takes the item of
+// rank r when items are ordered by that key count, decreasing (in buckets of
+// an eighth of an octave; ties by sequence, then slot), so long work starts
+// first and short work fills the launch's tail.  Every item gets exactly one
+// rank whatever the lengths hold.  Batches above kRankCap sequences or
+// kRankItems items are taken slot by slot (slot slowest), without ranking.
+constexpr int kRankCap = 2048;
+constexpr int kRankItems = 64 * kThreads;
+constexpr int kRankLdsBytes = (kThreads + kWaves + 2 + 2 * kRankCap) * 4;
+
+struct PrefillSlot {
+    int b, kh, z, nz;
+};
+
+__device__ __forceinline__ int len_bucket(int64_t len) {   // 0 .. 248, monotone in len
+    if (len <= 0) return 0;
+    const uint32_t x = len > 0x7fffffff ? 0x7fffffffu : (uint32_t)len;
+    const int e = 31 - __builtin_clz(x);
+    const int m = e >= 3 ? (int)(x >> (e - 3)) & 7 : (int)(x << (3 - e)) & 7;
+    return 1 + 8 * e + m;
+}
+
+// Exclusive prefix sum over the workgroup's threads in thread order; wsum
+// holds kWaves ints of LDS.  Contains barriers: every thread calls it.
+__device__ __forceinline__ int block_exclusive_scan(int v, int *wsum) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < wave; ++w) base += wsum[w];
+    __syncthreads();
+    return base + incl - v;
+}
+
+// Keys the heaviest wave of slot z of a sequence needs (0: no work).
+__device__ __forceinline__ int64_t slot_keys(int64_t len, int64_t qlen, int G, int z) {
+    if (qlen <= 0 || len < qlen) return 0;
+    const int64_t n_items = (qlen + kRows - 1) / kRows * G;
+    const int64_t n_wg = (n_items + kWaves - 1) / kWaves;
+    if (z >= n_wg) return 0;
+    const int64_t wi = n_wg - 1 - z;
+    const int64_t last = wi * kWaves + kWaves - 1 < n_items ? wi * kWaves + kWaves - 1 : n_items - 1;
+    const int64_t rows = (last / G + 1) * kRows;
+    return len - qlen + (rows < qlen ? rows : qlen);
+}
+
+// lds: at least kThreads + kWaves + 2 + 2 * kRankCap ints, free for the duration.
+__device__ PrefillSlot prefill_slot(const PrefillArgs &a, int *lds) {
+    const int tid = threadIdx.x;
+    const int nz = (int)(gridDim.x / ((unsigned)a.batch * (unsigned)a.n_kv_heads));
+    const int row = (int)(blockIdx.x / (unsigned)a.n_kv_heads);
+    PrefillSlot sl;
+    sl.kh = (int)(blockIdx.x % (unsigned)a.n_kv_heads);
+    sl.nz = nz;
+    if (a.batch == 1 || a.batch > kRankCap || (int64_t)a.batch * nz > kRankItems) {
+        // (one sequence: its slots are already in decreasing order)
+        sl.b = row % a.batch;
+        sl.z = row / a.batch;
+        return sl;
+    }
+    int *hist = lds, *wsum = lds + kThreads, *sel = lds + kThreads + kWaves;
+    int *slen = sel + 2, *sq = slen + kRankCap;
+    hist[tid] = 0;
+    for (int i = tid; i < a.batch; i += kThreads) {
+        slen[i] = a.lens[i];
+        const int64_t ql = (int64_t)a.cu_q[i + 1] - a.cu_q[i];
+        sq[i] = ql < 0 ? 0 : ql > 0x7fffffff ? 0x7fffffff : (int)ql;
+    }
+    __syncthreads();
+    const int n_it = a.batch * nz;
+    const int chunk = (n_it + kThreads - 1) / kThreads;
+    const int i0 = tid * chunk, i1 = i0 + chunk < n_it ? i0 + chunk : n_it;
+    auto bucket_of = [&](int i) {
+        const int bb = i / nz;
+        return len_bucket(slot_keys(slen[bb], sq[bb], a.group, i - bb * nz));
+    };
+    for (int i = i0; i < i1; ++i) atomicAdd(&hist[bucket_of(i)], 1);
+    __syncthreads();
+    // buckets in decreasing order: thread t takes bucket kThreads - 1 - t
+    const int bucket = kThreads - 1 - tid;
+    const int cnt = hist[bucket];
+    const int start = block_exclusive_scan(cnt, wsum);
+    if (row >= start && row < start + cnt) {
+        sel[0] = bucket;
+        sel[1] = row - start;
+    }
+    __syncthreads();
+    const int want = sel[0], j = sel[1];
+    // the j-th item (index order) of bucket want: thread t scans its chunk
+    int c = 0;
+    for (int i = i0; i < i1; ++i) c += bucket_of(i) == want;
+    const int before = block_exclusive_scan(c, wsum);
+    if (j >= before && j < before + c) {
+        int k = j - before;
+        for (int i = i0; i < i1; ++i)
+            if (bucket_of(i) == want && k-- == 0) sel[0] = i;
+    }
+    __syncthreads();
+    const int item = sel[0];
+    sl.b = item / nz;
+    sl.z = item - sl.b * nz;
+    __syncthreads();   // the caller reuses the LDS
+    return sl;
+}
+
+// Per-(sequence, kv head) setup shared by the prefill kernels: reads the
+// sequence's rows and length, counts (once) an inconsistent sequence and
+// every out-of-pool table entry within its length, zero-fills the rows of an
+// inconsistent sequence, and returns whether the workgroup has rows to
+// compute.  Uniform per workgroup.
+template <int BS>
+__device__ bool prefill_begin(const PrefillArgs &a, const PrefillSlot &sl, int32_t &q0, int &qlen, int64_t &len) {
+    const int b = sl.b, kh = sl.kh, tid = threadIdx.x;
     const int G = a.group;
     const int64_t max_len = (int64_t)a.max_blocks * BS;
-    const int32_t q0 = a.cu_q[b], q1 = a.cu_q[b + 1];
-    const int64_t len = a.lens[b];
-    const int qlen = q1 - q0;
+    q0 = a.cu_q[b];
+    const int32_t q1 = a.cu_q[b + 1];
+    len = a.lens[b];
+    qlen = q1 - q0;
     const bool rows_ok = q0 >= 0 && q1 >= q0 && q1 <= a.total_q;
     const bool seq_ok = rows_ok && len >= 0 && len <= max_len && qlen <= len;
     const int32_t *tbl = a.tables + (int64_t)b * a.max_blocks;
-
-    if (blockIdx.z == 0 && kh == 0) {
-        // Each invalid sequence and each out-of-pool table entry within its
-        // length is counted once.
+    if (sl.z == 0 && kh == 0) {
         if (!seq_ok) {
             if (tid == 0) atomicAdd(a.errors, 1ull);
         } else if (qlen > 0) {
@@ -203,7 +324,7 @@ void prefill_kernel(PrefillArgs a) {
     }
     if (!seq_ok) {
         // rows of a sequence whose lengths are inconsistent become zeros
-        if (rows_ok && blockIdx.z == 0) {
+        if (rows_ok && sl.z == 0) {
             const int64_t n = (int64_t)qlen * G * D;
             for (int64_t i = tid; i < n; i += kThreads) {
                 const int64_t r = i / (G * D), e = i % (G * D);
@@ -212,9 +333,26 @@ void prefill_kernel(PrefillArgs a) {
                 else ((uint16_t *)a.out)[idx] = 0;
             }
         }
-        return;
+        return false;
     }
-    if (qlen <= 0) return;
+    return qlen > 0;
+}
+
+template <int BS, bool QF32, int DT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AIRKV_PREFILL_WAVES_PER_EU)))
+void prefill_kernel(PrefillArgs a) {
+    __shared__ __align__(16) uint8_t smem[2 * STAGE];
+    static_assert(sizeof(smem) >= kRankLdsBytes, "dispatch ranking needs the tile LDS");
+    const PrefillSlot sl = prefill_slot(a, reinterpret_cast<int *>(smem));
+    const int b = sl.b, kh = sl.kh;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = a.group;
+    int32_t q0;
+    int qlen;
+    int64_t len;
+    if (!prefill_begin<BS>(a, sl, q0, qlen, len)) return;
+    const int32_t *tbl = a.tables + (int64_t)b * a.max_blocks;
 
     const int q_offset = (int)(len - qlen);
     const int ntb = (qlen + kRows - 1) / kRows;
@@ -323,7 +461,7 @@ void prefill_kernel(PrefillArgs a) {
                 __builtin_amdgcn_perm(v1[j >> 1], v0[j >> 1], (j & 1) ? 0x07060302u : 0x05040100u);
     };
 
-    for (int w = blockIdx.z; w < n_wg; w += gridDim.z) {
+    for (int w = sl.z; w < n_wg; w += sl.nz) {
         const int wi = n_wg - 1 - w;                   // heaviest work first
         const int item = wi * kWaves + wave;
         const bool wvalid = item < n_items;
@@ -504,12 +642,311 @@ void prefill_kernel(PrefillArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 pages: three LDS stages and tiles software-pipelined inside each wave.
+//
+// K and V tiles are staged row-major (256-byte rows); the 16-byte chunk c of
+// row r sits at chunk c ^ swz(r), swz swapping r's two low 2-bit fields,
+// which makes the K operand reads, the staging stores and the transposing V
+// reads bank-conflict free.  The V^T operand comes from two transposing
+// reads (ds_read_b64_tr_b16) per k-step: within each 16-lane group lane j
+// receives element j % 4 of the 8 bytes addressed by lanes 4k + j / 4, so
+// lane 16G + s points at V[kb + s/4][dblk + 4(s%4)] and receives V[kb + k][dblk
+// + s], k = 0..3 -- four consecutive keys of one head_dim column, which are
+// exactly the keys the S^T accumulator layout hands to P^T: keys 16 st + 4 hh
+// + 0..3 and 16 st + 8 + 4 hh + 0..3 for lane half hh.
+//
+// Iteration t: the QK^T products of tile t + 1 are issued first (their K
+// tile was staged an iteration earlier), then tile t's softmax runs on the
+// vector ALUs while the matrix cores work, then tile t's PV products; tile
+// t + 2 (loaded into registers an iteration earlier) is staged into the
+// third LDS buffer and the loads of tile t + 3 are issued after the barrier.
+// ---------------------------------------------------------------------------
+constexpr int kStages = 3;
+constexpr int TILE_BYTES = kKeys * D * 2;    // one K or V tile, bf16
+constexpr int STAGE_BYTES = 2 * TILE_BYTES;  // K then V
+
+__device__ __forceinline__ int tile_swz(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
+// byte offset of 16-byte chunk c of row r inside a staged tile
+__device__ __forceinline__ int tile_off(int r, int c) { return r * (D * 2) + ((c ^ tile_swz(r)) << 4); }
+
+template <int BS, bool QF32>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AIRKV_PREFILL_WAVES_PER_EU)))
+void prefill_bf16_kernel(PrefillArgs a) {
+    __shared__ __align__(16) uint8_t smem[kStages * STAGE_BYTES];
+    static_assert(sizeof(smem) >= kRankLdsBytes, "dispatch ranking needs the tile LDS");
+    const PrefillSlot sl = prefill_slot(a, reinterpret_cast<int *>(smem));
+    const int b = sl.b, kh = sl.kh;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = a.group;
+    int32_t q0;
+    int qlen;
+    int64_t len;
+    if (!prefill_begin<BS>(a, sl, q0, qlen, len)) return;
+    const int32_t *tbl = a.tables + (int64_t)b * a.max_blocks;
+    const int q_offset = (int)(len - qlen);
+    const int ntb = (qlen + kRows - 1) / kRows;
+    const int n_items = ntb * G;
+    const int n_wg = (n_items + kWaves - 1) / kWaves;
+    const int r32 = lane & 31, hh = lane >> 5;
+
+    // Staging: thread covers the 16-byte chunk tid % 16 of key rows tid / 16
+    // and 16 + tid / 16, for K and V alike (constant offsets inside a page).
+    constexpr int PAGE_BYTES = BS * D * 2;
+    int g_off[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) g_off[i] = ((((tid >> 4) + 16 * i) % BS) * D + (tid & 15) * 8) * 2;
+    struct TileRegs {
+        u32x4 k[2], v[2];
+        int kt;
+        bool ok0, ok1;
+    };
+    int32_t nb0 = 0, nb1 = 0;          // block ids of the next tile to load (fetched a tile ahead)
+    auto fetch_ids = [&](int t, int kend) {
+        const int last = (kend - 1) / BS;
+        const int j0 = (t * kKeys) / BS;
+        nb0 = tbl[j0 < last ? j0 : last];
+        if constexpr (BS == 16) nb1 = tbl[j0 + 1 < last ? j0 + 1 : last];
+        else nb1 = nb0;
+    };
+    auto load_tile = [&](int t, TileRegs &R) {
+        const int32_t b0 = __builtin_amdgcn_readfirstlane(nb0), b1 = __builtin_amdgcn_readfirstlane(nb1);
+        R.kt = t * kKeys;
+        R.ok0 = b0 >= 0 && b0 < a.num_blocks;
+        R.ok1 = b1 >= 0 && b1 < a.num_blocks;
+        const int64_t row0 = ((int64_t)(R.ok0 ? b0 : 0) * a.n_kv_heads + kh) * BS;
+        const int64_t row1 = ((int64_t)(R.ok1 ? b1 : 0) * a.n_kv_heads + kh) * BS;
+        const __amdgpu_buffer_rsrc_t k0 = page_rsrc(a.k_pages, row0 * D * 2, PAGE_BYTES);
+        const __amdgpu_buffer_rsrc_t v0 = page_rsrc(a.v_pages, row0 * D * 2, PAGE_BYTES);
+        const __amdgpu_buffer_rsrc_t k1 = page_rsrc(a.k_pages, row1 * D * 2, PAGE_BYTES);
+        const __amdgpu_buffer_rsrc_t v1 = page_rsrc(a.v_pages, row1 * D * 2, PAGE_BYTES);
+        R.k[0] = __builtin_amdgcn_raw_buffer_load_b128(k0, g_off[0], 0, 0);
+        R.v[0] = __builtin_amdgcn_raw_buffer_load_b128(v0, g_off[0], 0, 0);
+        R.k[1] = __builtin_amdgcn_raw_buffer_load_b128(BS == 16 ? k1 : k0, g_off[1], 0, 0);
+        R.v[1] = __builtin_amdgcn_raw_buffer_load_b128(BS == 16 ? v1 : v0, g_off[1], 0, 0);
+    };
+    // Keys past the sequence and rows of out-of-pool blocks are staged as
+    // zeros (stale page bytes may hold non-finite values); only the tiles
+    // that hold such keys (a uniform test) pay for the selects.
+    auto stage_tile = [&](int slot, TileRegs &R, int kend) {
+        uint8_t *ks = smem + slot * STAGE_BYTES;
+        uint8_t *vs = ks + TILE_BYTES;
+        if (!(R.ok0 && R.ok1 && R.kt + kKeys <= kend)) {
+            const u32x4 zero = {0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const bool okp = (BS == 16 && i == 1) ? R.ok1 : R.ok0;
+                const bool live = R.kt + (tid >> 4) + 16 * i < kend && okp;
+                R.k[i] = live ? R.k[i] : zero;
+                R.v[i] = live ? R.v[i] : zero;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int off = tile_off((tid >> 4) + 16 * i, tid & 15);
+            *reinterpret_cast<u32x4 *>(ks + off) = R.k[i];
+            *reinterpret_cast<u32x4 *>(vs + off) = R.v[i];
+        }
+    };
+
+    for (int w = sl.z; w < n_wg; w += sl.nz) {
+        const int wi = n_wg - 1 - w;                   // heaviest work first
+        const int item = wi * kWaves + wave;
+        const bool wvalid = item < n_items;
+        const int tb = (wvalid ? item : n_items - 1) / G;
+        const int g = (wvalid ? item : n_items - 1) % G;
+        const int h = kh * G + g;
+        const int r0 = tb * kRows;
+        const int last_item = (wi * kWaves + kWaves - 1 < n_items ? wi * kWaves + kWaves - 1 : n_items - 1);
+        const int tb_last = last_item / G;
+        const int rows_last = (tb_last + 1) * kRows < qlen ? (tb_last + 1) * kRows : qlen;
+        const int kend = q_offset + rows_last;          // keys the workgroup needs (<= len)
+        const int rows_w = r0 + kRows < qlen ? r0 + kRows : qlen;
+        const int nt_w = (q_offset + rows_w + kKeys - 1) / kKeys;   // tiles this wave needs
+        const int nt = (kend + kKeys - 1) / kKeys;
+
+        const int qrow = r0 + r32 < qlen ? r0 + r32 : qlen - 1;
+        const int qpos = q_offset + qrow;
+        u32x4 qhi[D / 16], qlo[D / 16];
+        {
+            const int64_t qbase = ((int64_t)(q0 + qrow) * a.n_q_heads + h) * D + 8 * hh;
+#pragma unroll
+            for (int ks = 0; ks < D / 16; ++ks) {
+                if constexpr (QF32) {
+                    const f32x4 *qp = reinterpret_cast<const f32x4 *>((const float *)a.q + qbase + 16 * ks);
+                    const f32x4 x0 = qp[0], x1 = qp[1];
+                    uint32_t hv[4], lv[4];
+                    split_pair(x0[0], x0[1], hv[0], lv[0]);
+                    split_pair(x0[2], x0[3], hv[1], lv[1]);
+                    split_pair(x1[0], x1[1], hv[2], lv[2]);
+                    split_pair(x1[2], x1[3], hv[3], lv[3]);
+                    qhi[ks] = u32x4{hv[0], hv[1], hv[2], hv[3]};
+                    qlo[ks] = u32x4{lv[0], lv[1], lv[2], lv[3]};
+                } else {
+                    qhi[ks] = *reinterpret_cast<const u32x4 *>((const uint16_t *)a.q + qbase + 16 * ks);
+                    qlo[ks] = u32x4{0, 0, 0, 0};
+                }
+            }
+            // consumed here so no vector-memory wait lands inside the tile loop
+#pragma unroll
+            for (int ks = 0; ks < D / 16; ++ks) {
+                asm volatile("" ::"v"(qhi[ks]));
+                if constexpr (QF32) asm volatile("" ::"v"(qlo[ks]));
+            }
+        }
+
+        f32x16 acc[D / 32];
+#pragma unroll
+        for (int n = 0; n < D / 32; ++n)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[n][i] = 0.0f;
+        float m_run = -INFINITY, l_run = 0.0f;
+
+        auto qk = [&](int slot) {
+            const uint8_t *ks_ = smem + slot * STAGE_BYTES;
+            f32x16 s;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < D / 16; ++ks) {
+                const u32x4 kA = *reinterpret_cast<const u32x4 *>(ks_ + tile_off(r32, 2 * ks + hh));
+                s = mfma32(kA, qhi[ks], s);
+                if constexpr (QF32) s = mfma32(kA, qlo[ks], s);
+            }
+            return s;
+        };
+        // softmax of tile t (scores s, S^T layout) and its PV products
+        auto softmax_pv = [&](int t, int slot, const f32x16 &s) {
+            const int kt = t * kKeys;
+            const bool diag = kt + kKeys - 1 > q_offset + r0;
+            const int kq = qpos - kt - 4 * hh;
+            float sc[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sc[i] = s[i];
+            if (diag) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) sc[i] = 8 * (i >> 2) + (i & 3) <= kq ? sc[i] : -INFINITY;
+            }
+            float mt = fmaxf(sc[0], sc[1]);
+#pragma unroll
+            for (int i = 2; i < 16; ++i) mt = fmaxf(mt, sc[i]);
+            mt = fmaxf(mt, __shfl_xor(mt, 32)) * a.scale_log2;
+            if (__ballot(mt > m_run + 8.0f) != 0ull) {
+                const float m_new = fmaxf(m_run, mt);
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);   // 0 on the first tile
+                l_run *= alpha;
+#pragma unroll
+                for (int n = 0; n < D / 32; ++n) acc[n] *= alpha;
+                m_run = m_new;
+            }
+            float p[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i)   // masked: exp2(-inf) = 0
+                p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], a.scale_log2, -m_run));
+            float ls = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) ls += p[i];
+            l_run += ls;
+            const uint8_t *vs_ = smem + slot * STAGE_BYTES + TILE_BYTES;
+            typedef short s16x4 __attribute__((ext_vector_type(4)));
+            const int grp = lane >> 4, sl = lane & 15;
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                uint32_t hv[4], lv[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) split_pair(p[8 * st + 2 * j], p[8 * st + 2 * j + 1], hv[j], lv[j]);
+                const u32x4 phi = {hv[0], hv[1], hv[2], hv[3]}, plo = {lv[0], lv[1], lv[2], lv[3]};
+                const int vrow = 16 * st + 4 * hh + (sl >> 2);           // keys kb .. kb + 3, then + 8
+#pragma unroll
+                for (int n = 0; n < D / 32; ++n) {
+                    const int col = 32 * n + 16 * (grp & 1) + 4 * (sl & 3);   // bf16 column of the 8 bytes
+                    const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) s16x4 *)(vs_ + tile_off(vrow, col >> 3) + (col & 7) * 2));
+                    const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) s16x4 *)(vs_ + tile_off(vrow + 8, col >> 3) + (col & 7) * 2));
+                    const u32x2 a0 = __builtin_bit_cast(u32x2, t0), a1 = __builtin_bit_cast(u32x2, t1);
+                    const u32x4 va = {a0[0], a0[1], a1[0], a1[1]};
+                    acc[n] = mfma32(va, phi, acc[n]);
+                    acc[n] = mfma32(va, plo, acc[n]);
+                }
+            }
+        };
+
+        TileRegs R;
+        fetch_ids(0, kend);
+        load_tile(0, R);
+        fetch_ids(1, kend);
+        stage_tile(0, R, kend);
+        if (nt > 1) {
+            load_tile(1, R);
+            fetch_ids(2, kend);
+            stage_tile(1, R, kend);
+        }
+        if (nt > 2) {
+            load_tile(2, R);
+            fetch_ids(3, kend);
+        }
+        __syncthreads();
+        f32x16 s_cur = qk(0);
+        int slot_t = 0;
+        for (int t = 0; t < nt; ++t) {
+            const int slot_n = slot_t == kStages - 1 ? 0 : slot_t + 1;         // tile t + 1
+            const int slot_nn = slot_n == kStages - 1 ? 0 : slot_n + 1;        // tile t + 2
+            f32x16 s_next = s_cur;
+            if (wvalid && t + 1 < nt_w) s_next = qk(slot_n);
+            if (wvalid && t < nt_w) softmax_pv(t, slot_t, s_cur);
+            if (t + 2 < nt) stage_tile(slot_nn, R, kend);
+            __syncthreads();
+            if (t + 3 < nt) {
+                load_tile(t + 3, R);
+                fetch_ids(t + 4, kend);
+            }
+            s_cur = s_next;
+            slot_t = slot_n;
+        }
+
+        if (wvalid && r0 + r32 < qlen) {
+            const float l = l_run + __shfl_xor(l_run, 32);
+            const float inv = 1.0f / l;
+            const int64_t orow = ((int64_t)(q0 + r0 + r32) * a.n_q_heads + h) * D + 4 * hh;
+            if (a.out_dtype == AIR_KV_F32) {
+#pragma unroll
+                for (int n = 0; n < D / 32; ++n)
+#pragma unroll
+                    for (int i4 = 0; i4 < 4; ++i4)
+                        *reinterpret_cast<f32x4 *>((float *)a.out + orow + 32 * n + 8 * i4) =
+                            f32x4{acc[n][4 * i4], acc[n][4 * i4 + 1], acc[n][4 * i4 + 2], acc[n][4 * i4 + 3]} * inv;
+            } else {
+#pragma unroll
+                for (int n = 0; n < D / 32; ++n)
+#pragma unroll
+                    for (int i4 = 0; i4 < 4; ++i4) {
+                        const f32x2 x = f32x2{acc[n][4 * i4], acc[n][4 * i4 + 1]} * inv;
+                        const f32x2 y = f32x2{acc[n][4 * i4 + 2], acc[n][4 * i4 + 3]} * inv;
+                        *reinterpret_cast<u32x2 *>((uint16_t *)a.out + orow + 32 * n + 8 * i4) =
+                            u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2)),
+                                  __builtin_bit_cast(uint32_t, __builtin_convertvector(y, bf16x2))};
+                    }
+            }
+        }
+        __syncthreads();      // the next work item restages every LDS buffer
+    }
+}
+
 template <int BS, int DT>
 hipError_t launch_dt(const PrefillArgs &a, hipStream_t s, dim3 grid) {
-    if (a.q_dtype == AIR_KV_F32)
-        hipLaunchKernelGGL((prefill_kernel<BS, true, DT>), grid, dim3(kThreads), 0, s, a);
-    else
-        hipLaunchKernelGGL((prefill_kernel<BS, false, DT>), grid, dim3(kThreads), 0, s, a);
+    if constexpr (DT == AIR_KV_BF16) {
+        if (a.q_dtype == AIR_KV_F32)
+            hipLaunchKernelGGL((prefill_bf16_kernel<BS, true>), grid, dim3(kThreads), 0, s, a);
+        else
+            hipLaunchKernelGGL((prefill_bf16_kernel<BS, false>), grid, dim3(kThreads), 0, s, a);
+    } else {
+        if (a.q_dtype == AIR_KV_F32)
+            hipLaunchKernelGGL((prefill_kernel<BS, true, DT>), grid, dim3(kThreads), 0, s, a);
+        else
+            hipLaunchKernelGGL((prefill_kernel<BS, false, DT>), grid, dim3(kThreads), 0, s, a);
+    }
     return hipGetLastError();
 }
 
@@ -533,13 +970,15 @@ bool prefill_supported(int dtype, int head_dim, int block_size, int scale_group)
 
 hipError_t launch_prefill(const PrefillArgs &a, int dtype, int block_size, int32_t max_q_len,
                           hipStream_t s) {
-    // grid: x = sequence, y = kv head, z = workgroups per (sequence, kv head)
-    // sized for max_q_len; the kernel strides over z, so a sequence longer
-    // than max_q_len is still covered completely.
+    // one-dimensional grid, n_kv_heads workgroups per (sequence, slot), nz
+    // slots per sequence sized for max_q_len; the kernel strides over its
+    // slots, so a sequence longer than max_q_len is still covered completely.
     const int64_t ntb = ((int64_t)(max_q_len > 0 ? max_q_len : 1) + kRows - 1) / kRows;
     int64_t nz = (ntb * a.group + kWaves - 1) / kWaves;
-    nz = nz > 65535 ? 65535 : nz;
-    const dim3 grid((unsigned)a.batch, (unsigned)a.n_kv_heads, (unsigned)nz);
+    const int64_t cap = (int64_t)0x7fffffff / ((int64_t)a.batch * a.n_kv_heads);
+    nz = nz > cap ? cap : nz;
+    if (nz < 1) return hipErrorInvalidConfiguration;
+    const dim3 grid((unsigned)((int64_t)a.batch * a.n_kv_heads * nz));
     return block_size == 16 ? launch_bs<16>(a, dtype, s, grid) : launch_bs<32>(a, dtype, s, grid);
 }
 
