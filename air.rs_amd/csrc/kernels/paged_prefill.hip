@@ -645,10 +645,9 @@ void prefill_kernel(PrefillArgs a) {
 // ---------------------------------------------------------------------------
 // bf16 pages: three LDS stages and tiles software-pipelined inside each wave.
 //
-// K and V tiles are staged row-major (256-byte rows); the 16-byte chunk c of
-// row r sits at chunk c ^ swz(r), swz swapping r's two low 2-bit fields,
-// which makes the K operand reads, the staging stores and the transposing V
-// reads bank-conflict free.  The V^T operand comes from two transposing
+// K and V tiles are staged row-major at padded pitches (below), which makes
+// the K operand reads, the staging stores and the transposing V reads
+// bank-conflict free.  The V^T operand comes from two transposing
 // reads (ds_read_b64_tr_b16) per k-step: within each 16-lane group lane j
 // receives element j % 4 of the 8 bytes addressed by lanes 4k + j / 4, so
 // lane 16G + s points at V[kb + s/4][dblk + 4(s%4)] and receives V[kb + k][dblk
@@ -663,12 +662,16 @@ void prefill_kernel(PrefillArgs a) {
 // third LDS buffer and the loads of tile t + 3 are issued after the barrier.
 // ---------------------------------------------------------------------------
 constexpr int kStages = 3;
-constexpr int TILE_BYTES = kKeys * D * 2;    // one K or V tile, bf16
-constexpr int STAGE_BYTES = 2 * TILE_BYTES;  // K then V
+template <int N> struct Int { static constexpr int value = N; };
+// Padded row pitches: K rows 272 bytes (consecutive rows start 4 banks
+// apart, so the 16 rows of a K operand read hit 16 distinct 16-byte bank
+// groups), V rows 320 bytes (rows start 16 banks apart, so the 4 rows x 64
+// bytes of a transposing read cover the 64 banks once).  Every LDS address
+// is then one per-lane register plus an immediate.
+constexpr int BF_KPITCH = D * 2 + 16, BF_VPITCH = D * 2 + 64;
+constexpr int KTILE_BYTES = kKeys * BF_KPITCH, VTILE_BYTES = kKeys * BF_VPITCH;
+constexpr int STAGE_BYTES = KTILE_BYTES + VTILE_BYTES;   // K then V
 
-__device__ __forceinline__ int tile_swz(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
-// byte offset of 16-byte chunk c of row r inside a staged tile
-__device__ __forceinline__ int tile_off(int r, int c) { return r * (D * 2) + ((c ^ tile_swz(r)) << 4); }
 
 template <int BS, bool QF32>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AIRKV_PREFILL_WAVES_PER_EU)))
@@ -731,7 +734,7 @@ void prefill_bf16_kernel(PrefillArgs a) {
     // that hold such keys (a uniform test) pay for the selects.
     auto stage_tile = [&](int slot, TileRegs &R, int kend) {
         uint8_t *ks = smem + slot * STAGE_BYTES;
-        uint8_t *vs = ks + TILE_BYTES;
+        uint8_t *vs = ks + KTILE_BYTES;
         if (!(R.ok0 && R.ok1 && R.kt + kKeys <= kend)) {
             const u32x4 zero = {0, 0, 0, 0};
 #pragma unroll
@@ -744,9 +747,9 @@ void prefill_bf16_kernel(PrefillArgs a) {
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const int off = tile_off((tid >> 4) + 16 * i, tid & 15);
-            *reinterpret_cast<u32x4 *>(ks + off) = R.k[i];
-            *reinterpret_cast<u32x4 *>(vs + off) = R.v[i];
+            const int row = (tid >> 4) + 16 * i;
+            *reinterpret_cast<u32x4 *>(ks + row * BF_KPITCH + (tid & 15) * 16) = R.k[i];
+            *reinterpret_cast<u32x4 *>(vs + row * BF_VPITCH + (tid & 15) * 16) = R.v[i];
         }
     };
 
@@ -763,8 +766,11 @@ void prefill_bf16_kernel(PrefillArgs a) {
         const int rows_last = (tb_last + 1) * kRows < qlen ? (tb_last + 1) * kRows : qlen;
         const int kend = q_offset + rows_last;          // keys the workgroup needs (<= len)
         const int rows_w = r0 + kRows < qlen ? r0 + kRows : qlen;
-        const int nt_w = (q_offset + rows_w + kKeys - 1) / kKeys;   // tiles this wave needs
-        const int nt = (kend + kKeys - 1) / kKeys;
+        // uniform per wave (nt per workgroup): kept in scalar registers so the
+        // guards below are scalar branches
+        const int nt_w = __builtin_amdgcn_readfirstlane(wvalid ? (q_offset + rows_w + kKeys - 1) / kKeys : 0);
+        const int nt = __builtin_amdgcn_readfirstlane((kend + kKeys - 1) / kKeys);
+        const int diag_kt = __builtin_amdgcn_readfirstlane(q_offset + r0 - kKeys + 1);   // first masked tile start
 
         const int qrow = r0 + r32 < qlen ? r0 + r32 : qlen - 1;
         const int qpos = q_offset + qrow;
@@ -810,21 +816,17 @@ void prefill_bf16_kernel(PrefillArgs a) {
             for (int i = 0; i < 16; ++i) s[i] = 0.0f;
 #pragma unroll
             for (int ks = 0; ks < D / 16; ++ks) {
-                const u32x4 kA = *reinterpret_cast<const u32x4 *>(ks_ + tile_off(r32, 2 * ks + hh));
+                const u32x4 kA = *reinterpret_cast<const u32x4 *>(ks_ + r32 * BF_KPITCH + (2 * ks + hh) * 16);
                 s = mfma32(kA, qhi[ks], s);
                 if constexpr (QF32) s = mfma32(kA, qlo[ks], s);
             }
             return s;
         };
         // softmax of tile t (scores s, S^T layout) and its PV products
-        auto softmax_pv = [&](int t, int slot, const f32x16 &s) {
+        auto softmax_pv = [&](int t, int slot, f32x16 &sc) {
             const int kt = t * kKeys;
-            const bool diag = kt + kKeys - 1 > q_offset + r0;
-            const int kq = qpos - kt - 4 * hh;
-            float sc[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) sc[i] = s[i];
-            if (diag) {
+            if (kt > diag_kt) {   // masked in place: keys past the query's position
+                const int kq = qpos - kt - 4 * hh;
 #pragma unroll
                 for (int i = 0; i < 16; ++i) sc[i] = 8 * (i >> 2) + (i & 3) <= kq ? sc[i] : -INFINITY;
             }
@@ -844,11 +846,11 @@ void prefill_bf16_kernel(PrefillArgs a) {
 #pragma unroll
             for (int i = 0; i < 16; ++i)   // masked: exp2(-inf) = 0
                 p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], a.scale_log2, -m_run));
-            float ls = 0.0f;
+            float ls = p[0];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) ls += p[i];
+            for (int i = 1; i < 16; ++i) ls += p[i];
             l_run += ls;
-            const uint8_t *vs_ = smem + slot * STAGE_BYTES + TILE_BYTES;
+            const uint8_t *vs_ = smem + slot * STAGE_BYTES + KTILE_BYTES;
             typedef short s16x4 __attribute__((ext_vector_type(4)));
             const int grp = lane >> 4, sl = lane & 15;
 #pragma unroll
@@ -862,9 +864,9 @@ void prefill_bf16_kernel(PrefillArgs a) {
                 for (int n = 0; n < D / 32; ++n) {
                     const int col = 32 * n + 16 * (grp & 1) + 4 * (sl & 3);   // bf16 column of the 8 bytes
                     const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) s16x4 *)(vs_ + tile_off(vrow, col >> 3) + (col & 7) * 2));
+                        (__attribute__((address_space(3))) s16x4 *)(vs_ + vrow * BF_VPITCH + col * 2));
                     const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) s16x4 *)(vs_ + tile_off(vrow + 8, col >> 3) + (col & 7) * 2));
+                        (__attribute__((address_space(3))) s16x4 *)(vs_ + (vrow + 8) * BF_VPITCH + col * 2));
                     const u32x2 a0 = __builtin_bit_cast(u32x2, t0), a1 = __builtin_bit_cast(u32x2, t1);
                     const u32x4 va = {a0[0], a0[1], a1[0], a1[1]};
                     acc[n] = mfma32(va, phi, acc[n]);
@@ -888,22 +890,29 @@ void prefill_bf16_kernel(PrefillArgs a) {
             fetch_ids(3, kend);
         }
         __syncthreads();
-        f32x16 s_cur = qk(0);
-        int slot_t = 0;
-        for (int t = 0; t < nt; ++t) {
-            const int slot_n = slot_t == kStages - 1 ? 0 : slot_t + 1;         // tile t + 1
-            const int slot_nn = slot_n == kStages - 1 ? 0 : slot_n + 1;        // tile t + 2
-            f32x16 s_next = s_cur;
-            if (wvalid && t + 1 < nt_w) s_next = qk(slot_n);
-            if (wvalid && t < nt_w) softmax_pv(t, slot_t, s_cur);
-            if (t + 2 < nt) stage_tile(slot_nn, R, kend);
+        // One pipeline step for tile t, whose LDS slot S = t % 3 is a
+        // compile-time constant (the loop is unrolled six times: three slots
+        // times two score buffers), so every LDS address is a loop-invariant
+        // register plus an immediate offset.
+        auto step = [&](int t, auto slot, f32x16 &s_cur, f32x16 &s_next) {
+            constexpr int S = decltype(slot)::value;
+            if (t + 1 < nt_w) s_next = qk((S + 1) % kStages);
+            if (t < nt_w) softmax_pv(t, S, s_cur);
+            if (t + 2 < nt) stage_tile((S + 2) % kStages, R, kend);
             __syncthreads();
             if (t + 3 < nt) {
                 load_tile(t + 3, R);
                 fetch_ids(t + 4, kend);
             }
-            s_cur = s_next;
-            slot_t = slot_n;
+        };
+        f32x16 sa = qk(0), sb = sa;
+        for (int t = 0; t < nt; t += 6) {
+            step(t, Int<0>{}, sa, sb);
+            if (t + 1 < nt) step(t + 1, Int<1>{}, sb, sa);
+            if (t + 2 < nt) step(t + 2, Int<2>{}, sa, sb);
+            if (t + 3 < nt) step(t + 3, Int<0>{}, sb, sa);
+            if (t + 4 < nt) step(t + 4, Int<1>{}, sa, sb);
+            if (t + 5 < nt) step(t + 5, Int<2>{}, sb, sa);
         }
 
         if (wvalid && r0 + r32 < qlen) {
