@@ -822,8 +822,9 @@ void prefill_bf16_kernel(PrefillArgs a) {
             }
             return s;
         };
-        // softmax of tile t (scores s, S^T layout) and its PV products
-        auto softmax_pv = [&](int t, int slot, f32x16 &sc) {
+        // softmax of tile t (scores s, S^T layout), first half: causal mask,
+        // tile max, lazy rescale
+        auto softmax_head = [&](int t, f32x16 &sc) {
             const int kt = t * kKeys;
             if (kt > diag_kt) {   // masked in place: keys past the query's position
                 const int kq = qpos - kt - 4 * hh;
@@ -842,6 +843,9 @@ void prefill_bf16_kernel(PrefillArgs a) {
                 for (int n = 0; n < D / 32; ++n) acc[n] *= alpha;
                 m_run = m_new;
             }
+        };
+        // second half: probabilities, their sum, and the PV products
+        auto softmax_pv = [&](int slot, const f32x16 &sc) {
             float p[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i)   // masked: exp2(-inf) = 0
@@ -896,8 +900,28 @@ void prefill_bf16_kernel(PrefillArgs a) {
         // register plus an immediate offset.
         auto step = [&](int t, auto slot, f32x16 &s_cur, f32x16 &s_next) {
             constexpr int S = decltype(slot)::value;
-            if (t + 1 < nt_w) s_next = qk((S + 1) % kStages);
-            if (t < nt_w) softmax_pv(t, S, s_cur);
+            // Unconditional: a wave past its last tile (t >= nt_w) sees
+            // only keys beyond its rows, which the mask turns into zero
+            // probabilities, and the S^T product of a slot past the last
+            // tile reads stale but in-bounds LDS that is never used.  One
+            // basic block then holds tile t + 1's S^T products and tile t's
+            // exponentials and PV products, interleaved below.
+            softmax_head(t, s_cur);
+            s_next = qk((S + 1) % kStages);
+            softmax_pv(S, s_cur);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+            }
             if (t + 2 < nt) stage_tile((S + 2) % kStages, R, kend);
             __syncthreads();
             if (t + 3 < nt) {
