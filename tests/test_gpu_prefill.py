@@ -90,6 +90,45 @@ def test_prefill_max_q_len_below_actual_still_complete():
     assert rel_err(got, want) <= 1e-3
 
 
+def test_prefill_ranked_dispatch_mixed_batch():
+    """Workgroups start in decreasing order of the keys they need, ranked
+    inside the kernel: a batch of 24 sequences with empty, single-row,
+    whole-sequence and prefixed chunks must still cover every row once (the
+    output starts as NaN, so a row that no workgroup serves fails)."""
+    rng = np.random.default_rng(81)
+    q_lens = [0, 1, 33, 64, 100, 0, 7, 96] + [int(x) for x in rng.integers(0, 90, 16)]
+    ctx = [q + int(p) for q, p in zip(q_lens, rng.integers(0, 400, len(q_lens)))]
+    ctx = [max(c, 1) for c in ctx]
+    ctx[2] = 33                          # whole-sequence prefill
+    cfg = workloads.Config("rank", 8, 2, 128, 16, airkv.BF16, len(q_lens))
+    got, want = _prefill_case(cfg, ctx, q_lens, seed=83)
+    err = rel_err(got, want)
+    log(f"prefill ranked mixed batch of {len(q_lens)}: rel err {err:.2e}")
+    assert err <= 1e-3
+
+
+def test_prefill_unranked_orders_large_batch_and_many_slots():
+    """Past 2048 sequences, or 16384 (sequence, slot) items, workgroups keep
+    slot-major order without ranking; both fallbacks cover every row."""
+    rng = np.random.default_rng(85)
+    n = 2100
+    q_lens = [int(x) for x in rng.integers(1, 4, n)]
+    ctx = [q + int(p) for q, p in zip(q_lens, rng.integers(0, 30, n))]
+    cfg = workloads.Config("big", 8, 2, 128, 16, airkv.BF16, n)
+    got, want = _prefill_case(cfg, ctx, q_lens, seed=87)
+    err = rel_err(got, want)
+    log(f"prefill batch {n} (unranked): rel err {err:.2e}")
+    assert err <= 1e-3
+    # 130 sequences x 128 slots (max_q_len 4096, group 4) = 16640 items
+    q_lens = [int(x) for x in rng.integers(0, 40, 130)]
+    ctx = [max(q + int(p), 1) for q, p in zip(q_lens, rng.integers(0, 200, 130))]
+    cfg = workloads.Config("slots", 8, 2, 128, 16, airkv.BF16, 130)
+    got, want = _prefill_case(cfg, ctx, q_lens, seed=89, max_q_len=4096)
+    err = rel_err(got, want)
+    log(f"prefill 16640 items (unranked): rel err {err:.2e}")
+    assert err <= 1e-3
+
+
 def test_prefill_c5_chunks_scaled():
     """configs[4] prefill geometry: 512-token chunks (bs 32, 32 q / 8 kv,
     bf16) over prefixes from the lognormal context mix; two sequences and a
