@@ -33,8 +33,9 @@
 //
 // Each wave resolves the sequence, block id and valid token count of 64 of its
 // tiles at once (lane k: tile k), then takes them with readlane, so tile
-// addresses live in scalar registers and no load waits on another.  Three
-// register sets rotate: two tiles are in flight while the third is computed.
+// addresses live in scalar registers and no load waits on another.  A ring of
+// register sets rotates: all but one hold tiles in flight while the other is
+// computed.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -64,6 +65,12 @@ constexpr int kMinChunk = 4;               // tiles per slice at least
 #endif
 #ifndef AIRKV_DECODE_QWAVES_PER_EU
 #define AIRKV_DECODE_QWAVES_PER_EU 3       // the same for 1-byte pages (fewer raw registers per tile)
+#endif
+#ifndef AIRKV_DECODE_RING
+#define AIRKV_DECODE_RING 3               // tile register sets per wave, bf16 pages (ring - 1 in flight)
+#endif
+#ifndef AIRKV_DECODE_QRING
+#define AIRKV_DECODE_QRING 3              // the same for 1-byte pages
 #endif
 #ifndef AIRKV_DECODE_NT_LOADS
 #define AIRKV_DECODE_NT_LOADS 1            // non-temporal K/V loads
@@ -319,6 +326,16 @@ void decode_mfma_kernel(DecodeArgs a) {
                 qlo[ks] = u32x4{0, 0, 0, 0};
             }
         }
+        // Consumed here, on the rare path that loads them: otherwise the
+        // compiler cannot tell at the QK products whether Q is still in
+        // flight, and since vector loads retire in order it waits for every
+        // load issued before -- the next tiles' pages included -- on every
+        // tile.
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            asm volatile("" ::"v"(qhi[ks]));
+            if constexpr (QF32) asm volatile("" ::"v"(qlo[ks]));
+        }
     };
 
     f32x4 acc[DTILES];
@@ -519,22 +536,41 @@ void decode_mfma_kernel(DecodeArgs a) {
         load_window(c0);
         if (c0 == lo) load_q(__builtin_amdgcn_readlane(seq_l, 0));
         const int n = hi - c0 < 64 ? hi - c0 : 64;
-        // Three register sets used in rotation: two tiles are in flight while
-        // the third is computed.  Loads are issued unconditionally (past the
-        // end they re-read the last tile, an L2 hit) so no branch joins paths
-        // with different loads in flight.
+        // kRing register sets used in rotation: kRing - 1 tiles are in
+        // flight while one is computed.  Loads are issued unconditionally
+        // (past the end they re-read the last tile, an L2 hit) so no branch
+        // joins paths with different loads in flight.
+        constexpr int kRing = QUANT ? AIRKV_DECODE_QRING : AIRKV_DECODE_RING;
         auto clampi = [&](int i) { return i < n ? i : n - 1; };
-        Tile<DT> ta, tb, tc;
-        bool oka = load_tile(0, ta), okb = load_tile(clampi(1), tb), okc;
-        for (int i = 0; i < n; i += 3) {
-            okc = load_tile(clampi(i + 2), tc);
-            compute_tile(c0 + i, i, ta, oka);
-            if (i + 1 >= n) break;
-            oka = load_tile(clampi(i + 3), ta);
-            compute_tile(c0 + i + 1, i + 1, tb, okb);
-            if (i + 2 >= n) break;
-            okb = load_tile(clampi(i + 4), tb);
-            compute_tile(c0 + i + 2, i + 2, tc, okc);
+        if constexpr (kRing == 3) {
+            // written out: the compiler allocates this form in fewer
+            // registers than the general ring below
+            Tile<DT> ta, tb, tc;
+            bool oka = load_tile(0, ta), okb = load_tile(clampi(1), tb), okc;
+            for (int i = 0; i < n; i += 3) {
+                okc = load_tile(clampi(i + 2), tc);
+                compute_tile(c0 + i, i, ta, oka);
+                if (i + 1 >= n) break;
+                oka = load_tile(clampi(i + 3), ta);
+                compute_tile(c0 + i + 1, i + 1, tb, okb);
+                if (i + 2 >= n) break;
+                okb = load_tile(clampi(i + 4), tb);
+                compute_tile(c0 + i + 2, i + 2, tc, okc);
+            }
+        } else {
+            Tile<DT> ring[kRing];
+            bool ok[kRing];
+#pragma unroll
+            for (int j = 0; j < kRing - 1; ++j) ok[j] = load_tile(clampi(j), ring[j]);
+            for (int i = 0; i < n; i += kRing) {
+#pragma unroll
+                for (int j = 0; j < kRing; ++j) {
+                    if (i + j >= n) break;
+                    const int jl = (j + kRing - 1) % kRing;      // the set freed by the previous tile
+                    ok[jl] = load_tile(clampi(i + j + kRing - 1), ring[jl]);
+                    compute_tile(c0 + i + j, i + j, ring[j], ok[j]);
+                }
+            }
         }
     }
 }
