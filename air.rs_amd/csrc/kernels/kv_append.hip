@@ -4,8 +4,10 @@
 //
 // One thread owns 8 consecutive head_dim elements of one (token, kv head) row
 // and handles both K and V: two 32-byte f32 loads each, one 32/16/8-byte store
-// each.  Consecutive threads cover a row, then the next head of the same
-// token, so the f32 source streams fully coalesced.  For INT8/FP8 the
+// each.  Consecutive threads cover a row, then the same head of the next
+// token (four tokens per wave at head_dim 128), so a wave writes one
+// contiguous run of page rows when its tokens share a block and reads four
+// whole source rows.  For INT8/FP8 the
 // scale_group/8 lanes of one scale group reduce their absmax with butterfly
 // shuffles; the group's first lane stores the f32 scale.
 #include <hip/hip_runtime.h>
@@ -26,7 +28,7 @@ constexpr int kThreads = 256;
 struct AppendArgs {
     const float *k, *v;
     const int64_t *slots;
-    int64_t n_rows;          // n_tokens * n_kv_heads
+    int64_t n_tokens;
     int64_t num_slots;       // num_blocks * block_size
     int32_t n_kv_heads, head_dim, block_size, scale_group;
     void *k_pages, *v_pages;
@@ -36,13 +38,20 @@ struct AppendArgs {
 
 template <int DT>
 __global__ __launch_bounds__(kThreads) void kv_append_kernel(AppendArgs a) {
+    // thread -> (chunk c, token t % 4, kv head h, token t / 4), chunk fastest:
+    // 4 * chunks consecutive threads (a wave at head_dim 128) cover four
+    // consecutive tokens of one head, whose page rows are one contiguous run
+    // when the tokens share a block (prefill chunks)
     const int chunks = a.head_dim >> 3;
     const int64_t gid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    const int64_t row = gid / chunks;
-    const int c = (int)(gid - row * chunks);
-    const bool active = row < a.n_rows;
-    const int64_t t = active ? row / a.n_kv_heads : 0;
-    const int h = active ? (int)(row - t * a.n_kv_heads) : 0;
+    const int c = (int)(gid % chunks);
+    const int64_t rest = gid / chunks;
+    const int tl = (int)(rest & 3);
+    const int64_t rest2 = rest >> 2;
+    const int h = (int)(rest2 % a.n_kv_heads);
+    const int64_t t = (rest2 / a.n_kv_heads) * 4 + tl;
+    const bool active = t < a.n_tokens;
+    const int64_t row = t * a.n_kv_heads + h;
     const int64_t slot = active ? a.slots[t] : -1;
     const bool valid = slot >= 0 && slot < a.num_slots;
     if (active && slot >= a.num_slots && c == 0 && h == 0) atomicAdd(a.errors, 1ull);
@@ -84,14 +93,14 @@ hipError_t launch_append(const air_kv_pool &p, hipStream_t s, const float *k, co
                          const int64_t *slots, int32_t n_tokens) {
     AppendArgs a;
     a.k = k; a.v = v; a.slots = slots;
-    a.n_rows = (int64_t)n_tokens * p.desc.n_kv_heads;
+    a.n_tokens = n_tokens;
     a.num_slots = p.desc.num_blocks * p.desc.block_size;
     a.n_kv_heads = p.desc.n_kv_heads; a.head_dim = p.desc.head_dim;
     a.block_size = p.desc.block_size; a.scale_group = p.desc.scale_group;
     a.k_pages = p.k_pages; a.v_pages = p.v_pages;
     a.k_scales = p.k_scales; a.v_scales = p.v_scales;
     a.errors = p.errors;
-    const int64_t threads = a.n_rows * (p.desc.head_dim / 8);
+    const int64_t threads = ((int64_t)n_tokens + 3) / 4 * 4 * p.desc.n_kv_heads * (p.desc.head_dim / 8);
     const int64_t blocks = (threads + kThreads - 1) / kThreads;
     if (blocks > INT32_MAX) return hipErrorInvalidValue;
     dim3 grid((unsigned)blocks);

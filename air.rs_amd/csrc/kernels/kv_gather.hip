@@ -1,12 +1,12 @@
 // Gather: pages -> one contiguous view per sequence (dequantizing INT8/FP8).
 //
-// Work is the flat list of (sequence, page, kv head) tiles of every live
-// sequence, so variable lengths cost nothing: each workgroup builds the
-// exclusive prefix sum of pages-per-sequence in LDS once, then walks the tile
-// list with a grid stride, finding a tile's sequence by binary search.  A
-// tile is block_size rows of head_dim elements of K and of V; each thread
-// moves 8 elements (a 16-byte bf16 load) per tensor per step, so a bf16
-// tile of 16 x 128 is exactly one pass of 256 threads.
+// Work is the flat list of (sequence, page) pairs of every live sequence, so
+// variable lengths cost nothing: each workgroup builds the exclusive prefix
+// sum of pages-per-sequence in LDS once, then walks the page list with a grid
+// stride, finding a page's sequence by binary search.  A page is block_size
+// rows of head_dim elements of K and of V for every kv head; each thread
+// moves 8 elements (a 16-byte bf16 load) per tensor and head, so the 16 x 128
+// rows of one head are one pass of 256 threads, four heads at a time.
 #include <hip/hip_runtime.h>
 
 #include "../pool.hpp"
@@ -14,7 +14,7 @@
 #include "page_io.hpp"
 
 #ifndef AIRKV_GATHER_WGS_PER_CU
-#define AIRKV_GATHER_WGS_PER_CU 8          // build-time tuning knob: resident workgroups per CU
+#define AIRKV_GATHER_WGS_PER_CU 32         // build-time tuning knob: workgroups per CU in the grid (8 resident)
 #endif
 
 namespace airkv {
@@ -101,13 +101,14 @@ __global__ __launch_bounds__(kThreads) void kv_gather_kernel(GatherArgs a) {
         }
     }
 
-    const int64_t total_tiles = (int64_t)carry * a.n_kv_heads;
+    // One page of one sequence per step, all kv heads: the page's table
+    // entry, length and output offset are looked up once, and each thread
+    // keeps kHeadUnroll heads' K and V loads in flight before storing them.
+    constexpr int kHeadUnroll = 4;
     const int rows = a.block_size, d = a.head_dim;
     const int tile_elems = rows * d;
     const int ng = DT == AIR_KV_INT8 || DT == AIR_KV_FP8 ? d / a.scale_group : 1;
-    for (int64_t tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
-        const int32_t page_g = (int32_t)(tile / a.n_kv_heads);
-        const int h = (int)(tile - (int64_t)page_g * a.n_kv_heads);
+    for (int64_t page_g = blockIdx.x; page_g < carry; page_g += gridDim.x) {
         // sequence owning global page index page_g: last b with prefix[b] <= page_g
         int lo = 0, hi = a.batch - 1;
         while (lo < hi) {
@@ -115,12 +116,12 @@ __global__ __launch_bounds__(kThreads) void kv_gather_kernel(GatherArgs a) {
             if (s_prefix[mid] <= page_g) lo = mid; else hi = mid - 1;
         }
         const int b = lo;
-        const int32_t p = page_g - s_prefix[b];
+        const int32_t p = (int32_t)(page_g - s_prefix[b]);
         int64_t len = a.lens[b];
         len = len > max_len ? max_len : len;
         const int32_t blk = a.tables[(int64_t)b * a.max_blocks + p];
-        if (blk < 0 || blk >= a.num_blocks) {
-            if (tid == 0) atomicAdd(a.errors, 1ull);
+        if (blk < 0 || blk >= a.num_blocks) {     // one count per (page, kv head)
+            if (tid == 0) atomicAdd(a.errors, (unsigned long long)a.n_kv_heads);
             continue;
         }
         const int64_t out_base = a.out_offsets[b];
@@ -128,18 +129,30 @@ __global__ __launch_bounds__(kThreads) void kv_gather_kernel(GatherArgs a) {
             const int r = e / d, col = e - r * d;
             const int64_t t = (int64_t)p * rows + r;
             if (t >= len) continue;
-            const int64_t src_row = ((int64_t)blk * a.n_kv_heads + h) * rows + r;
-            const int64_t src = src_row * d + col;
-            const int64_t sidx = src_row * ng + col / (a.scale_group > 0 ? a.scale_group : 1);
-            const int64_t dst = out_base + (a.layout == AIR_KV_LAYOUT_HEAD_MAJOR
-                                                ? ((int64_t)h * len + t) * d + col
-                                                : (t * a.n_kv_heads + h) * d + col);
-            float xk[8], xv[8];
-            u32x4 rk = {0, 0, 0, 0}, rv = rk;
-            load8<DT>(a.k_pages, a.k_scales, src, sidx, xk, &rk);
-            load8<DT>(a.v_pages, a.v_scales, src, sidx, xv, &rv);
-            store8<DT, OUT>(a.out_k, dst, xk, rk);
-            store8<DT, OUT>(a.out_v, dst, xv, rv);
+            for (int h0 = 0; h0 < a.n_kv_heads; h0 += kHeadUnroll) {
+                float xk[kHeadUnroll][8], xv[kHeadUnroll][8];
+                u32x4 rk[kHeadUnroll], rv[kHeadUnroll];
+#pragma unroll
+                for (int u = 0; u < kHeadUnroll; ++u) {
+                    const int h = h0 + u < a.n_kv_heads ? h0 + u : a.n_kv_heads - 1;
+                    const int64_t src_row = ((int64_t)blk * a.n_kv_heads + h) * rows + r;
+                    const int64_t src = src_row * d + col;
+                    const int64_t sidx = src_row * ng + col / (a.scale_group > 0 ? a.scale_group : 1);
+                    rk[u] = rv[u] = u32x4{0, 0, 0, 0};
+                    load8<DT>(a.k_pages, a.k_scales, src, sidx, xk[u], &rk[u]);
+                    load8<DT>(a.v_pages, a.v_scales, src, sidx, xv[u], &rv[u]);
+                }
+#pragma unroll
+                for (int u = 0; u < kHeadUnroll; ++u) {
+                    const int h = h0 + u;
+                    if (h >= a.n_kv_heads) break;
+                    const int64_t dst = out_base + (a.layout == AIR_KV_LAYOUT_HEAD_MAJOR
+                                                        ? ((int64_t)h * len + t) * d + col
+                                                        : (t * a.n_kv_heads + h) * d + col);
+                    store8<DT, OUT>(a.out_k, dst, xk[u], rk[u]);
+                    store8<DT, OUT>(a.out_v, dst, xv[u], rv[u]);
+                }
+            }
         }
     }
 }

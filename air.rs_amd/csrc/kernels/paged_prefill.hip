@@ -765,10 +765,8 @@ void prefill_bf16_kernel(PrefillArgs a) {
         const int tb_last = last_item / G;
         const int rows_last = (tb_last + 1) * kRows < qlen ? (tb_last + 1) * kRows : qlen;
         const int kend = q_offset + rows_last;          // keys the workgroup needs (<= len)
-        const int rows_w = r0 + kRows < qlen ? r0 + kRows : qlen;
-        // uniform per wave (nt per workgroup): kept in scalar registers so the
+        // uniform per workgroup / wave: kept in scalar registers so the
         // guards below are scalar branches
-        const int nt_w = __builtin_amdgcn_readfirstlane(wvalid ? (q_offset + rows_w + kKeys - 1) / kKeys : 0);
         const int nt = __builtin_amdgcn_readfirstlane((kend + kKeys - 1) / kKeys);
         const int diag_kt = __builtin_amdgcn_readfirstlane(q_offset + r0 - kKeys + 1);   // first masked tile start
 
@@ -900,7 +898,7 @@ void prefill_bf16_kernel(PrefillArgs a) {
         // register plus an immediate offset.
         auto step = [&](int t, auto slot, f32x16 &s_cur, f32x16 &s_next) {
             constexpr int S = decltype(slot)::value;
-            // Unconditional: a wave past its last tile (t >= nt_w) sees
+            // Unconditional: a wave past the last tile its own rows need sees
             // only keys beyond its rows, which the mask turns into zero
             // probabilities, and the S^T product of a slot past the last
             // tile reads stale but in-bounds LDS that is never used.  One
