@@ -9,7 +9,9 @@
 // The reference folds each vector left to right (Iterator::sum, f32::min /
 // max folds, a dot product per projected row), and the fold order fixes the
 // rounding of the mean, the norm and every projection.  So one lane owns one
-// row and runs the folds in that order.  It loads its whole row itself (any
+// row and runs the folds in that order (the value codec's min / max folds,
+// whose result does not depend on how the row is split, take four lanes per
+// row).  It loads its whole row itself (any
 // pool dtype, dequantized by the shared page loader) with back-to-back
 // 16-byte pieces, so every cache line is fetched once, and keeps it in
 // registers.  Products and sums round separately (no contraction), as
@@ -55,22 +57,25 @@ __device__ __forceinline__ bool row_elem(const RowSource &s, int64_t r, int dim,
     return ok;
 }
 
-// Row r into registers (its own lane): D / 8 pieces of 8 elements, read
-// back to back by the same lane.  Plain (cacheable) loads: the lanes of a
+// Row r (or its N elements from `first`) into registers: N / 8 pieces of 8
+// elements, read back to back by the same lane.  Plain (cacheable) loads: the lanes of a
 // wave read 64 different rows, so each 128-byte line is needed by several
 // consecutive loads of one lane and must stay in cache between them (a
 // streaming load would fetch it again).  INT8 / FP8 rows are dequantized as
 // q * scale with one rounding (src/kv_cache.rs:88, src/fp8.rs:263-264).
 // Rows of out-of-pool blocks read as zeros and `live` is false for them.
-template <int DT, int D>
-__device__ __forceinline__ void load_row(const RowSource &s, int64_t r, float (&x)[D], bool &live) {
+template <int DT, int D, int N = D>
+__device__ __forceinline__ void load_row(const RowSource &s, int64_t r, float (&x)[N], bool &live,
+                                         int first = 0) {
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    static_assert(N % 8 == 0, "whole 8-element pieces");
     int64_t e;
     live = row_elem(s, r, D, e);
+    e += first;
 #pragma unroll
-    for (int c = 0; c < D / 8; ++c) {
+    for (int c = 0; c < N / 8; ++c) {
         const int64_t el = e + 8 * c;
         float v[8];
         if constexpr (DT == AIR_KV_F32) {
@@ -151,23 +156,45 @@ __global__ __launch_bounds__(kThreads) void key_compress_kernel(CompressArgs a) 
     }
 }
 
+// Four lanes per row, each folding a quarter: min / max need no fixed order
+// across quarters.  The fold keeps the accumulator unless x <= it (x < it for
+// max's mirror), so fold(L ++ R) from +inf equals fold_min(fold(L),
+// fold(R)) for consecutive parts L, R -- the right part's own fold wins
+// exactly when it reaches the left result, ties included -- and combining
+// the quarters left to right reproduces the reference's left fold bit for
+// bit (signed zeros and NaN skipping included).  A wave then reads 16 whole
+// rows and writes 16 contiguous code rows.
 template <int DT, int D>
 __global__ __launch_bounds__(kThreads) void value_compress_kernel(CompressArgs a) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    for (int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x; r < a.n_rows;
-         r += (int64_t)gridDim.x * kThreads) {
-        float x[D];
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    constexpr int P = 4, N = D / P;                // lanes per row, elements per lane
+    const int part = threadIdx.x & (P - 1);
+    // the four lanes of a row share r, so they run the loop in lockstep
+    for (int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x; t / P < a.n_rows;
+         t += (int64_t)gridDim.x * kThreads) {
+        const int64_t r = t / P;
+        float x[N];
         bool live;
-        load_row<DT, D>(a.src, r, x, live);
-        if (!live && a.errors && (r % a.src.rows_per_block) == 0) atomicAdd(a.errors, 1ull);
+        load_row<DT, D, N>(a.src, r, x, live, part * N);
+        if (!live && a.errors && part == 0 && (r % a.src.rows_per_block) == 0) atomicAdd(a.errors, 1ull);
         float lo = INFINITY, hi = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < D; ++j) {                  // (:198-199)
+        for (int j = 0; j < N; ++j) {                  // (:198-199)
             lo = fold_min(lo, x[j]);
             hi = fold_max(hi, x[j]);
         }
+        // quarters 0+1 and 2+3, then the halves: the lower part is the left operand
+        float o = __shfl_xor(lo, 1);
+        lo = (part & 1) ? fold_min(o, lo) : fold_min(lo, o);
+        o = __shfl_xor(hi, 1);
+        hi = (part & 1) ? fold_max(o, hi) : fold_max(hi, o);
+        o = __shfl_xor(lo, 2);
+        lo = (part & 2) ? fold_min(o, lo) : fold_min(lo, o);
+        o = __shfl_xor(hi, 2);
+        hi = (part & 2) ? fold_max(o, hi) : fold_max(hi, o);
         float scale;
-        uint32_t q[D / 4];
+        uint32_t q[N / 4];
         {
 #pragma clang fp contract(off)
             const float range = hi - lo;
@@ -181,27 +208,12 @@ __global__ __launch_bounds__(kThreads) void value_compress_kernel(CompressArgs a
             // round to code 0 either way); other rows (a subnormal or
             // infinite scale, i.e. tiny or non-finite data) divide exactly.
             const float y = 1.0f / scale;
-            auto codes = [&](auto quotient) {
-#pragma unroll
-                for (int j4 = 0; j4 < D / 4; ++j4) {
-                    uint32_t w = 0;
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        float t = roundf(quotient(x[4 * j4 + k] - lo));
-                        t = t < 0.0f ? 0.0f : t;
-                        t = t > 255.0f ? 255.0f : t;
-                        const uint32_t c = (t != t) ? 0u : (uint32_t)t;   // `as u8`: NaN -> 0
-                        w |= c << (8 * k);
-                    }
-                    q[j4] = w;
-                }
-            };
             if (__builtin_isnormal(scale) && __builtin_isnormal(y)) {
                 // d = v - min >= 0 (or NaN) here, so round half away from zero
                 // is trunc + (fraction >= 0.5), and only the upper clamp and
                 // NaN need handling
 #pragma unroll
-                for (int j4 = 0; j4 < D / 4; ++j4) {
+                for (int j4 = 0; j4 < N / 4; ++j4) {
                     uint32_t w = 0;
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
@@ -209,23 +221,42 @@ __global__ __launch_bounds__(kThreads) void value_compress_kernel(CompressArgs a
                         const float q0 = d * y;
                         const float rem = __builtin_fmaf(-q0, scale, d);
                         const float quo = __builtin_fmaf(rem, y, q0);
-                        const float t = __builtin_truncf(quo);
-                        float r = t + (quo - t >= 0.5f ? 1.0f : 0.0f);
-                        r = r <= 255.0f ? r : (r == r ? 255.0f : 0.0f);
-                        w |= (uint32_t)r << (8 * k);
+                        const float tq = __builtin_truncf(quo);
+                        float rq = tq + (quo - tq >= 0.5f ? 1.0f : 0.0f);
+                        rq = rq <= 255.0f ? rq : (rq == rq ? 255.0f : 0.0f);
+                        w |= (uint32_t)rq << (8 * k);
                     }
                     q[j4] = w;
                 }
             } else {
-                codes([&](float d) { return d / scale; });
+#pragma unroll
+                for (int j4 = 0; j4 < N / 4; ++j4) {
+                    uint32_t w = 0;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        float tq = roundf((x[4 * j4 + k] - lo) / scale);
+                        tq = tq < 0.0f ? 0.0f : tq;
+                        tq = tq > 255.0f ? 255.0f : tq;
+                        const uint32_t c = (tq != tq) ? 0u : (uint32_t)tq;   // `as u8`: NaN -> 0
+                        w |= c << (8 * k);
+                    }
+                    q[j4] = w;
+                }
             }
         }
-        if (!live) { scale = 0.0f; lo = 0.0f; for (int j = 0; j < D / 4; ++j) q[j] = 0; }
-        u32x4 *dst = reinterpret_cast<u32x4 *>(a.codes + r * D);
+        if (!live) { scale = 0.0f; lo = 0.0f; for (int j = 0; j < N / 4; ++j) q[j] = 0; }
+        uint8_t *dst = a.codes + r * D + part * N;
+        if constexpr (N >= 16) {
 #pragma unroll
-        for (int j = 0; j < D / 16; ++j) dst[j] = u32x4{q[4 * j], q[4 * j + 1], q[4 * j + 2], q[4 * j + 3]};
-        a.f0[r] = scale;
-        a.f1[r] = lo;
+            for (int j = 0; j < N / 16; ++j)
+                reinterpret_cast<u32x4 *>(dst)[j] = u32x4{q[4 * j], q[4 * j + 1], q[4 * j + 2], q[4 * j + 3]};
+        } else {
+            *reinterpret_cast<u32x2 *>(dst) = u32x2{q[0], q[1]};
+        }
+        if (part == 0) {
+            a.f0[r] = scale;
+            a.f1[r] = lo;
+        }
     }
 }
 
@@ -351,7 +382,8 @@ bool compress_dim_supported(int dim) { return dim == 32 || dim == 64 || dim == 1
 
 hipError_t launch_compress(CompressKind kind, const CompressArgs &a, int cus, hipStream_t s) {
     if (a.n_rows == 0) return hipSuccess;
-    const dim3 grid((unsigned)grid_for(a.n_rows, kThreads, cus));
+    const int lanes_per_row = kind == CompressKind::Value ? 4 : 1;
+    const dim3 grid((unsigned)grid_for(a.n_rows * lanes_per_row, kThreads, cus));
     switch (kind) {
     case CompressKind::Key: AIRKV_LAUNCH_D(key_compress_kernel, a, s, grid) break;
     case CompressKind::Value: AIRKV_LAUNCH_D(value_compress_kernel, a, s, grid) break;
