@@ -34,18 +34,14 @@
 //                   bf16 halves (~16 mantissa bits): bf16 probabilities alone
 //                   leave ~1e-3 relative error at these lengths.
 //
-// bf16 pages (prefill_bf16_kernel): K and V tiles are staged row-major in
-// three LDS stages, 16-byte chunks XOR-swizzled by row; the V^T operand comes
+// K and V tiles are staged row-major in three LDS stages (1-byte codes
+// dequantized to bf16 on the way, exactly as the decode kernel does, and
+// their probabilities then take the hi bf16 half only); the V^T operand comes
 // from two transposing reads (ds_read_b64_tr_b16) per 16 keys.  The loop is
 // software-pipelined: the S^T product of tile t + 1 is issued before the
 // softmax and PV products of tile t, tile t + 2 is written to LDS after them,
 // and the page loads of tile t + 3 are in flight in registers, with one
 // barrier per tile.
-//
-// 1-byte pages (prefill_kernel): codes are dequantized to bf16 on the way to
-// LDS; V is stored transposed, V^T[d][c] with the key of column c = c with
-// bits 2 and 3 swapped, so a lane's eight keys of one step are one contiguous
-// 16-byte read.  Two LDS buffers, page loads two tiles ahead in registers.
 //
 // Keys past the sequence and out-of-pool table entries are staged as zeros
 // (stale page bytes may hold non-finite values).
@@ -73,11 +69,6 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kRows = 32;                   // query rows per wave
 constexpr int kKeys = 32;                   // keys per tile
 constexpr int D = 128;                      // head_dim
-constexpr int KPITCH = D * 2 + 16;          // bytes per K row in LDS (bank-spread 16-byte reads)
-constexpr int VPITCH = kKeys * 2 + 16;      // bytes per V^T row in LDS
-constexpr int KBUF = kKeys * KPITCH;
-constexpr int VBUF = D * VPITCH;
-constexpr int STAGE = KBUF + VBUF;
 
 #ifndef AIRKV_PREFILL_WAVES_PER_EU
 #define AIRKV_PREFILL_WAVES_PER_EU 2        // register budget: waves per SIMD
@@ -109,11 +100,6 @@ __device__ __forceinline__ void split_pair(float x, float y, uint32_t &hi, uint3
     const f32x2 r = v - __builtin_convertvector(h, f32x2);
     hi = __builtin_bit_cast(uint32_t, h);
     lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2));
-}
-
-// LDS column of key k inside a V^T row: bits 2 and 3 swapped (an involution).
-__device__ __forceinline__ int vcol_of_key(int k) {
-    return (k & 0x13) | ((k & 4) << 1) | ((k & 8) >> 1);
 }
 
 // Eight cache elements of one row as bf16 (16 bytes).  bf16 pages are raw
@@ -338,312 +324,9 @@ __device__ bool prefill_begin(const PrefillArgs &a, const PrefillSlot &sl, int32
     return qlen > 0;
 }
 
-template <int BS, bool QF32, int DT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AIRKV_PREFILL_WAVES_PER_EU)))
-void prefill_kernel(PrefillArgs a) {
-    __shared__ __align__(16) uint8_t smem[2 * STAGE];
-    static_assert(sizeof(smem) >= kRankLdsBytes, "dispatch ranking needs the tile LDS");
-    const PrefillSlot sl = prefill_slot(a, reinterpret_cast<int *>(smem));
-    const int b = sl.b, kh = sl.kh;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int G = a.group;
-    int32_t q0;
-    int qlen;
-    int64_t len;
-    if (!prefill_begin<BS>(a, sl, q0, qlen, len)) return;
-    const int32_t *tbl = a.tables + (int64_t)b * a.max_blocks;
-
-    const int q_offset = (int)(len - qlen);
-    const int ntb = (qlen + kRows - 1) / kRows;
-    const int n_items = ntb * G;
-    const int n_wg = (n_items + kWaves - 1) / kWaves;
-    const int r32 = lane & 31, hh = lane >> 5;
-
-    // Staging roles.  K: thread covers head_dim 8*(tid % 16) .. +8 of key rows
-    // tid / 16 and 16 + tid / 16.  V: thread covers keys
-    // 2p and 2p + 1 (p = tid % 16) at head_dim 8*dc .. +8 (dc = tid / 16), so
-    // it writes key pairs as packed dwords of V^T.
-    const int vp = tid & 15, vdc = tid >> 4;
-    const int n_sc = DT == AIR_KV_BF16 ? 0 : D / a.scale_group;
-
-    // One tile's loaded rows (this thread's two K chunks and two V chunks)
-    // and the tile's uniform facts: first key, and whether each page is
-    // inside the pool.
-    struct TileRegs {
-        Raw8<DT> k[2], v[2];
-        int kt;
-        bool ok0, ok1;
-    };
-    // The pages of tile t are 32 / BS consecutive table entries, the same for
-    // the whole workgroup.  They are fetched one tile ahead of the page loads
-    // (nb0, nb1 hold the ids of the next tile to load), so a page load never
-    // waits on its table entry.  kend <= len keeps every index inside the
-    // table row.  Both entries are loaded unconditionally from indices
-    // clamped to the last page in use (a branch here would make the compiler
-    // wait for every load in flight).
-    int32_t nb0 = 0, nb1 = 0;
-    auto fetch_ids = [&](int t, int kend) {
-        const int last = (kend - 1) / BS;
-        const int j0 = (t * kKeys) / BS;
-        nb0 = tbl[j0 < last ? j0 : last];
-        if constexpr (BS == 16) nb1 = tbl[j0 + 1 < last ? j0 + 1 : last];
-        else nb1 = nb0;
-    };
-    // Per-thread byte offsets inside a page (constant across tiles).  K chunk
-    // i: key row (tid / 16) + 16 i of the tile; V chunk i: key 2 vp + i.
-    constexpr int EB = DT == AIR_KV_BF16 ? 2 : 1;
-    constexpr int PAGE_BYTES = BS * D * EB;
-    int k_off[2], v_off[2], ks_off[2], vs_off[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int kr = ((tid >> 4) + 16 * i) % BS, vr = (2 * vp + i) % BS;
-        k_off[i] = (kr * D + (tid & 15) * 8) * EB;
-        v_off[i] = (vr * D + vdc * 8) * EB;
-        ks_off[i] = (kr * n_sc + ((tid & 15) * 8) / (n_sc ? a.scale_group : 1)) * 4;
-        vs_off[i] = (vr * n_sc + (vdc * 8) / (n_sc ? a.scale_group : 1)) * 4;
-    }
-    auto load_tile = [&](int t, TileRegs &R) {
-        const int32_t b0 = __builtin_amdgcn_readfirstlane(nb0), b1 = __builtin_amdgcn_readfirstlane(nb1);
-        R.kt = t * kKeys;
-        R.ok0 = b0 >= 0 && b0 < a.num_blocks;
-        R.ok1 = b1 >= 0 && b1 < a.num_blocks;
-        const int64_t row0 = ((int64_t)(R.ok0 ? b0 : 0) * a.n_kv_heads + kh) * BS;
-        const int64_t row1 = ((int64_t)(R.ok1 ? b1 : 0) * a.n_kv_heads + kh) * BS;
-        const __amdgpu_buffer_rsrc_t k0 = page_rsrc(a.k_pages, row0 * D * EB, PAGE_BYTES);
-        const __amdgpu_buffer_rsrc_t v0 = page_rsrc(a.v_pages, row0 * D * EB, PAGE_BYTES);
-        const __amdgpu_buffer_rsrc_t k1 = page_rsrc(a.k_pages, row1 * D * EB, PAGE_BYTES);
-        const __amdgpu_buffer_rsrc_t v1 = page_rsrc(a.v_pages, row1 * D * EB, PAGE_BYTES);
-        __amdgpu_buffer_rsrc_t ks0 = k0, vs0 = v0, ks1 = k1, vs1 = v1;
-        if constexpr (DT != AIR_KV_BF16) {
-            ks0 = page_rsrc(a.k_scales, row0 * n_sc * 4, BS * n_sc * 4);
-            vs0 = page_rsrc(a.v_scales, row0 * n_sc * 4, BS * n_sc * 4);
-            ks1 = page_rsrc(a.k_scales, row1 * n_sc * 4, BS * n_sc * 4);
-            vs1 = page_rsrc(a.v_scales, row1 * n_sc * 4, BS * n_sc * 4);
-        }
-        // BS 16: K chunk i and V keys >= 16 lie in the tile's second page
-        load_raw<DT>(k0, ks0, k_off[0], ks_off[0], R.k[0]);
-        if constexpr (BS == 16) load_raw<DT>(k1, ks1, k_off[1], ks_off[1], R.k[1]);
-        else load_raw<DT>(k0, ks0, k_off[1], ks_off[1], R.k[1]);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            if (BS == 16 && vp >= 8) load_raw<DT>(v1, vs1, v_off[i], vs_off[i], R.v[i]);
-            else load_raw<DT>(v0, vs0, v_off[i], vs_off[i], R.v[i]);
-        }
-    };
-    // Stale page bytes may hold non-finite values: keys past the sequence and
-    // rows of out-of-pool blocks are staged as zeros.  Only the tiles that
-    // hold such keys (uniform test) pay for the selects.
-    auto stage_tile = [&](int buf, const TileRegs &R, int kend) {
-        uint8_t *ks = smem + buf * STAGE;
-        uint8_t *vs = ks + KBUF;
-        const u32x4 zero = {0, 0, 0, 0};
-        u32x4 kx[2] = {to_bf16x8<DT>(R.k[0]), to_bf16x8<DT>(R.k[1])};
-        u32x4 v0 = to_bf16x8<DT>(R.v[0]), v1 = to_bf16x8<DT>(R.v[1]);
-        if (!(R.ok0 && R.ok1 && R.kt + kKeys <= kend)) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int r = (tid >> 4) + 16 * i;
-                const bool okp = (BS == 16 && i == 1) ? R.ok1 : R.ok0;
-                kx[i] = (R.kt + r < kend && okp) ? kx[i] : zero;
-            }
-            const bool okv = (BS == 16 && vp >= 8) ? R.ok1 : R.ok0;
-            v0 = (R.kt + 2 * vp < kend && okv) ? v0 : zero;
-            v1 = (R.kt + 2 * vp + 1 < kend && okv) ? v1 : zero;
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-            *reinterpret_cast<u32x4 *>(ks + ((tid >> 4) + 16 * i) * KPITCH + (tid & 15) * 16) = kx[i];
-        const int cp = vcol_of_key(2 * vp) >> 1;          // dword column of the key pair
-#pragma unroll
-        for (int j = 0; j < 8; ++j)       // bf16 j of both keys as one dword: (key 2p, key 2p + 1)
-            *reinterpret_cast<uint32_t *>(vs + (vdc * 8 + j) * VPITCH + cp * 4) =
-                __builtin_amdgcn_perm(v1[j >> 1], v0[j >> 1], (j & 1) ? 0x07060302u : 0x05040100u);
-    };
-
-    for (int w = sl.z; w < n_wg; w += sl.nz) {
-        const int wi = n_wg - 1 - w;                   // heaviest work first
-        const int item = wi * kWaves + wave;
-        const bool wvalid = item < n_items;
-        const int tb = (wvalid ? item : n_items - 1) / G;
-        const int g = (wvalid ? item : n_items - 1) % G;
-        const int h = kh * G + g;
-        const int r0 = tb * kRows;
-        const int last_item = (wi * kWaves + kWaves - 1 < n_items ? wi * kWaves + kWaves - 1 : n_items - 1);
-        const int tb_last = last_item / G;
-        const int rows_last = (tb_last + 1) * kRows < qlen ? (tb_last + 1) * kRows : qlen;
-        const int kend = q_offset + rows_last;          // keys the workgroup needs (<= len)
-        const int rows_w = r0 + kRows < qlen ? r0 + kRows : qlen;
-        const int kend_w = q_offset + rows_w;           // keys this wave needs
-        const int nt = (kend + kKeys - 1) / kKeys;
-
-        // Q^T as the B operand: lane holds query row r0 + lane % 32 (clamped
-        // to the last row; rows past q_len are computed and not stored),
-        // head_dim 16*ks + 8*(lane / 32) .. +8.
-        const int qrow = r0 + r32 < qlen ? r0 + r32 : qlen - 1;
-        const int qpos = q_offset + qrow;
-        u32x4 qhi[D / 16], qlo[D / 16];
-        {
-            const int64_t qbase = ((int64_t)(q0 + qrow) * a.n_q_heads + h) * D + 8 * hh;
-#pragma unroll
-            for (int ks = 0; ks < D / 16; ++ks) {
-                if constexpr (QF32) {
-                    const f32x4 *qp = reinterpret_cast<const f32x4 *>((const float *)a.q + qbase + 16 * ks);
-                    const f32x4 x0 = qp[0], x1 = qp[1];
-                    const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-                    uint32_t hv[8], lv[8];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) split_bf16(x[j], hv[j], lv[j]);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        qhi[ks][j] = hv[2 * j] | (hv[2 * j + 1] << 16);
-                        qlo[ks][j] = lv[2 * j] | (lv[2 * j + 1] << 16);
-                    }
-                } else {
-                    qhi[ks] = *reinterpret_cast<const u32x4 *>((const uint16_t *)a.q + qbase + 16 * ks);
-                    qlo[ks] = u32x4{0, 0, 0, 0};
-                }
-            }
-            // Consume Q here, once per work item: otherwise the compiler
-            // cannot tell inside the tile loop that these loads have landed
-            // and waits on the vector-memory counter there, i.e. on the page
-            // loads issued for later tiles.
-#pragma unroll
-            for (int ks = 0; ks < D / 16; ++ks) {
-                asm volatile("" ::"v"(qhi[ks]));
-                if constexpr (QF32) asm volatile("" ::"v"(qlo[ks]));
-            }
-        }
-
-        f32x16 acc[D / 32];
-#pragma unroll
-        for (int n = 0; n < D / 32; ++n)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) acc[n][i] = 0.0f;
-        float m_run = -INFINITY, l_run = 0.0f;
-
-        auto compute_tile = [&](int t, int buf) {
-            const uint8_t *ks_ = smem + buf * STAGE;
-            const uint8_t *vs_ = ks_ + KBUF;
-            const int kt = t * kKeys;
-            f32x16 s;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s[i] = 0.0f;
-#pragma unroll
-            for (int ks = 0; ks < D / 16; ++ks) {
-                const u32x4 ka = *reinterpret_cast<const u32x4 *>(ks_ + r32 * KPITCH + (16 * ks + 8 * hh) * 2);
-                s = mfma32(ka, qhi[ks], s);
-                if constexpr (QF32) s = mfma32(ka, qlo[ks], s);
-            }
-            // lane holds S[key kt + 8*(i/4) + 4*hh + i%4][query r32].  Only
-            // tiles that cross the causal diagonal of the wave's first row
-            // need the mask (a uniform test).  The scale (> 0) is applied
-            // after the max and inside the exponent's fma.
-            const bool diag = kt + kKeys - 1 > q_offset + r0;
-            const int kq = qpos - kt - 4 * hh;       // key i is visible when 8*(i/4) + i%4 <= kq
-            float sc[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) sc[i] = s[i];
-            if (diag) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) sc[i] = 8 * (i >> 2) + (i & 3) <= kq ? sc[i] : -INFINITY;
-            }
-            float mt = fmaxf(sc[0], sc[1]);
-#pragma unroll
-            for (int i = 2; i < 16; ++i) mt = fmaxf(mt, sc[i]);
-            mt = fmaxf(mt, __shfl_xor(mt, 32)) * a.scale_log2;
-            if (__ballot(mt > m_run + 8.0f) != 0ull) {
-                const float m_new = fmaxf(m_run, mt);
-                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);   // 0 on the first tile
-                l_run *= alpha;
-#pragma unroll
-                for (int n = 0; n < D / 32; ++n) acc[n] *= alpha;
-                m_run = m_new;
-            }
-            float p[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i)   // masked: exp2(-inf) = 0
-                p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], a.scale_log2, -m_run));
-            float ls = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) ls += p[i];
-            l_run += ls;
-#pragma unroll
-            for (int st = 0; st < 2; ++st) {
-                uint32_t hv[4], lv[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) split_pair(p[8 * st + 2 * j], p[8 * st + 2 * j + 1], hv[j], lv[j]);
-                const u32x4 phi = {hv[0], hv[1], hv[2], hv[3]}, plo = {lv[0], lv[1], lv[2], lv[3]};
-#pragma unroll
-                for (int n = 0; n < D / 32; ++n) {
-                    const u32x4 va = *reinterpret_cast<const u32x4 *>(vs_ + (32 * n + r32) * VPITCH +
-                                                                      (16 * st + 8 * hh) * 2);
-                    acc[n] = mfma32(va, phi, acc[n]);
-                    acc[n] = mfma32(va, plo, acc[n]);
-                }
-            }
-        };
-
-        // Two register sets hold the next two tiles: the loads of tile t + 2
-        // are issued before tile t is computed, and tile t + 1 (loaded a tile
-        // earlier) is staged after it, so every load has about two tiles of
-        // compute to land.  The loop is unrolled by two so both sets stay in
-        // fixed registers; even tiles use LDS buffer 0, odd tiles buffer 1.
-        TileRegs ra, rb;
-        fetch_ids(0, kend);
-        load_tile(0, ra);
-        fetch_ids(1, kend);
-        if (nt > 1) load_tile(1, rb);
-        fetch_ids(2, kend);
-        stage_tile(0, ra, kend);
-        __syncthreads();
-        for (int t = 0; t < nt; t += 2) {
-            if (t + 2 < nt) {
-                load_tile(t + 2, ra);
-                fetch_ids(t + 3, kend);
-            }
-            if (wvalid && t * kKeys < kend_w) compute_tile(t, 0);
-            if (t + 1 < nt) stage_tile(1, rb, kend);
-            __syncthreads();
-            if (t + 1 >= nt) break;
-            if (t + 3 < nt) {
-                load_tile(t + 3, rb);
-                fetch_ids(t + 4, kend);
-            }
-            if (wvalid && (t + 1) * kKeys < kend_w) compute_tile(t + 1, 1);
-            if (t + 2 < nt) stage_tile(0, ra, kend);
-            __syncthreads();
-        }
-
-        if (wvalid && r0 + r32 < qlen) {
-            const float l = l_run + __shfl_xor(l_run, 32);
-            const float inv = 1.0f / l;
-            const int64_t orow = ((int64_t)(q0 + r0 + r32) * a.n_q_heads + h) * D + 4 * hh;
-            if (a.out_dtype == AIR_KV_F32) {
-#pragma unroll
-                for (int n = 0; n < D / 32; ++n)
-#pragma unroll
-                    for (int i4 = 0; i4 < 4; ++i4)
-                        *reinterpret_cast<f32x4 *>((float *)a.out + orow + 32 * n + 8 * i4) =
-                            f32x4{acc[n][4 * i4], acc[n][4 * i4 + 1], acc[n][4 * i4 + 2], acc[n][4 * i4 + 3]} * inv;
-            } else {
-#pragma unroll
-                for (int n = 0; n < D / 32; ++n)
-#pragma unroll
-                    for (int i4 = 0; i4 < 4; ++i4) {
-                        const f32x2 x = f32x2{acc[n][4 * i4], acc[n][4 * i4 + 1]} * inv;
-                        const f32x2 y = f32x2{acc[n][4 * i4 + 2], acc[n][4 * i4 + 3]} * inv;
-                        *reinterpret_cast<u32x2 *>((uint16_t *)a.out + orow + 32 * n + 8 * i4) =
-                            u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2)),
-                                  __builtin_bit_cast(uint32_t, __builtin_convertvector(y, bf16x2))};
-                    }
-            }
-        }
-    }
-}
-
 // ---------------------------------------------------------------------------
-// bf16 pages: three LDS stages and tiles software-pipelined inside each wave.
+// Three LDS stages and tiles software-pipelined inside each wave (every page
+// dtype: 1-byte codes are dequantized to bf16 on their way to LDS).
 //
 // K and V tiles are staged row-major at padded pitches (below), which makes
 // the K operand reads, the staging stores and the transposing V reads
@@ -668,14 +351,18 @@ template <int N> struct Int { static constexpr int value = N; };
 // groups), V rows 320 bytes (rows start 16 banks apart, so the 4 rows x 64
 // bytes of a transposing read cover the 64 banks once).  Every LDS address
 // is then one per-lane register plus an immediate.
-constexpr int BF_KPITCH = D * 2 + 16, BF_VPITCH = D * 2 + 64;
-constexpr int KTILE_BYTES = kKeys * BF_KPITCH, VTILE_BYTES = kKeys * BF_VPITCH;
+constexpr int KPITCH = D * 2 + 16, VPITCH = D * 2 + 64;
+constexpr int KTILE_BYTES = kKeys * KPITCH, VTILE_BYTES = kKeys * VPITCH;
 constexpr int STAGE_BYTES = KTILE_BYTES + VTILE_BYTES;   // K then V
 
 
-template <int BS, bool QF32>
+template <int BS, bool QF32, int DT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AIRKV_PREFILL_WAVES_PER_EU)))
-void prefill_bf16_kernel(PrefillArgs a) {
+void prefill_pipe_kernel(PrefillArgs a) {
+    constexpr int EB = DT == AIR_KV_BF16 ? 2 : 1;   // bytes per page element
+    // bf16 pages: P as hi + lo bf16 halves; 1-byte pages, whose V operand is
+    // already a bf16 rounding of code * scale, take the hi half only
+    constexpr bool kSplitP = DT == AIR_KV_BF16;
     __shared__ __align__(16) uint8_t smem[kStages * STAGE_BYTES];
     static_assert(sizeof(smem) >= kRankLdsBytes, "dispatch ranking needs the tile LDS");
     const PrefillSlot sl = prefill_slot(a, reinterpret_cast<int *>(smem));
@@ -694,14 +381,20 @@ void prefill_bf16_kernel(PrefillArgs a) {
     const int n_wg = (n_items + kWaves - 1) / kWaves;
     const int r32 = lane & 31, hh = lane >> 5;
 
-    // Staging: thread covers the 16-byte chunk tid % 16 of key rows tid / 16
-    // and 16 + tid / 16, for K and V alike (constant offsets inside a page).
-    constexpr int PAGE_BYTES = BS * D * 2;
-    int g_off[2];
+    // Staging: thread covers head_dim 8 * (tid % 16) .. + 8 of key rows
+    // tid / 16 and 16 + tid / 16, for K and V alike (constant offsets inside
+    // a page); 1-byte pages also load the f32 scale of that group.
+    constexpr int PAGE_BYTES = BS * D * EB;
+    const int n_sc = DT == AIR_KV_BF16 ? 1 : D / a.scale_group;
+    int g_off[2], s_off[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) g_off[i] = ((((tid >> 4) + 16 * i) % BS) * D + (tid & 15) * 8) * 2;
+    for (int i = 0; i < 2; ++i) {
+        const int prow = ((tid >> 4) + 16 * i) % BS;
+        g_off[i] = (prow * D + (tid & 15) * 8) * EB;
+        s_off[i] = DT == AIR_KV_BF16 ? 0 : (prow * n_sc + ((tid & 15) * 8) / a.scale_group) * 4;
+    }
     struct TileRegs {
-        u32x4 k[2], v[2];
+        Raw8<DT> k[2], v[2];
         int kt;
         bool ok0, ok1;
     };
@@ -720,14 +413,21 @@ void prefill_bf16_kernel(PrefillArgs a) {
         R.ok1 = b1 >= 0 && b1 < a.num_blocks;
         const int64_t row0 = ((int64_t)(R.ok0 ? b0 : 0) * a.n_kv_heads + kh) * BS;
         const int64_t row1 = ((int64_t)(R.ok1 ? b1 : 0) * a.n_kv_heads + kh) * BS;
-        const __amdgpu_buffer_rsrc_t k0 = page_rsrc(a.k_pages, row0 * D * 2, PAGE_BYTES);
-        const __amdgpu_buffer_rsrc_t v0 = page_rsrc(a.v_pages, row0 * D * 2, PAGE_BYTES);
-        const __amdgpu_buffer_rsrc_t k1 = page_rsrc(a.k_pages, row1 * D * 2, PAGE_BYTES);
-        const __amdgpu_buffer_rsrc_t v1 = page_rsrc(a.v_pages, row1 * D * 2, PAGE_BYTES);
-        R.k[0] = __builtin_amdgcn_raw_buffer_load_b128(k0, g_off[0], 0, 0);
-        R.v[0] = __builtin_amdgcn_raw_buffer_load_b128(v0, g_off[0], 0, 0);
-        R.k[1] = __builtin_amdgcn_raw_buffer_load_b128(BS == 16 ? k1 : k0, g_off[1], 0, 0);
-        R.v[1] = __builtin_amdgcn_raw_buffer_load_b128(BS == 16 ? v1 : v0, g_off[1], 0, 0);
+        const __amdgpu_buffer_rsrc_t k0 = page_rsrc(a.k_pages, row0 * D * EB, PAGE_BYTES);
+        const __amdgpu_buffer_rsrc_t v0 = page_rsrc(a.v_pages, row0 * D * EB, PAGE_BYTES);
+        const __amdgpu_buffer_rsrc_t k1 = page_rsrc(a.k_pages, row1 * D * EB, PAGE_BYTES);
+        const __amdgpu_buffer_rsrc_t v1 = page_rsrc(a.v_pages, row1 * D * EB, PAGE_BYTES);
+        __amdgpu_buffer_rsrc_t ks0 = k0, vs0 = v0, ks1 = k1, vs1 = v1;   // unused for bf16
+        if constexpr (DT != AIR_KV_BF16) {
+            ks0 = page_rsrc(a.k_scales, row0 * n_sc * 4, BS * n_sc * 4);
+            vs0 = page_rsrc(a.v_scales, row0 * n_sc * 4, BS * n_sc * 4);
+            ks1 = page_rsrc(a.k_scales, row1 * n_sc * 4, BS * n_sc * 4);
+            vs1 = page_rsrc(a.v_scales, row1 * n_sc * 4, BS * n_sc * 4);
+        }
+        load_raw<DT>(k0, ks0, g_off[0], s_off[0], R.k[0]);
+        load_raw<DT>(v0, vs0, g_off[0], s_off[0], R.v[0]);
+        load_raw<DT>(BS == 16 ? k1 : k0, BS == 16 ? ks1 : ks0, g_off[1], s_off[1], R.k[1]);
+        load_raw<DT>(BS == 16 ? v1 : v0, BS == 16 ? vs1 : vs0, g_off[1], s_off[1], R.v[1]);
     };
     // Keys past the sequence and rows of out-of-pool blocks are staged as
     // zeros (stale page bytes may hold non-finite values); only the tiles
@@ -735,21 +435,48 @@ void prefill_bf16_kernel(PrefillArgs a) {
     auto stage_tile = [&](int slot, TileRegs &R, int kend) {
         uint8_t *ks = smem + slot * STAGE_BYTES;
         uint8_t *vs = ks + KTILE_BYTES;
+        u32x4 kb[2], vb[2];                       // as bf16 (1-byte pages dequantized)
+        if constexpr (DT == AIR_KV_BF16) {
+            // masked in the load registers themselves: no copies on the
+            // common path
+            if (!(R.ok0 && R.ok1 && R.kt + kKeys <= kend)) {
+                const u32x4 zero = {0, 0, 0, 0};
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const bool okp = (BS == 16 && i == 1) ? R.ok1 : R.ok0;
+                    const bool live = R.kt + (tid >> 4) + 16 * i < kend && okp;
+                    R.k[i].w = live ? R.k[i].w : zero;
+                    R.v[i].w = live ? R.v[i].w : zero;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int row = (tid >> 4) + 16 * i;
+                *reinterpret_cast<u32x4 *>(ks + row * KPITCH + (tid & 15) * 16) = R.k[i].w;
+                *reinterpret_cast<u32x4 *>(vs + row * VPITCH + (tid & 15) * 16) = R.v[i].w;
+            }
+            return;
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            kb[i] = to_bf16x8<DT>(R.k[i]);
+            vb[i] = to_bf16x8<DT>(R.v[i]);
+        }
         if (!(R.ok0 && R.ok1 && R.kt + kKeys <= kend)) {
             const u32x4 zero = {0, 0, 0, 0};
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const bool okp = (BS == 16 && i == 1) ? R.ok1 : R.ok0;
                 const bool live = R.kt + (tid >> 4) + 16 * i < kend && okp;
-                R.k[i] = live ? R.k[i] : zero;
-                R.v[i] = live ? R.v[i] : zero;
+                kb[i] = live ? kb[i] : zero;
+                vb[i] = live ? vb[i] : zero;
             }
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int row = (tid >> 4) + 16 * i;
-            *reinterpret_cast<u32x4 *>(ks + row * BF_KPITCH + (tid & 15) * 16) = R.k[i];
-            *reinterpret_cast<u32x4 *>(vs + row * BF_VPITCH + (tid & 15) * 16) = R.v[i];
+            *reinterpret_cast<u32x4 *>(ks + row * KPITCH + (tid & 15) * 16) = kb[i];
+            *reinterpret_cast<u32x4 *>(vs + row * VPITCH + (tid & 15) * 16) = vb[i];
         }
     };
 
@@ -814,7 +541,7 @@ void prefill_bf16_kernel(PrefillArgs a) {
             for (int i = 0; i < 16; ++i) s[i] = 0.0f;
 #pragma unroll
             for (int ks = 0; ks < D / 16; ++ks) {
-                const u32x4 kA = *reinterpret_cast<const u32x4 *>(ks_ + r32 * BF_KPITCH + (2 * ks + hh) * 16);
+                const u32x4 kA = *reinterpret_cast<const u32x4 *>(ks_ + r32 * KPITCH + (2 * ks + hh) * 16);
                 s = mfma32(kA, qhi[ks], s);
                 if constexpr (QF32) s = mfma32(kA, qlo[ks], s);
             }
@@ -859,20 +586,28 @@ void prefill_bf16_kernel(PrefillArgs a) {
             for (int st = 0; st < 2; ++st) {
                 uint32_t hv[4], lv[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) split_pair(p[8 * st + 2 * j], p[8 * st + 2 * j + 1], hv[j], lv[j]);
+                for (int j = 0; j < 4; ++j) {
+                    if constexpr (kSplitP) {
+                        split_pair(p[8 * st + 2 * j], p[8 * st + 2 * j + 1], hv[j], lv[j]);
+                    } else {
+                        const f32x2 pv = {p[8 * st + 2 * j], p[8 * st + 2 * j + 1]};
+                        hv[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(pv, bf16x2));
+                        lv[j] = 0;
+                    }
+                }
                 const u32x4 phi = {hv[0], hv[1], hv[2], hv[3]}, plo = {lv[0], lv[1], lv[2], lv[3]};
                 const int vrow = 16 * st + 4 * hh + (sl >> 2);           // keys kb .. kb + 3, then + 8
 #pragma unroll
                 for (int n = 0; n < D / 32; ++n) {
                     const int col = 32 * n + 16 * (grp & 1) + 4 * (sl & 3);   // bf16 column of the 8 bytes
                     const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) s16x4 *)(vs_ + vrow * BF_VPITCH + col * 2));
+                        (__attribute__((address_space(3))) s16x4 *)(vs_ + vrow * VPITCH + col * 2));
                     const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) s16x4 *)(vs_ + (vrow + 8) * BF_VPITCH + col * 2));
+                        (__attribute__((address_space(3))) s16x4 *)(vs_ + (vrow + 8) * VPITCH + col * 2));
                     const u32x2 a0 = __builtin_bit_cast(u32x2, t0), a1 = __builtin_bit_cast(u32x2, t1);
                     const u32x4 va = {a0[0], a0[1], a1[0], a1[1]};
                     acc[n] = mfma32(va, phi, acc[n]);
-                    acc[n] = mfma32(va, plo, acc[n]);
+                    if constexpr (kSplitP) acc[n] = mfma32(va, plo, acc[n]);
                 }
             }
         };
@@ -914,9 +649,10 @@ void prefill_bf16_kernel(PrefillArgs a) {
                 __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
+            constexpr int kPv = kSplitP ? 16 : 8;      // PV products per tile
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            for (int i = 0; i < kPv; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 16 / kPv, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
             }
@@ -967,17 +703,10 @@ void prefill_bf16_kernel(PrefillArgs a) {
 
 template <int BS, int DT>
 hipError_t launch_dt(const PrefillArgs &a, hipStream_t s, dim3 grid) {
-    if constexpr (DT == AIR_KV_BF16) {
-        if (a.q_dtype == AIR_KV_F32)
-            hipLaunchKernelGGL((prefill_bf16_kernel<BS, true>), grid, dim3(kThreads), 0, s, a);
-        else
-            hipLaunchKernelGGL((prefill_bf16_kernel<BS, false>), grid, dim3(kThreads), 0, s, a);
-    } else {
-        if (a.q_dtype == AIR_KV_F32)
-            hipLaunchKernelGGL((prefill_kernel<BS, true, DT>), grid, dim3(kThreads), 0, s, a);
-        else
-            hipLaunchKernelGGL((prefill_kernel<BS, false, DT>), grid, dim3(kThreads), 0, s, a);
-    }
+    if (a.q_dtype == AIR_KV_F32)
+        hipLaunchKernelGGL((prefill_pipe_kernel<BS, true, DT>), grid, dim3(kThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL((prefill_pipe_kernel<BS, false, DT>), grid, dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 
