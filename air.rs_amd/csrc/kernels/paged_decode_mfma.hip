@@ -105,6 +105,24 @@ __device__ __forceinline__ void split_bf16(float x, uint32_t &hi, uint32_t &lo) 
     lo = bf16_bits(x - __uint_as_float(hi << 16));
 }
 
+// The same for a pair of finite values, packed (element 0 in the low half),
+// with the hardware round-to-nearest-even conversions.
+__device__ __forceinline__ void split_pair(float x, float y, uint32_t &hi, uint32_t &lo) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const f32x2 v = {x, y};
+    const bf16x2 h = __builtin_convertvector(v, bf16x2);
+    const f32x2 r = v - __builtin_convertvector(h, f32x2);
+    hi = __builtin_bit_cast(uint32_t, h);
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2));
+}
+
+__device__ __forceinline__ uint32_t bf16_pair(float x, float y) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{x, y}), bf16x2));
+}
+
 __device__ __forceinline__ void store_out(const DecodeArgs &a, int64_t idx, float v) {
     if (a.out_dtype == AIR_KV_F32) ((float *)a.out)[idx] = v;
     else ((uint16_t *)a.out)[idx] = bf16_rne(v);
@@ -468,7 +486,7 @@ void decode_mfma_kernel(DecodeArgs a) {
         // max, so the result is unchanged.
         if (__ballot(mt > m_run + 8.0f) != 0ull) {
             const float m_new = fmaxf(m_run, mt);
-            const float alpha = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - m_new);
+            const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
             l_run *= alpha;
 #pragma unroll
             for (int n = 0; n < DTILES; ++n) acc[n] *= alpha;
@@ -476,21 +494,24 @@ void decode_mfma_kernel(DecodeArgs a) {
         }
         float p[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p[i] = (sc[i] == -INFINITY) ? 0.0f : exp2f(sc[i] - m_run);
+        // (the select covers a tile whose tokens are all masked while the
+        // running max is still -inf)
+        for (int i = 0; i < 4; ++i) p[i] = (sc[i] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(sc[i] - m_run);
         l_run += (p[0] + p[1]) + (p[2] + p[3]);
         // P^T as the B operand (lane: tokens 4*g4 .. +3 of head r16).  bf16
         // pages take hi + lo bf16 halves (~16 mantissa bits); 1-byte pages,
         // whose V operand is already a bf16 rounding of code * scale, take
         // the hi half only.
-        uint32_t h[4], l[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if constexpr (QUANT) h[i] = bf16_bits(p[i]);
-            else split_bf16(p[i], h[i], l[i]);
+        u32x2 p_hi, p_lo = {0, 0};
+        if constexpr (QUANT) {
+            p_hi = u32x2{bf16_pair(p[0], p[1]), bf16_pair(p[2], p[3])};
+        } else {
+            uint32_t h0, l0, h1, l1;
+            split_pair(p[0], p[1], h0, l0);
+            split_pair(p[2], p[3], h1, l1);
+            p_hi = u32x2{h0, h1};
+            p_lo = u32x2{l0, l1};
         }
-        const u32x2 p_hi = {h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-        u32x2 p_lo = {0, 0};
-        if constexpr (!QUANT) p_lo = u32x2{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
         // V tile -> LDS as bf16 (token rows beyond the sequence are zeroed: p = 0
         // there, but stale page bytes may hold non-finite values)
         if constexpr (QUANT) {
