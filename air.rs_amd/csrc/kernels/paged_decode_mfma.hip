@@ -599,23 +599,25 @@ void decode_mfma_kernel(DecodeArgs a) {
 
 // Log-sum-exp merge of the pieces of one (sequence, kv head): one wave per
 // query head of the group, lane l holding head_dim columns 2l and 2l + 1.
-// The pieces' (max, sum) and partial outputs are loaded together, eight pieces
-// at a time, and folded with an online rescale, so the merge costs one memory
-// round trip after the prefix.  Also writes zeros for an empty sequence and
+// The pieces' (max, sum) and partial outputs are loaded together, sixteen
+// pieces at a time, and folded with an online rescale, so the merge costs one
+// memory round trip per sixteen pieces.  Also writes zeros for an empty sequence and
 // counts sequence lengths outside [0, max_blocks * block_size].
 template <int D>
 __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
     static_assert(D == 128, "lane holds two head_dim columns");
-    constexpr int kBatch = 8;
+    constexpr int kBatch = 16;
     const int b = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = a.group;
     const int64_t max_len = (int64_t)a.max_blocks * a.block_size;
-    if (tid == 0 && kh == 0 && (a.lens[b] < 0 || a.lens[b] > max_len)) atomicAdd(a.errors, 1ull);
+    if (tid == 0 && kh == 0 && blockIdx.z == 0 && (a.lens[b] < 0 || a.lens[b] > max_len))
+        atomicAdd(a.errors, 1ull);
     const int p0 = a.prefix[b], p1 = a.prefix[b + 1];
     const int64_t obase = ((int64_t)b * a.n_q_heads + kh * G) * D;
     if (p0 == p1) {                                      // empty sequence: zeros
-        for (int idx = tid; idx < G * D; idx += kThreads) store_out(a, obase + idx, 0.0f);
+        if (blockIdx.z == 0)
+            for (int idx = tid; idx < G * D; idx += kThreads) store_out(a, obase + idx, 0.0f);
         return;
     }
     const int chunk = slice_chunk(a.prefix[a.batch], a.slices);
@@ -624,7 +626,8 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
     const int n = w1 - w0 + 1;
     // row of (piece p, head h): row0 + p * G + h
     const int64_t row0 = ((int64_t)kh * a.slots + b + w0) * G;
-    for (int h = wave; h < G; h += kWaves) {
+    // one wave per query head of the group (grid z covers groups above kWaves)
+    for (int h = blockIdx.z * kWaves + wave; h < G; h += gridDim.z * kWaves) {
         float m = -INFINITY, l = 0.0f, o0 = 0.0f, o1 = 0.0f;
         for (int q0 = 0; q0 < n; q0 += kBatch) {
             float pm[kBatch], pl[kBatch];
@@ -641,7 +644,7 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
             for (int i = 0; i < kBatch; ++i) {
                 if (pm[i] == -INFINITY) continue;            // past the last piece (or all masked)
                 const float m_new = fmaxf(m, pm[i]);
-                const float sa = exp2f(m - m_new), sb = exp2f(pm[i] - m_new);
+                const float sa = __builtin_amdgcn_exp2f(m - m_new), sb = __builtin_amdgcn_exp2f(pm[i] - m_new);
                 l = l * sa + pl[i] * sb;
                 o0 = o0 * sa + pv[i].x * sb;
                 o1 = o1 * sa + pv[i].y * sb;
@@ -666,7 +669,8 @@ hipError_t launch_cfg(const DecodeArgs &a, hipStream_t s) {
     hipLaunchKernelGGL((decode_mfma_kernel<128, BS, QF32, DT>), grid, dim3(kThreads), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((decode_merge_kernel<128>), dim3((unsigned)a.batch, (unsigned)a.n_kv_heads),
+    hipLaunchKernelGGL((decode_merge_kernel<128>),
+                       dim3((unsigned)a.batch, (unsigned)a.n_kv_heads, (unsigned)((a.group + kWaves - 1) / kWaves)),
                        dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
