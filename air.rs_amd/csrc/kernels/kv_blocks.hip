@@ -1,6 +1,9 @@
 // Whole-block copies inside a pool: the page copy that copy-on-write needs
-// (BlockAllocator::cow_write only copies metadata, src/paged_attention.rs:160).
-// One workgroup per (pair, tensor); 16-byte vector copies.
+// (BlockAllocator::cow_write only copies metadata, src/paged_attention.rs:160),
+// and the moves between pages and a contiguous staging buffer that let the
+// host swap copies (KvSwapManager's closures, src/kv_swap.rs:55-98) travel as
+// one large transfer.  One workgroup per (block, tensor); 16-byte
+// non-temporal pieces, every load of a thread issued before its stores.
 #include <hip/hip_runtime.h>
 
 #include "../pool.hpp"
@@ -9,6 +12,31 @@ namespace airkv {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kUnroll = 8;   // 16-byte pieces in flight per thread: a 32 KB slab in one pass
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// bytes (a multiple of 16) from in to out.  The loads of a pass are all
+// issued before its stores: in and out are never proven disjoint, so a
+// load-store loop would wait for each store before the next load.
+__device__ __forceinline__ void move_slab(const uint8_t *in, uint8_t *out, uint64_t bytes) {
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(in);
+    u32x4 *dst = reinterpret_cast<u32x4 *>(out);
+    const uint64_t n16 = bytes / 16;
+    for (uint64_t base = 0; base < n16; base += (uint64_t)kThreads * kUnroll) {
+        u32x4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint64_t i = base + (uint64_t)u * kThreads + threadIdx.x;
+            if (i < n16) v[u] = __builtin_nontemporal_load(src + i);
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint64_t i = base + (uint64_t)u * kThreads + threadIdx.x;
+            if (i < n16) __builtin_nontemporal_store(v[u], dst + i);
+        }
+    }
+}
 
 struct CopyArgs {
     const int32_t *src, *dst;
@@ -27,9 +55,31 @@ __global__ __launch_bounds__(kThreads) void copy_blocks_kernel(CopyArgs a) {
         if (threadIdx.x == 0 && which == 0) atomicAdd(a.errors, 1ull);
         return;
     }
-    const uint4 *in = reinterpret_cast<const uint4 *>(a.bases[which] + (uint64_t)s * bytes);
-    uint4 *out = reinterpret_cast<uint4 *>(a.bases[which] + (uint64_t)d * bytes);
-    for (uint64_t i = threadIdx.x; i < bytes / 16; i += kThreads) out[i] = in[i];
+    move_slab(a.bases[which] + (uint64_t)s * bytes, a.bases[which] + (uint64_t)d * bytes, bytes);
+}
+
+// Block i of the list <-> staging + i * block_bytes, laid out as the host
+// buffers of air_kv_read_blocks / air_kv_write_blocks: K slab, V slab, K
+// scales, V scales.  The ids were checked on the host.
+struct StageArgs {
+    const int32_t *ids;
+    uint8_t *bases[4];
+    uint64_t slab_bytes[4];
+    uint8_t *staging;
+    uint64_t block_bytes;
+    int to_staging;
+};
+
+__global__ __launch_bounds__(kThreads) void stage_blocks_kernel(StageArgs a) {
+    const int i = blockIdx.x, which = blockIdx.y;
+    const uint64_t bytes = a.slab_bytes[which];
+    if (bytes == 0) return;
+    uint64_t off = 0;
+    for (int j = 0; j < which; ++j) off += a.slab_bytes[j];
+    uint8_t *st = a.staging + (uint64_t)i * a.block_bytes + off;
+    uint8_t *pg = a.bases[which] + (uint64_t)a.ids[i] * bytes;
+    if (a.to_staging) move_slab(pg, st, bytes);
+    else move_slab(st, pg, bytes);
 }
 
 }  // namespace
@@ -44,6 +94,22 @@ hipError_t launch_copy_blocks(const air_kv_pool &p, hipStream_t s, const int32_t
     a.slab_bytes[2] = a.slab_bytes[3] = p.scale_slab_bytes;
     a.errors = p.errors;
     hipLaunchKernelGGL(copy_blocks_kernel, dim3((unsigned)n, 4), dim3(kThreads), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_stage_blocks(const air_kv_pool &p, hipStream_t s, const int32_t *ids, int32_t n,
+                               void *staging, bool to_staging) {
+    if (n <= 0) return hipSuccess;
+    StageArgs a;
+    a.ids = ids;
+    a.bases[0] = (uint8_t *)p.k_pages; a.bases[1] = (uint8_t *)p.v_pages;
+    a.bases[2] = (uint8_t *)p.k_scales; a.bases[3] = (uint8_t *)p.v_scales;
+    a.slab_bytes[0] = a.slab_bytes[1] = p.page_slab_bytes;
+    a.slab_bytes[2] = a.slab_bytes[3] = p.scale_slab_bytes;
+    a.staging = (uint8_t *)staging;
+    a.block_bytes = p.block_bytes;
+    a.to_staging = to_staging ? 1 : 0;
+    hipLaunchKernelGGL(stage_blocks_kernel, dim3((unsigned)n, 4), dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 

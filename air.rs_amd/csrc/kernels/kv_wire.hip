@@ -8,7 +8,9 @@
 // via load8), 32 interleaved wire bytes out, so reads and writes stay
 // 16-byte coalesced.  The int8 variant rounds the values to bf16 (the wire
 // element), reduces their absmax over the whole block in LDS, and writes
-// round(x * (1 / scale)) codes in wire order with one f32 scale per block.
+// round(x * (1 / scale)) codes in wire order with one f32 scale per block;
+// blocks of up to 8 items per thread (bs 16, 8 heads, d 128 is exactly that)
+// stay in registers between the two steps, larger ones are read twice.
 #include <hip/hip_runtime.h>
 
 #include "../pool.hpp"
@@ -21,6 +23,7 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
+constexpr int kHeldItems = 8;   // (token, head, 8-element) items a thread holds for the int8 pack
 
 struct WireArgs {
     const int32_t *ids;
@@ -82,17 +85,84 @@ __global__ __launch_bounds__(kThreads) void kv_pack_kernel(WireArgs a) {
         return (((int64_t)t * a.n_kv_heads + h) * a.head_dim + 8 * c) * 2;   // wire element
     };
     if constexpr (!INT8) {
+        // up to kHeldItems items per thread loaded before any is stored (the
+        // compiler cannot move a load above a store it cannot prove disjoint)
         uint16_t *out = (uint16_t *)a.wire + (int64_t)blockIdx.x * wire_elems;
-        for (int it = threadIdx.x; it < items; it += kThreads) {
-            float k[8], v[8];
-            const int64_t we = load_item(it, k, v);
-            u32x4 lo, hi;
-            interleave(k, v, lo, hi);
-            __builtin_nontemporal_store(lo, reinterpret_cast<u32x4 *>(out + we));
-            __builtin_nontemporal_store(hi, reinterpret_cast<u32x4 *>(out + we + 8));
+        for (int base = 0; base < items; base += kThreads * kHeldItems) {
+            u32x4 lo[kHeldItems], hi[kHeldItems];
+            int64_t we[kHeldItems];
+#pragma unroll
+            for (int u = 0; u < kHeldItems; ++u) {
+                const int it = base + threadIdx.x + u * kThreads;
+                we[u] = -1;
+                if (it < items) {
+                    float k[8], v[8];
+                    we[u] = load_item(it, k, v);
+                    interleave(k, v, lo[u], hi[u]);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kHeldItems; ++u) {
+                if (we[u] < 0) continue;
+                __builtin_nontemporal_store(lo[u], reinterpret_cast<u32x4 *>(out + we[u]));
+                __builtin_nontemporal_store(hi[u], reinterpret_cast<u32x4 *>(out + we[u] + 8));
+            }
         }
+    } else if (items <= kThreads * kHeldItems) {
+        // the block held in registers as its bf16 wire pairs (k | v << 16):
+        // one read of the pages, the absmax over the held values, then codes
+        u32x4 wlo[kHeldItems], whi[kHeldItems];
+        float m = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kHeldItems; ++u) {
+            const int it = threadIdx.x + u * kThreads;
+            wlo[u] = whi[u] = u32x4{0, 0, 0, 0};
+            if (it < items) {
+                float k[8], v[8];
+                (void)load_item(it, k, v);
+                interleave(k, v, wlo[u], whi[u]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    m = absmax_step(m, __uint_as_float(wlo[u][j] << 16));
+                    m = absmax_step(m, __uint_as_float(wlo[u][j] & 0xFFFF0000u));
+                    m = absmax_step(m, __uint_as_float(whi[u][j] << 16));
+                    m = absmax_step(m, __uint_as_float(whi[u][j] & 0xFFFF0000u));
+                }
+            }
+        }
+        const float max_val = block_absmax(m, s_red);
+        float scale, inv;
+        {
+#pragma clang fp contract(off)
+            scale = max_val > 0.0f ? max_val / 127.0f : 1.0f;
+            inv = 1.0f / scale;
+        }
+        int8_t *out = a.codes + (int64_t)blockIdx.x * wire_elems;
+#pragma unroll
+        for (int u = 0; u < kHeldItems; ++u) {
+            const int it = threadIdx.x + u * kThreads;
+            if (it >= items) break;
+            const int t = it / (a.n_kv_heads * chunks);
+            const int rem = it - t * a.n_kv_heads * chunks;
+            const int h = rem / chunks, c = rem - h * chunks;
+            const int64_t we = (((int64_t)t * a.n_kv_heads + h) * a.head_dim + 8 * c) * 2;
+            u32x4 q;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t p0 = j < 2 ? wlo[u][2 * j] : whi[u][2 * j - 4];
+                const uint32_t p1 = j < 2 ? wlo[u][2 * j + 1] : whi[u][2 * j - 3];
+                const uint32_t c0 = (uint8_t)pd_code(__uint_as_float(p0 << 16), inv);
+                const uint32_t c1 = (uint8_t)pd_code(__uint_as_float(p0 & 0xFFFF0000u), inv);
+                const uint32_t c2 = (uint8_t)pd_code(__uint_as_float(p1 << 16), inv);
+                const uint32_t c3 = (uint8_t)pd_code(__uint_as_float(p1 & 0xFFFF0000u), inv);
+                q[j] = c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
+            }
+            __builtin_nontemporal_store(q, reinterpret_cast<u32x4 *>(out + we));
+        }
+        if (threadIdx.x == 0) a.wire_scales[blockIdx.x] = scale;
     } else {
-        // pass 1: absmax of the bf16 wire values; pass 2 re-reads (cache hits)
+        // larger blocks: pass 1 takes the absmax of the bf16 wire values,
+        // pass 2 reads the pages again
         float m = 0.0f;
         for (int it = threadIdx.x; it < items; it += kThreads) {
             float k[8], v[8];
@@ -147,31 +217,47 @@ __global__ __launch_bounds__(kThreads) void kv_unpack_kernel(WireArgs a) {
     const int ng = (DT == AIR_KV_INT8 || DT == AIR_KV_FP8) ? a.head_dim / a.scale_group : 1;
     const int lanes = (DT == AIR_KV_INT8 || DT == AIR_KV_FP8) ? a.scale_group / 8 : 1;
     // items are walked in whole rounds so every lane of a scale group (which
-    // share a row: chunks is a multiple of lanes) joins the shuffles
-    for (int base = 0; base < items; base += kThreads) {
-        const int it = base + (int)threadIdx.x;
-        const bool valid = it < items;
-        const int itc = valid ? it : 0;
-        const int t = itc / (a.n_kv_heads * chunks);
-        const int rem = itc - t * a.n_kv_heads * chunks;
-        const int h = rem / chunks, c = rem - h * chunks;
-        const int64_t we = (((int64_t)t * a.n_kv_heads + h) * a.head_dim + 8 * c) * 2;
-        const u32x4 lo = *reinterpret_cast<const u32x4 *>(in + we);
-        const u32x4 hi = *reinterpret_cast<const u32x4 *>(in + we + 8);
-        float k[8], v[8];
+    // share a row: chunks is a multiple of lanes) joins the shuffles; the
+    // wire pieces of kHeldItems rounds are loaded before any is stored
+    for (int base0 = 0; base0 < items; base0 += kThreads * kHeldItems) {
+        u32x4 wlo[kHeldItems], whi[kHeldItems];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            k[j] = __uint_as_float(lo[j] << 16);
-            v[j] = __uint_as_float(lo[j] & 0xFFFF0000u);
-            k[4 + j] = __uint_as_float(hi[j] << 16);
-            v[4 + j] = __uint_as_float(hi[j] & 0xFFFF0000u);
+        for (int u = 0; u < kHeldItems; ++u) {
+            const int it = base0 + u * kThreads + (int)threadIdx.x;
+            const int itc = it < items ? it : 0;
+            const int t = itc / (a.n_kv_heads * chunks);
+            const int rem = itc - t * a.n_kv_heads * chunks;
+            const int h = rem / chunks, c = rem - h * chunks;
+            const int64_t we = (((int64_t)t * a.n_kv_heads + h) * a.head_dim + 8 * c) * 2;
+            wlo[u] = *reinterpret_cast<const u32x4 *>(in + we);
+            whi[u] = *reinterpret_cast<const u32x4 *>(in + we + 8);
         }
-        const int64_t row = ((int64_t)blk * a.n_kv_heads + h) * a.block_size + t;
-        const int64_t elem = row * a.head_dim + 8 * c;
-        const int64_t sidx = row * ng + (8 * c) / (a.scale_group > 0 ? a.scale_group : 1);
-        const bool lead = (c % lanes) == 0;
-        store_row_chunk<DT>(k, a.k_pages, a.k_scales, elem, sidx, lead, lanes, valid);
-        store_row_chunk<DT>(v, a.v_pages, a.v_scales, elem, sidx, lead, lanes, valid);
+#pragma unroll
+        for (int u = 0; u < kHeldItems; ++u) {
+            const int base = base0 + u * kThreads;
+            if (base >= items) break;
+            const int it = base + (int)threadIdx.x;
+            const bool valid = it < items;
+            const int itc = valid ? it : 0;
+            const int t = itc / (a.n_kv_heads * chunks);
+            const int rem = itc - t * a.n_kv_heads * chunks;
+            const int h = rem / chunks, c = rem - h * chunks;
+            const u32x4 lo = wlo[u], hi = whi[u];
+            float k[8], v[8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                k[j] = __uint_as_float(lo[j] << 16);
+                v[j] = __uint_as_float(lo[j] & 0xFFFF0000u);
+                k[4 + j] = __uint_as_float(hi[j] << 16);
+                v[4 + j] = __uint_as_float(hi[j] & 0xFFFF0000u);
+            }
+            const int64_t row = ((int64_t)blk * a.n_kv_heads + h) * a.block_size + t;
+            const int64_t elem = row * a.head_dim + 8 * c;
+            const int64_t sidx = row * ng + (8 * c) / (a.scale_group > 0 ? a.scale_group : 1);
+            const bool lead = (c % lanes) == 0;
+            store_row_chunk<DT>(k, a.k_pages, a.k_scales, elem, sidx, lead, lanes, valid);
+            store_row_chunk<DT>(v, a.v_pages, a.v_scales, elem, sidx, lead, lanes, valid);
+        }
     }
 }
 

@@ -95,6 +95,7 @@ int air_kv_pool_destroy(air_kv_pool *p) {
     (void)hipFree(p->k_pages); (void)hipFree(p->v_pages);
     (void)hipFree(p->k_scales); (void)hipFree(p->v_scales);
     (void)hipFree(p->errors);
+    (void)hipFree(p->stage);
     (void)hipSetDevice(dev_prev);
     delete p;
     return AIR_KV_OK;
@@ -274,56 +275,93 @@ static int check_ids(const air_kv_pool *p, const int32_t *ids, int32_t n) {
     return AIR_KV_OK;
 }
 
-int air_kv_read_blocks(air_kv_pool *p, void *stream, const int32_t *ids, int32_t n, void *host_dst) {
-    if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
-    if (n < 0 || (n > 0 && (!ids || !host_dst))) return fail(AIR_KV_E_INVALID_ARG, "bad block list");
-    if (int rc = check_ids(p, ids, n)) return rc;
-    hipStream_t s = (hipStream_t)stream;
-    uint8_t *dst = (uint8_t *)host_dst;
-    for (int32_t i = 0; i < n; ++i) {
-        const size_t b = (size_t)ids[i];
-        uint8_t *o = dst + (size_t)i * p->block_bytes;
-        const void *srcs[4] = {(const uint8_t *)p->k_pages + b * p->page_slab_bytes,
-                               (const uint8_t *)p->v_pages + b * p->page_slab_bytes,
-                               p->k_scales ? (const uint8_t *)p->k_scales + b * p->scale_slab_bytes : nullptr,
-                               p->v_scales ? (const uint8_t *)p->v_scales + b * p->scale_slab_bytes : nullptr};
-        const size_t sizes[4] = {p->page_slab_bytes, p->page_slab_bytes, p->scale_slab_bytes,
-                                 p->scale_slab_bytes};
-        for (int j = 0; j < 4; ++j) {
-            if (!sizes[j]) continue;
-            hipError_t e = hipMemcpyAsync(o, srcs[j], sizes[j], hipMemcpyDeviceToHost, s);
-            if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(D2H)");
-            o += sizes[j];
+// Host swap copies.  Whole blocks move through a device staging buffer in
+// the host layout (K slab, V slab, K scales, V scales per block), so each
+// chunk of up to kStageBytes crosses PCIe as one transfer instead of one
+// transfer per slab.  The staging is allocated on the first call and kept;
+// if that allocation fails the slabs are copied one by one.
+static constexpr size_t kStageBytes = (size_t)64 << 20;
+
+static bool ensure_stage(air_kv_pool *p) {
+    if (p->stage) return true;
+    size_t nb = kStageBytes / p->block_bytes;
+    if (nb < 1) nb = 1;
+    void *mem = nullptr;
+    if (hipMalloc(&mem, nb * p->block_bytes + nb * sizeof(int32_t)) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    p->stage = mem;
+    p->stage_blocks = nb;
+    return true;
+}
+
+// The slabs of block b, in the host layout.
+static void block_slabs(const air_kv_pool *p, size_t b, uint8_t *ptrs[4], size_t sizes[4]) {
+    ptrs[0] = (uint8_t *)p->k_pages + b * p->page_slab_bytes;
+    ptrs[1] = (uint8_t *)p->v_pages + b * p->page_slab_bytes;
+    ptrs[2] = p->k_scales ? (uint8_t *)p->k_scales + b * p->scale_slab_bytes : nullptr;
+    ptrs[3] = p->v_scales ? (uint8_t *)p->v_scales + b * p->scale_slab_bytes : nullptr;
+    sizes[0] = sizes[1] = p->page_slab_bytes;
+    sizes[2] = sizes[3] = p->scale_slab_bytes;
+}
+
+static int move_blocks(air_kv_pool *p, hipStream_t s, const int32_t *ids, int32_t n, uint8_t *host,
+                       bool to_host) {
+    const size_t bb = p->block_bytes;
+    if (ensure_stage(p)) {
+        int32_t *dids = (int32_t *)((uint8_t *)p->stage + p->stage_blocks * bb);
+        for (int32_t c0 = 0; c0 < n; c0 += (int32_t)p->stage_blocks) {
+            const int32_t cn = n - c0 < (int32_t)p->stage_blocks ? n - c0 : (int32_t)p->stage_blocks;
+            hipError_t e = hipMemcpyAsync(dids, ids + c0, cn * sizeof(int32_t), hipMemcpyHostToDevice, s);
+            if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(ids)");
+            if (to_host) {
+                if ((e = airkv::launch_stage_blocks(*p, s, dids, cn, p->stage, true)) != hipSuccess)
+                    return hip_fail(e, "stage blocks");
+                if ((e = hipMemcpyAsync(host + (size_t)c0 * bb, p->stage, cn * bb, hipMemcpyDeviceToHost, s)) !=
+                    hipSuccess)
+                    return hip_fail(e, "hipMemcpyAsync(D2H)");
+            } else {
+                if ((e = hipMemcpyAsync(p->stage, host + (size_t)c0 * bb, cn * bb, hipMemcpyHostToDevice, s)) !=
+                    hipSuccess)
+                    return hip_fail(e, "hipMemcpyAsync(H2D)");
+                if ((e = airkv::launch_stage_blocks(*p, s, dids, cn, p->stage, false)) != hipSuccess)
+                    return hip_fail(e, "unstage blocks");
+            }
+        }
+    } else {
+        for (int32_t i = 0; i < n; ++i) {
+            uint8_t *ptrs[4];
+            size_t sizes[4];
+            block_slabs(p, (size_t)ids[i], ptrs, sizes);
+            uint8_t *h = host + (size_t)i * bb;
+            for (int j = 0; j < 4; ++j) {
+                if (!sizes[j]) continue;
+                hipError_t e = to_host ? hipMemcpyAsync(h, ptrs[j], sizes[j], hipMemcpyDeviceToHost, s)
+                                       : hipMemcpyAsync(ptrs[j], h, sizes[j], hipMemcpyHostToDevice, s);
+                if (e != hipSuccess) return hip_fail(e, to_host ? "hipMemcpyAsync(D2H)" : "hipMemcpyAsync(H2D)");
+                h += sizes[j];
+            }
         }
     }
     hipError_t e = hipStreamSynchronize(s);
     return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "hipStreamSynchronize");
 }
 
+int air_kv_read_blocks(air_kv_pool *p, void *stream, const int32_t *ids, int32_t n, void *host_dst) {
+    if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
+    if (n < 0 || (n > 0 && (!ids || !host_dst))) return fail(AIR_KV_E_INVALID_ARG, "bad block list");
+    if (int rc = check_ids(p, ids, n)) return rc;
+    if (n == 0) return AIR_KV_OK;
+    return move_blocks(p, (hipStream_t)stream, ids, n, (uint8_t *)host_dst, true);
+}
+
 int air_kv_write_blocks(air_kv_pool *p, void *stream, const int32_t *ids, int32_t n, const void *host_src) {
     if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
     if (n < 0 || (n > 0 && (!ids || !host_src))) return fail(AIR_KV_E_INVALID_ARG, "bad block list");
     if (int rc = check_ids(p, ids, n)) return rc;
-    hipStream_t s = (hipStream_t)stream;
-    const uint8_t *src = (const uint8_t *)host_src;
-    for (int32_t i = 0; i < n; ++i) {
-        const size_t b = (size_t)ids[i];
-        const uint8_t *in = src + (size_t)i * p->block_bytes;
-        void *dsts[4] = {(uint8_t *)p->k_pages + b * p->page_slab_bytes,
-                         (uint8_t *)p->v_pages + b * p->page_slab_bytes,
-                         p->k_scales ? (uint8_t *)p->k_scales + b * p->scale_slab_bytes : nullptr,
-                         p->v_scales ? (uint8_t *)p->v_scales + b * p->scale_slab_bytes : nullptr};
-        const size_t sizes[4] = {p->page_slab_bytes, p->page_slab_bytes, p->scale_slab_bytes,
-                                 p->scale_slab_bytes};
-        for (int j = 0; j < 4; ++j) {
-            if (!sizes[j]) continue;
-            hipError_t e = hipMemcpyAsync(dsts[j], in, sizes[j], hipMemcpyHostToDevice, s);
-            if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(H2D)");
-            in += sizes[j];
-        }
-    }
-    hipError_t e = hipStreamSynchronize(s);
-    return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "hipStreamSynchronize");
+    if (n == 0) return AIR_KV_OK;
+    return move_blocks(p, (hipStream_t)stream, ids, n, (uint8_t *)const_cast<void *>(host_src), false);
 }
 
 void air_kv_pool_read_cb(void *ctx, uint32_t block, uint8_t *dst, size_t bytes) {

@@ -20,6 +20,10 @@ struct air_kv_pool {
     size_t page_slab_bytes = 0;  // one block of K (or of V)
     size_t scale_slab_bytes = 0; // one block of K scales (or of V scales)
     size_t block_bytes = 0;      // K + V + scales of one block
+    // Host swap copies: device staging of whole blocks (host layout) plus
+    // their ids, allocated on first use and kept until the pool is destroyed.
+    void *stage = nullptr;
+    size_t stage_blocks = 0;     // blocks the staging holds
 };
 
 namespace airkv {
@@ -56,6 +60,8 @@ hipError_t launch_decode(const air_kv_pool &pool, hipStream_t s, const DecodePla
                          void *workspace, void *out, int32_t out_dtype);
 hipError_t launch_copy_blocks(const air_kv_pool &pool, hipStream_t s, const int32_t *src,
                               const int32_t *dst, int32_t n);
+hipError_t launch_stage_blocks(const air_kv_pool &pool, hipStream_t s, const int32_t *ids, int32_t n,
+                               void *staging, bool to_staging);
 size_t wire_block_bytes(const air_kv_pool &pool);
 hipError_t launch_pack_blocks(const air_kv_pool &pool, hipStream_t s, const int32_t *ids, int32_t n,
                               void *out);

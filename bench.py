@@ -246,6 +246,69 @@ def compress_leg(torch, iters=10):
             "blocks": nb, "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
 
 
+def blocks_leg(torch, iters=20):
+    """Page-granular block work (the f1 CoW / swap hooks and the f2 KvBlock
+    wire format) on a bf16 pool (bs 16, 8 kv heads, d 128: 64 KB of K+V per
+    block), 4096 shuffled blocks per call, device-resident:
+      copy_blocks      read + write of every block (CoW copy);
+      pack_blocks      pages read, [bs][heads][d][K|V] bf16 wire written;
+      unpack_blocks    wire read, pages written;
+      pack_blocks_int8 pages read, int8 wire codes + one f32 scale written.
+    Two disjoint block sets (and wire buffers) alternate between calls, so no
+    call finds its 512 MB in the 256 MB MALL.  The host swap copies
+    (read_blocks / write_blocks: synchronous, pageable host memory) are timed
+    on 1024 blocks with the wall clock; their rate is PCIe-inclusive and is
+    reported beside, never as a device figure."""
+    import numpy as np
+
+    import airkv
+    n = 4096
+    nb = 4 * n + 64
+    pool = airkv.KvPool(nb, 16, 8, 128, airkv.BF16)
+    for c0 in range(0, nb * 16, 1 << 17):
+        c1 = min(nb * 16, c0 + (1 << 17))
+        k = torch.randn(c1 - c0, 8, 128, device="cuda")
+        pool.append(k, torch.randn_like(k), torch.arange(c0, c1, dtype=torch.int64, device="cuda"))
+    del k
+    perm = np.random.default_rng(11).permutation(nb).astype(np.int32)
+    sets = [(torch.from_numpy(perm[j * 2 * n:j * 2 * n + n]).cuda(),
+             torch.from_numpy(perm[j * 2 * n + n:(j + 1) * 2 * n]).cuda()) for j in range(2)]
+    blk = pool.block_bytes
+    wires = [pool.pack_blocks(src) for src, _ in sets]
+    res = {"blocks": n, "block_bytes": blk}
+    flip = [0]
+
+    def rate(name, fn, nbytes):
+        def call():
+            fn(flip[0])
+            flip[0] ^= 1
+        call()
+        ms = timed_loop(torch, call, iters)
+        res[name] = {"gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "us": round(ms * 1e3, 1),
+                     "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+
+    rate("copy_blocks", lambda j: pool.copy_blocks(*sets[j]), 2 * n * blk + 8 * n)
+    rate("pack_blocks", lambda j: pool.pack_blocks(sets[j][0], out=wires[j]), 2 * n * blk + 4 * n)
+    rate("unpack_blocks", lambda j: pool.unpack_blocks(sets[j][1], wires[j]), 2 * n * blk + 4 * n)
+    rate("pack_blocks_int8", lambda j: pool.pack_blocks_int8(sets[j][0]), n * blk + n * blk // 2 + 8 * n)
+    ids = perm[:1024]
+    host = pool.read_blocks(ids)
+    for name, fn in (("host_read_blocks", lambda: pool.read_blocks(ids)),
+                     ("host_write_blocks", lambda: pool.write_blocks(ids, host))):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / 3
+        res[name] = {"gbps_pcie_inclusive": round(len(ids) * blk / dt / 1e9, 2), "ms": round(dt * 1e3, 2),
+                     "blocks": len(ids), "host_memory": "pageable"}
+    assert pool.error_count() == 0
+    pool.close()
+    return res
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -399,6 +462,8 @@ def main():
         log(f"prefill {extra['prefill_c5']['tflops']} TFLOP/s")
         extra["kv_compress_blocks"] = compress_leg(torch)
         log(f"compress blocks {extra['kv_compress_blocks']['gbps']} GB/s")
+        extra["kv_blocks"] = blocks_leg(torch)
+        log(f"block copy / wire {extra['kv_blocks']}")
 
     cpu = None
     if not args.no_cpu:
