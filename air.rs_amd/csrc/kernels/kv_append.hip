@@ -100,15 +100,29 @@ hipError_t launch_append(const air_kv_pool &p, hipStream_t s, const float *k, co
     a.k_pages = p.k_pages; a.v_pages = p.v_pages;
     a.k_scales = p.k_scales; a.v_scales = p.v_scales;
     a.errors = p.errors;
-    const int64_t threads = ((int64_t)n_tokens + 3) / 4 * 4 * p.desc.n_kv_heads * (p.desc.head_dim / 8);
-    const int64_t blocks = (threads + kThreads - 1) / kThreads;
-    if (blocks > INT32_MAX) return hipErrorInvalidValue;
-    dim3 grid((unsigned)blocks);
-    switch (p.desc.dtype) {
-    case AIR_KV_F32: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_F32>, grid, dim3(kThreads), 0, s, a); break;
-    case AIR_KV_BF16: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_BF16>, grid, dim3(kThreads), 0, s, a); break;
-    case AIR_KV_INT8: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_INT8>, grid, dim3(kThreads), 0, s, a); break;
-    default: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_FP8>, grid, dim3(kThreads), 0, s, a); break;
+    // a dispatch counts its work-items in 32 bits: long appends take several
+    // launches of at most kMaxBlocks workgroups, each a whole number of
+    // four-token groups
+    constexpr int64_t kMaxBlocks = ((int64_t)1 << 32) / kThreads - 1;
+    const int64_t per_token = (int64_t)p.desc.n_kv_heads * (p.desc.head_dim / 8);
+    const int64_t max_tokens = kMaxBlocks * kThreads / (4 * per_token) * 4;
+    for (int64_t t0 = 0; t0 < n_tokens; t0 += max_tokens) {
+        const int64_t nt = n_tokens - t0 < max_tokens ? n_tokens - t0 : max_tokens;
+        AppendArgs c = a;
+        c.k = k + t0 * per_token * 8;
+        c.v = v + t0 * per_token * 8;
+        c.slots = slots + t0;
+        c.n_tokens = nt;
+        const int64_t threads = (nt + 3) / 4 * 4 * per_token;
+        dim3 grid((unsigned)((threads + kThreads - 1) / kThreads));
+        switch (p.desc.dtype) {
+        case AIR_KV_F32: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_F32>, grid, dim3(kThreads), 0, s, c); break;
+        case AIR_KV_BF16: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_BF16>, grid, dim3(kThreads), 0, s, c); break;
+        case AIR_KV_INT8: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_INT8>, grid, dim3(kThreads), 0, s, c); break;
+        default: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_FP8>, grid, dim3(kThreads), 0, s, c); break;
+        }
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
     }
     return hipGetLastError();
 }

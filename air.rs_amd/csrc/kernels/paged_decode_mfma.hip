@@ -475,7 +475,14 @@ void decode_mfma_kernel(DecodeArgs a) {
         // lane holds S[token 4*g4 + i][head r16]
         float sc[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sc[i] = 4 * g4 + i < nv ? s[i] * a.scale_log2 : -INFINITY;
+        for (int i = 0; i < 4; ++i) sc[i] = s[i] * a.scale_log2;
+        // only a sequence's last tile (or a tile of an out-of-pool block) is
+        // partial: the masks run on those tiles alone (nv is uniform)
+        const bool full = nv == 16;
+        if (!full) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[i] = 4 * g4 + i < nv ? sc[i] : -INFINITY;
+        }
         float mt = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
         mt = fmaxf(mt, __shfl_xor(mt, 16));
         mt = fmaxf(mt, __shfl_xor(mt, 32));
@@ -516,19 +523,23 @@ void decode_mfma_kernel(DecodeArgs a) {
         // there, but stale page bytes may hold non-finite values)
         if constexpr (QUANT) {
             const float vsc = __uint_as_float(t.vs);
-            const bool live = vrow < nv;
+            const bool live = full || vrow < nv;
             u32x2 *dst = reinterpret_cast<u32x2 *>(sv + vrow * PITCH);
+            u32x2 x[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const u32x2 x = dequant4<DT>(t.v[i >> 2][i & 3], vsc);
-                dst[(vcol / 4 + i) ^ (vrow & 7)] = live ? x : u32x2{0, 0};
+            for (int i = 0; i < 8; ++i) x[i] = dequant4<DT>(t.v[i >> 2][i & 3], vsc);
+            if (!full) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) x[i] = live ? x[i] : u32x2{0, 0};
             }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dst[(vcol / 4 + i) ^ (vrow & 7)] = x[i];
         } else {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int row = v * 4 + vrow;
                 u32x4 x = t.v[v];
-                if (row >= nv) x = u32x4{0, 0, 0, 0};
+                if (!full && row >= nv) x = u32x4{0, 0, 0, 0};
                 u32x2 *dst = reinterpret_cast<u32x2 *>(sv + row * PITCH);
                 dst[(vcol / 4) ^ (row & 7)] = u32x2{x[0], x[1]};
                 dst[(vcol / 4 + 1) ^ (row & 7)] = u32x2{x[2], x[3]};

@@ -735,7 +735,9 @@ hipError_t launch_prefill(const PrefillArgs &a, int dtype, int block_size, int32
     // slots, so a sequence longer than max_q_len is still covered completely.
     const int64_t ntb = ((int64_t)(max_q_len > 0 ? max_q_len : 1) + kRows - 1) / kRows;
     int64_t nz = (ntb * a.group + kWaves - 1) / kWaves;
-    const int64_t cap = (int64_t)0x7fffffff / ((int64_t)a.batch * a.n_kv_heads);
+    // a dispatch counts its work-items in 32 bits: at most 2^32 / 256 - 1
+    // workgroups (fewer slots per sequence only lengthen each slot's stride)
+    const int64_t cap = ((int64_t)0xffffffff / kThreads) / ((int64_t)a.batch * a.n_kv_heads);
     nz = nz > cap ? cap : nz;
     if (nz < 1) return hipErrorInvalidConfiguration;
     const dim3 grid((unsigned)((int64_t)a.batch * a.n_kv_heads * nz));
