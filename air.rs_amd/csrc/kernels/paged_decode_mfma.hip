@@ -70,7 +70,7 @@ constexpr int kMinChunk = 4;               // tiles per slice at least
 #define AIRKV_DECODE_RING 3               // tile register sets per wave, bf16 pages (ring - 1 in flight)
 #endif
 #ifndef AIRKV_DECODE_QRING
-#define AIRKV_DECODE_QRING 3              // the same for 1-byte pages
+#define AIRKV_DECODE_QRING 2              // the same for 1-byte pages (fewer in flight measured faster)
 #endif
 #ifndef AIRKV_DECODE_NT_LOADS
 #define AIRKV_DECODE_NT_LOADS 1            // non-temporal K/V loads
