@@ -67,10 +67,10 @@ constexpr int kMinChunk = 4;               // tiles per slice at least
 #define AIRKV_DECODE_QWAVES_PER_EU 3       // the same for 1-byte pages (fewer raw registers per tile)
 #endif
 #ifndef AIRKV_DECODE_RING
-#define AIRKV_DECODE_RING 3               // tile register sets per wave, bf16 pages (ring - 1 in flight)
+#define AIRKV_DECODE_RING 2               // tile register sets per wave, bf16 pages (ring - 1 in flight)
 #endif
 #ifndef AIRKV_DECODE_QRING
-#define AIRKV_DECODE_QRING 2              // the same for 1-byte pages (fewer in flight measured faster)
+#define AIRKV_DECODE_QRING 2              // the same for 1-byte pages
 #endif
 #ifndef AIRKV_DECODE_NT_LOADS
 #define AIRKV_DECODE_NT_LOADS 1            // non-temporal K/V loads
@@ -344,17 +344,12 @@ void decode_mfma_kernel(DecodeArgs a) {
                 qlo[ks] = u32x4{0, 0, 0, 0};
             }
         }
-        // bf16 pages: consumed here, on the rare path that loads them;
-        // otherwise the compiler cannot tell at the QK products whether Q is
-        // still in flight, and since vector loads retire in order it waits
-        // for every load issued before (the next tiles' pages included) on
-        // every tile.  1-byte pages keep that wait: they measured 2.5% faster
-        // with it (c3 133.7 against 137.0 us).
-#pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) {
-            if constexpr (!QUANT) asm volatile("" ::"v"(qhi[ks]));
-            if constexpr (QF32 && !QUANT) asm volatile("" ::"v"(qlo[ks]));
-        }
+        // Q is loaded on a branch (a new sequence), so at the QK products the
+        // compiler waits for it as if it were in flight, and vector loads
+        // retire in order: every tile waits there for most of the next
+        // tile's page loads.  Consuming Q here instead (an empty asm use)
+        // removes that wait and measured slower on every page dtype: fewer
+        // loads in flight is faster for these scattered page reads.
     };
 
     f32x4 acc[DTILES];
