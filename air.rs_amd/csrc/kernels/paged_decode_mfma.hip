@@ -33,9 +33,11 @@
 //
 // Each wave resolves the sequence, block id and valid token count of 64 of its
 // tiles at once (lane k: tile k), then takes them with readlane, so tile
-// addresses live in scalar registers and no load waits on another.  A ring of
-// register sets rotates: all but one hold tiles in flight while the other is
-// computed.
+// addresses live in scalar registers and no load waits on another.  By
+// default a wave loads a tile and then computes it, with nothing else in
+// flight: the other waves of its SIMD overlap its loads, and for these
+// scattered page reads that measured faster than keeping one or two more
+// tiles in flight per wave (a ring of register sets, a build-time knob).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -67,10 +69,10 @@ constexpr int kMinChunk = 4;               // tiles per slice at least
 #define AIRKV_DECODE_QWAVES_PER_EU 3       // the same for 1-byte pages (fewer raw registers per tile)
 #endif
 #ifndef AIRKV_DECODE_RING
-#define AIRKV_DECODE_RING 2               // tile register sets per wave, bf16 pages (ring - 1 in flight)
+#define AIRKV_DECODE_RING 1               // tile register sets per wave, bf16 pages (ring - 1 in flight)
 #endif
 #ifndef AIRKV_DECODE_QRING
-#define AIRKV_DECODE_QRING 2              // the same for 1-byte pages
+#define AIRKV_DECODE_QRING 1              // the same for 1-byte pages
 #endif
 #ifndef AIRKV_DECODE_NT_LOADS
 #define AIRKV_DECODE_NT_LOADS 1            // non-temporal K/V loads
