@@ -75,15 +75,21 @@ constexpr int kMinChunk = 4;               // tiles per slice at least
 #define AIRKV_DECODE_QRING 1              // the same for 1-byte pages
 #endif
 #ifndef AIRKV_DECODE_NT_LOADS
-#define AIRKV_DECODE_NT_LOADS 1            // non-temporal K/V loads
+#define AIRKV_DECODE_NT_LOADS 1            // non-temporal K/V loads, bf16 pages
+#endif
+#ifndef AIRKV_DECODE_QNT_LOADS
+#define AIRKV_DECODE_QNT_LOADS 0           // the same for 1-byte pages (plain loads measured faster)
 #endif
 
 // Buffer descriptor word 3 for raw (untyped) buffer access on gfx9-class
 // GPUs, and the cache-policy bits of the K/V loads: 2 = nt, streaming.  K/V
 // bytes are read exactly once, and on MI355X random 4 KB page reads run at
-// ~6.85 TB/s with nt against ~6.05 TB/s without (measured).
+// ~6.85 TB/s with nt against ~6.05 TB/s without (measured); the bf16 decode
+// keeps that ratio (c2 105 against 118 us), while 1-byte pages (2 KB slabs)
+// measured 3% faster with plain loads.
 constexpr int kBufferWord3 = 0x00020000;
 constexpr int kLoadAux = AIRKV_DECODE_NT_LOADS ? 2 : 0;
+constexpr int kQLoadAux = AIRKV_DECODE_QNT_LOADS ? 2 : 0;
 
 __device__ __forceinline__ f32x4 mfma_qk(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
@@ -391,16 +397,16 @@ void decode_mfma_kernel(DecodeArgs a) {
         if constexpr (QUANT) {
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                t.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, k_boff + 16 * i, 0, kLoadAux);
-                t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, v_boff + 16 * i, 0, kLoadAux);
+                t.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, k_boff + 16 * i, 0, kQLoadAux);
+                t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, v_boff + 16 * i, 0, kQLoadAux);
             }
             const int64_t srow = row0 * n_sc;
             const __amdgpu_buffer_rsrc_t rks = __builtin_amdgcn_make_buffer_rsrc(
                 (void *)(a.k_scales + srow), (short)0, 16 * n_sc * 4, kBufferWord3);
             const __amdgpu_buffer_rsrc_t rvs = __builtin_amdgcn_make_buffer_rsrc(
                 (void *)(a.v_scales + srow), (short)0, 16 * n_sc * 4, kBufferWord3);
-            t.ks = __builtin_amdgcn_raw_buffer_load_b32(rks, k_soff, 0, kLoadAux);
-            t.vs = __builtin_amdgcn_raw_buffer_load_b32(rvs, v_soff, 0, kLoadAux);
+            t.ks = __builtin_amdgcn_raw_buffer_load_b32(rks, k_soff, 0, kQLoadAux);
+            t.vs = __builtin_amdgcn_raw_buffer_load_b32(rvs, v_soff, 0, kQLoadAux);
         } else {
 #pragma unroll
             for (int ks = 0; ks < KSTEPS; ++ks)
