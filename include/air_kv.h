@@ -423,7 +423,10 @@ int air_kv_copy_blocks(air_kv_pool *pool, void *stream, const int32_t *src_block
 /* Page-granular device<->host copies for swap (the gpu_read / gpu_write
  * closures of src/kv_swap.rs:55-98).  ids are host int32; host buffers hold
  * n * block_bytes bytes, block i at offset i * block_bytes laid out as
- * K slab, V slab, K scales, V scales.  Both calls synchronise the stream. */
+ * K slab, V slab, K scales, V scales.  Both calls synchronise the stream.
+ * Blocks travel through a pool-owned 64 MB device staging buffer (allocated
+ * on the first call, freed with the pool), one PCIe transfer per 64 MB; two
+ * of these calls on one pool must not run concurrently. */
 int air_kv_read_blocks(air_kv_pool *pool, void *stream, const int32_t *ids, int32_t n, void *host_dst);
 int air_kv_write_blocks(air_kv_pool *pool, void *stream, const int32_t *ids, int32_t n,
                         const void *host_src);
