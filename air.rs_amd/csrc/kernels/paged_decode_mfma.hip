@@ -611,16 +611,39 @@ void decode_mfma_kernel(DecodeArgs a) {
     }
 }
 
-// Log-sum-exp merge of the pieces of one (sequence, kv head): one wave per
-// query head of the group, lane l holding head_dim columns 2l and 2l + 1.
-// The pieces' (max, sum) and partial outputs are loaded together, sixteen
-// pieces at a time, and folded with an online rescale, so the merge costs one
-// memory round trip per sixteen pieces.  Also writes zeros for an empty sequence and
-// counts sequence lengths outside [0, max_blocks * block_size].
-template <int D>
+// Log-sum-exp merge of the pieces of one (sequence, kv head), lane l holding
+// head_dim columns 2l and 2l + 1.  A wave loads the (max, sum) and partial
+// outputs of sixteen pieces together and folds them with an online rescale,
+// so it spends one memory round trip per sixteen pieces.  The kernel is bound
+// by those round trips and by how many waves it launches, not by bytes, so
+// the host picks WH, the waves per query head: one wave per head when the
+// batch's sequences have few pieces each (WH = 1, grid z covers groups above
+// four heads), and four waves per head when they have many (WH = 4, one
+// workgroup per head: wave w folds pieces w, w + 4, ... and the four parts
+// are folded in LDS in wave order).  Also writes zeros for an empty sequence
+// and counts sequence lengths outside [0, max_blocks * block_size].
+struct MergeAcc {
+    float m, l, o0, o1;
+};
+
+__device__ __forceinline__ void merge_fold(MergeAcc &c, float pm, float pl, float v0, float v1) {
+    if (pm == -INFINITY) return;                         // past the last piece (or all masked)
+    const float m_new = fmaxf(c.m, pm);
+    const float sa = __builtin_amdgcn_exp2f(c.m - m_new), sb = __builtin_amdgcn_exp2f(pm - m_new);
+    c.l = c.l * sa + pl * sb;
+    c.o0 = c.o0 * sa + v0 * sb;
+    c.o1 = c.o1 * sa + v1 * sb;
+    c.m = m_new;
+}
+
+template <int D, int WH>
 __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
     static_assert(D == 128, "lane holds two head_dim columns");
+    static_assert(WH == 1 || WH == kWaves, "one or all waves per head");
     constexpr int kBatch = 16;
+    constexpr int kHeadsPerGroup = kWaves / WH;          // query heads per workgroup
+    __shared__ float s_ml[kWaves][2];
+    __shared__ float2 s_o[kWaves][64];
     const int b = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = a.group;
@@ -638,40 +661,44 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
     const int w0 = p0 / chunk, w1 = (p1 - 1) / chunk;
     if (w0 == w1) return;                                // written by its slice
     const int n = w1 - w0 + 1;
+    const int sub = wave % WH;                           // this wave's share of the head's pieces
     // row of (piece p, head h): row0 + p * G + h
     const int64_t row0 = ((int64_t)kh * a.slots + b + w0) * G;
-    // one wave per query head of the group (grid z covers groups above kWaves)
-    for (int h = blockIdx.z * kWaves + wave; h < G; h += gridDim.z * kWaves) {
-        float m = -INFINITY, l = 0.0f, o0 = 0.0f, o1 = 0.0f;
-        for (int q0 = 0; q0 < n; q0 += kBatch) {
+    for (int h = blockIdx.z * kHeadsPerGroup + wave / WH; h < G; h += gridDim.z * kHeadsPerGroup) {
+        MergeAcc c{-INFINITY, 0.0f, 0.0f, 0.0f};
+        for (int q0 = sub; q0 < n; q0 += WH * kBatch) {
             float pm[kBatch], pl[kBatch];
             float2 pv[kBatch];
 #pragma unroll
             for (int i = 0; i < kBatch; ++i) {
-                const int p = q0 + i < n ? q0 + i : n - 1;
+                const int p = q0 + WH * i < n ? q0 + WH * i : q0;
                 const int64_t row = row0 + (int64_t)p * G + h;
-                pm[i] = q0 + i < n ? a.part_ml[row * 2] : -INFINITY;
+                pm[i] = q0 + WH * i < n ? a.part_ml[row * 2] : -INFINITY;
                 pl[i] = a.part_ml[row * 2 + 1];
                 pv[i] = *reinterpret_cast<const float2 *>(a.part_o + row * D + 2 * lane);
             }
 #pragma unroll
-            for (int i = 0; i < kBatch; ++i) {
-                if (pm[i] == -INFINITY) continue;            // past the last piece (or all masked)
-                const float m_new = fmaxf(m, pm[i]);
-                const float sa = __builtin_amdgcn_exp2f(m - m_new), sb = __builtin_amdgcn_exp2f(pm[i] - m_new);
-                l = l * sa + pl[i] * sb;
-                o0 = o0 * sa + pv[i].x * sb;
-                o1 = o1 * sa + pv[i].y * sb;
-                m = m_new;
-            }
+            for (int i = 0; i < kBatch; ++i) merge_fold(c, pm[i], pl[i], pv[i].x, pv[i].y);
         }
-        const float inv = 1.0f / l;
+        if constexpr (WH > 1) {                          // fold the four waves' parts
+            if (lane == 0) {
+                s_ml[wave][0] = c.m;
+                s_ml[wave][1] = c.l;
+            }
+            s_o[wave][lane] = float2{c.o0, c.o1};
+            __syncthreads();
+            if (sub != 0) continue;                      // one head per workgroup: loop ends
+            c = MergeAcc{-INFINITY, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int w = 0; w < WH; ++w) merge_fold(c, s_ml[w][0], s_ml[w][1], s_o[w][lane].x, s_o[w][lane].y);
+        }
+        const float inv = 1.0f / c.l;
         const int64_t oi = obase + (int64_t)h * D + 2 * lane;
         if (a.out_dtype == AIR_KV_F32) {
-            *reinterpret_cast<float2 *>((float *)a.out + oi) = float2{o0 * inv, o1 * inv};
+            *reinterpret_cast<float2 *>((float *)a.out + oi) = float2{c.o0 * inv, c.o1 * inv};
         } else {
             *reinterpret_cast<uint32_t *>((uint16_t *)a.out + oi) =
-                (uint32_t)bf16_rne(o0 * inv) | ((uint32_t)bf16_rne(o1 * inv) << 16);
+                (uint32_t)bf16_rne(c.o0 * inv) | ((uint32_t)bf16_rne(c.o1 * inv) << 16);
         }
     }
 }
@@ -683,9 +710,17 @@ hipError_t launch_cfg(const DecodeArgs &a, hipStream_t s) {
     hipLaunchKernelGGL((decode_mfma_kernel<128, BS, QF32, DT>), grid, dim3(kThreads), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((decode_merge_kernel<128>),
-                       dim3((unsigned)a.batch, (unsigned)a.n_kv_heads, (unsigned)((a.group + kWaves - 1) / kWaves)),
-                       dim3(kThreads), 0, s, a);
+    // Sequences average slices / batch pieces: past one round trip's worth,
+    // four waves share each head.
+    if (a.slices > 16 * a.batch) {
+        hipLaunchKernelGGL((decode_merge_kernel<128, kWaves>),
+                           dim3((unsigned)a.batch, (unsigned)a.n_kv_heads, (unsigned)a.group), dim3(kThreads), 0,
+                           s, a);
+    } else {
+        hipLaunchKernelGGL((decode_merge_kernel<128, 1>),
+                           dim3((unsigned)a.batch, (unsigned)a.n_kv_heads, (unsigned)((a.group + kWaves - 1) / kWaves)),
+                           dim3(kThreads), 0, s, a);
+    }
     return hipGetLastError();
 }
 
