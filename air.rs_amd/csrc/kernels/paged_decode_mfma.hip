@@ -613,8 +613,9 @@ void decode_mfma_kernel(DecodeArgs a) {
 
 // Log-sum-exp merge of the pieces of one (sequence, kv head), lane l holding
 // head_dim columns 2l and 2l + 1.  A wave loads the (max, sum) and partial
-// outputs of sixteen pieces together and folds them with an online rescale,
-// so it spends one memory round trip per sixteen pieces.  The kernel is bound
+// outputs of kBatch pieces together and folds them with an online rescale,
+// so it spends one memory round trip per kBatch pieces (16, or 4 when
+// sequences average about two pieces: fewer registers, more resident waves).  The kernel is bound
 // by those round trips and by how many waves it launches, not by bytes, so
 // the host picks WH, the waves per query head: one wave per head when the
 // batch's sequences have few pieces each (WH = 1, grid z covers groups above
@@ -636,11 +637,10 @@ __device__ __forceinline__ void merge_fold(MergeAcc &c, float pm, float pl, floa
     c.m = m_new;
 }
 
-template <int D, int WH>
+template <int D, int WH, int kBatch>
 __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
     static_assert(D == 128, "lane holds two head_dim columns");
     static_assert(WH == 1 || WH == kWaves, "one or all waves per head");
-    constexpr int kBatch = 16;
     constexpr int kHeadsPerGroup = kWaves / WH;          // query heads per workgroup
     __shared__ float s_ml[kWaves][2];
     __shared__ float2 s_o[kWaves][64];
@@ -713,11 +713,15 @@ hipError_t launch_cfg(const DecodeArgs &a, hipStream_t s) {
     // Sequences average slices / batch pieces: past one round trip's worth,
     // four waves share each head.
     if (a.slices > 16 * a.batch) {
-        hipLaunchKernelGGL((decode_merge_kernel<128, kWaves>),
+        hipLaunchKernelGGL((decode_merge_kernel<128, kWaves, 16>),
                            dim3((unsigned)a.batch, (unsigned)a.n_kv_heads, (unsigned)a.group), dim3(kThreads), 0,
                            s, a);
-    } else {
-        hipLaunchKernelGGL((decode_merge_kernel<128, 1>),
+    } else if (a.slices > 2 * a.batch) {
+        hipLaunchKernelGGL((decode_merge_kernel<128, 1, 16>),
+                           dim3((unsigned)a.batch, (unsigned)a.n_kv_heads, (unsigned)((a.group + kWaves - 1) / kWaves)),
+                           dim3(kThreads), 0, s, a);
+    } else {                    // about two pieces per sequence: fewer registers, more waves resident
+        hipLaunchKernelGGL((decode_merge_kernel<128, 1, 4>),
                            dim3((unsigned)a.batch, (unsigned)a.n_kv_heads, (unsigned)((a.group + kWaves - 1) / kWaves)),
                            dim3(kThreads), 0, s, a);
     }

@@ -154,6 +154,23 @@ def test_c5_shape_bf16_block32():
     assert err <= 1e-3
 
 
+@pytest.mark.parametrize("batch,lo,hi,dtype", [(300, 16, 700, airkv.BF16), (160, 300, 900, airkv.INT8),
+                                                (3, 20000, 30000, airkv.BF16)])
+def test_merge_modes(batch, lo, hi, dtype):
+    """The merge kernel's modes, picked from slices per sequence: many short
+    sequences (about two pieces each, four-piece batches), a middle case, and
+    a few long sequences (four waves per query head), plus an empty sequence."""
+    log(f"merge modes batch={batch} lens=[{lo}, {hi}) dtype={dtype}")
+    cfg = workloads.Config("merge", 32, 8, 128, 16, dtype, batch)
+    rng = np.random.default_rng(batch)
+    lens = [int(x) for x in rng.integers(lo, hi, batch)]
+    got, want, _ = _decode_case(cfg, lens, seed=60 + batch, empty=(batch // 2,))
+    err = rel_err(got, want)
+    log(f"  rel err {err:.2e}")
+    assert err <= TOL[dtype]
+    assert np.count_nonzero(got[batch // 2]) == 0
+
+
 @pytest.mark.parametrize("q_bf16,out_bf16", [(False, False), (False, True), (True, True)])
 def test_bf16_group16_query_and_output_dtypes(q_bf16, out_bf16):
     """GQA group 16 (32 q / 2 kv heads); f32 queries take the split hi/lo
