@@ -156,6 +156,122 @@ __global__ __launch_bounds__(kThreads) void key_compress_kernel(CompressArgs a) 
     }
 }
 
+// The same codec for sources whose rows come in contiguous runs of 64 (dense
+// rows, or pool blocks of n_kv_heads * block_size rows, a multiple of 64): a
+// wave takes 64 consecutive rows, lane l owning row l.  Loading row by row
+// sends each load instruction to 64 cache lines; here the wave reads its
+// rows' bytes as consecutive 16-byte pieces (each instruction covers whole
+// lines), 128 bytes of every row at a time, parks them in its own LDS slice
+// (row pitch 144 bytes: the 16 rows that one read phase serves start on 16
+// distinct 4-bank groups) and reads its own row back.  The folds then run in
+// the reference's order on the row kept in registers in its stored form
+// (f32, bf16 pairs or 1-byte codes, converted on each pass exactly as the
+// per-row loader converts them).
+constexpr int kStagePiece = 128;                     // row bytes staged per pass
+constexpr int kStagePitch = kStagePiece + 16;
+
+template <int DT>
+constexpr int elem_bytes() {
+    return DT == AIR_KV_F32 ? 4 : (DT == AIR_KV_BF16 ? 2 : 1);
+}
+
+template <int DT, int D>
+__global__ __launch_bounds__(kThreads) void key_compress_staged_kernel(CompressArgs a) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    constexpr int EB = elem_bytes<DT>();
+    constexpr int RB = D * EB;                           // row bytes
+    constexpr int PB = RB < kStagePiece ? RB : kStagePiece;
+    constexpr int CPR = PB / 16;                         // 16-byte chunks per row and pass
+    constexpr int W = (D + 63) / 64;
+    static_assert(RB % PB == 0 && PB % 16 == 0, "whole 16-byte chunks");
+    __shared__ __align__(16) uint8_t smem[kThreads / 64][64 * kStagePitch];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint8_t *lds = smem[wave];
+    const int64_t groups = (a.n_rows + 63) / 64;
+    for (int64_t g = (int64_t)blockIdx.x * (kThreads / 64) + wave; g < groups;
+         g += (int64_t)gridDim.x * (kThreads / 64)) {
+        const int64_t r0 = 64 * g, r = r0 + lane;
+        int64_t e0;
+        const bool live = row_elem(a.src, r0, D, e0);    // the 64 rows share one block
+        const uint8_t *gbase = (const uint8_t *)a.src.base + e0 * EB;
+        uint32_t raw[RB / 4];
+#pragma unroll
+        for (int p = 0; p < RB / PB; ++p) {
+            u32x4 c[CPR];
+#pragma unroll
+            for (int i = 0; i < CPR; ++i) {              // chunk k = 64 i + lane: row k / CPR
+                const int k = 64 * i + lane, row = k / CPR, ch = k % CPR;
+                c[i] = live && r0 + row < a.n_rows
+                           ? *reinterpret_cast<const u32x4 *>(gbase + (int64_t)row * RB + p * PB + 16 * ch)
+                           : u32x4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int i = 0; i < CPR; ++i) {
+                const int k = 64 * i + lane, row = k / CPR, ch = k % CPR;
+                *reinterpret_cast<u32x4 *>(lds + row * kStagePitch + 16 * ch) = c[i];
+            }
+#pragma unroll
+            for (int ch = 0; ch < CPR; ++ch) {
+                const u32x4 v = *reinterpret_cast<const u32x4 *>(lds + lane * kStagePitch + 16 * ch);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) raw[(p * PB + 16 * ch) / 4 + j] = v[j];
+            }
+        }
+        if (r >= a.n_rows) continue;
+        if (!live && a.errors && (r % a.src.rows_per_block) == 0) atomicAdd(a.errors, 1ull);
+        float sc[(EB == 1) ? D / 8 : 1];                 // scale of each 8 elements (1-byte rows;
+        if constexpr (EB == 1) {                         // scale groups are multiples of 8)
+            const int64_t el = e0 + (int64_t)lane * D;
+#pragma unroll
+            for (int j = 0; j < D / 8; ++j) sc[j] = live ? a.src.scales[(el + 8 * j) / a.src.scale_group] : 0.0f;
+        }
+        auto xv = [&](int j) -> float {
+            if constexpr (DT == AIR_KV_F32) {
+                return __uint_as_float(raw[j]);
+            } else if constexpr (DT == AIR_KV_BF16) {
+                return (j & 1) ? __uint_as_float(raw[j >> 1] & 0xFFFF0000u) : __uint_as_float(raw[j >> 1] << 16);
+            } else {
+#pragma clang fp contract(off)
+                const uint32_t byte = (raw[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+                const float val = DT == AIR_KV_INT8 ? (float)(int32_t)(int8_t)byte : fp8_decode(byte);
+                return val * sc[j >> 3];
+            }
+        };
+        float mean, mag;
+        uint64_t bits[W];
+        {
+#pragma clang fp contract(off)
+            float s = -0.0f, ss = -0.0f;               // both folds left to right, (:83-87), (:90)
+#pragma unroll
+            for (int j = 0; j < D; ++j) {
+                const float x = xv(j);
+                const float q = x * x;
+                s += x;
+                ss += q;
+            }
+            mean = s / (float)D;
+            mag = sqrtf(ss);
+            // convert again for the sign pass rather than keep D floats live
+#pragma unroll
+            for (int i = 0; i < RB / 4; ++i) asm volatile("" : "+v"(raw[i]));
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+                uint64_t word = 0;
+#pragma unroll
+                for (int j = 0; j < 64 && 64 * w + j < D; ++j)
+                    word |= (uint64_t)(xv(64 * w + j) >= mean) << j;   // (:95-100)
+                bits[w] = word;
+            }
+        }
+        if (!live) { mean = 0.0f; mag = 0.0f; for (int w = 0; w < W; ++w) bits[w] = 0; }
+#pragma unroll
+        for (int w = 0; w < W; ++w) a.bits[r * W + w] = bits[w];
+        a.f0[r] = mag;
+        a.f1[r] = mean;
+    }
+}
+
 // Four lanes per row, each folding a quarter: min / max need no fixed order
 // across quarters.  The fold keeps the accumulator unless x <= it (x < it for
 // max's mirror), so fold(L ++ R) from +inf equals fold_min(fold(L),
@@ -178,13 +294,35 @@ __global__ __launch_bounds__(kThreads) void value_compress_kernel(CompressArgs a
         bool live;
         load_row<DT, D, N>(a.src, r, x, live, part * N);
         if (!live && a.errors && part == 0 && (r % a.src.rows_per_block) == 0) atomicAdd(a.errors, 1ull);
+        // (:198-199).  The folds' value is the row's NaN-ignoring min / max,
+        // which the hardware min / max give in one instruction per element
+        // once signalling NaNs are quieted (given one, they return a NaN
+        // rather than the other operand); they may differ from the folds only
+        // in the sign of a zero result, so rows whose min or max is zero run
+        // the folds themselves.
         float lo = INFINITY, hi = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < N; ++j) {                  // (:198-199)
-            lo = fold_min(lo, x[j]);
-            hi = fold_max(hi, x[j]);
+        for (int j = 0; j < N; ++j) {
+            const float c = __builtin_canonicalizef(x[j]);
+            lo = __builtin_fminf(lo, c);
+            hi = __builtin_fmaxf(hi, c);
         }
-        // quarters 0+1 and 2+3, then the halves: the lower part is the left operand
+        lo = __builtin_fminf(lo, __shfl_xor(lo, 1));
+        hi = __builtin_fmaxf(hi, __shfl_xor(hi, 1));
+        lo = __builtin_fminf(lo, __shfl_xor(lo, 2));
+        hi = __builtin_fmaxf(hi, __shfl_xor(hi, 2));
+        if (lo == 0.0f || hi == 0.0f) {
+            lo = INFINITY;
+            hi = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                lo = fold_min(lo, x[j]);
+                hi = fold_max(hi, x[j]);
+            }
+        }
+        // quarters 0+1 and 2+3, then the halves: the lower part is the left
+        // operand (on rows that took the hardware min / max every quarter
+        // holds the same value and this changes nothing)
         float o = __shfl_xor(lo, 1);
         lo = (part & 1) ? fold_min(o, lo) : fold_min(lo, o);
         o = __shfl_xor(hi, 1);
@@ -209,9 +347,11 @@ __global__ __launch_bounds__(kThreads) void value_compress_kernel(CompressArgs a
             // infinite scale, i.e. tiny or non-finite data) divide exactly.
             const float y = 1.0f / scale;
             if (__builtin_isnormal(scale) && __builtin_isnormal(y)) {
-                // d = v - min >= 0 (or NaN) here, so round half away from zero
-                // is trunc + (fraction >= 0.5), and only the upper clamp and
-                // NaN need handling
+                // d = v - min >= 0 (or NaN) here, so round half away from
+                // zero is floor(quo + 0.5): the sum is exact below 256 (quo
+                // and quo + 0.5 share a binade or the sum lands on a power of
+                // two), and past 255.5 the clamp decides.  max(., 0) sends NaN
+                // to 0 (`as u8`), min(., 255) clamps.
 #pragma unroll
                 for (int j4 = 0; j4 < N / 4; ++j4) {
                     uint32_t w = 0;
@@ -221,9 +361,8 @@ __global__ __launch_bounds__(kThreads) void value_compress_kernel(CompressArgs a
                         const float q0 = d * y;
                         const float rem = __builtin_fmaf(-q0, scale, d);
                         const float quo = __builtin_fmaf(rem, y, q0);
-                        const float tq = __builtin_truncf(quo);
-                        float rq = tq + (quo - tq >= 0.5f ? 1.0f : 0.0f);
-                        rq = rq <= 255.0f ? rq : (rq == rq ? 255.0f : 0.0f);
+                        float rq = __builtin_floorf(quo + 0.5f);
+                        rq = __builtin_fminf(__builtin_fmaxf(rq, 0.0f), 255.0f);
                         w |= (uint32_t)rq << (8 * k);
                     }
                     q[j4] = w;
@@ -384,6 +523,13 @@ hipError_t launch_compress(CompressKind kind, const CompressArgs &a, int cus, hi
     if (a.n_rows == 0) return hipSuccess;
     const int lanes_per_row = kind == CompressKind::Value ? 4 : 1;
     const dim3 grid((unsigned)grid_for(a.n_rows * lanes_per_row, kThreads, cus));
+    // rows in contiguous runs of 64: the staged key codec, one wave per 64 rows
+    const bool runs64 = !a.src.ids || a.src.rows_per_block % 64 == 0;
+    if (kind == CompressKind::Key && runs64) {
+        const dim3 g((unsigned)grid_for((a.n_rows + 63) / 64 * 64, kThreads, cus));
+        AIRKV_LAUNCH_D(key_compress_staged_kernel, a, s, g)
+        return hipGetLastError();
+    }
     switch (kind) {
     case CompressKind::Key: AIRKV_LAUNCH_D(key_compress_kernel, a, s, grid) break;
     case CompressKind::Value: AIRKV_LAUNCH_D(value_compress_kernel, a, s, grid) break;

@@ -39,6 +39,14 @@ def _edge_rows(d):
     rows.append(r)                                                    # all NaN
     r = np.zeros(d, np.float32); r[::3] = 1.0; r[1::3] = -0.0
     rows.append(r)                                                    # +0 / -0 tie order in min / max
+    r = np.zeros(d, np.float32); r[::3] = -1.0; r[1::3] = -0.0
+    rows.append(r)                                                    # the same for max
+    r = np.linspace(-2, 3, d).astype(np.float32)
+    r.view(np.uint32)[2::7] = np.uint32(0x7F800001)                   # signalling NaNs are ignored too
+    r.view(np.uint32)[4] = np.uint32(0xFFA00000)
+    rows.append(r)
+    r = np.full(d, -0.0, np.float32); r[d // 2:] = 0.0
+    rows.append(r)                                                    # -0 then +0: the last zero wins
     return np.stack(rows)
 
 
