@@ -639,6 +639,11 @@ void prefill_pipe_kernel(PrefillArgs a) {
             // tile reads stale but in-bounds LDS that is never used.  One
             // basic block then holds tile t + 1's S^T products and tile t's
             // exponentials and PV products, interleaved below.
+            // The products and exponentials run at raised wave priority and
+            // staging, the barrier and the page loads at the base one: when
+            // both waves of a SIMD can issue, the one computing goes first
+            // (measured 0-7% faster across chunk mixes, none slower).
+            __builtin_amdgcn_s_setprio(1);
             softmax_head(t, s_cur);
             s_next = qk((S + 1) % kStages);
             softmax_pv(S, s_cur);
@@ -656,6 +661,7 @@ void prefill_pipe_kernel(PrefillArgs a) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
             }
+            __builtin_amdgcn_s_setprio(0);
             if (t + 2 < nt) stage_tile((S + 2) % kStages, R, kend);
             __syncthreads();
             if (t + 3 < nt) {
