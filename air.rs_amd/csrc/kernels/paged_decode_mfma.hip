@@ -604,7 +604,13 @@ void decode_mfma_kernel(DecodeArgs a) {
                     if (i + j >= n) break;
                     const int jl = (j + kRing - 1) % kRing;      // the set freed by the previous tile
                     ok[jl] = load_tile(clampi(i + j + kRing - 1), ring[jl]);
+                    // 1-byte pages: a tile's dequantization and products at
+                    // raised wave priority, so a SIMD's computing wave issues
+                    // ahead of one that is waiting to load (c4 ~2% faster;
+                    // bf16 pages measured no change)
+                    if constexpr (QUANT) __builtin_amdgcn_s_setprio(1);
                     compute_tile(c0 + i + j, i + j, ring[j], ok[j]);
+                    if constexpr (QUANT) __builtin_amdgcn_s_setprio(0);
                 }
             }
         }
