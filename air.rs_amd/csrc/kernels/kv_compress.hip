@@ -348,10 +348,11 @@ __global__ __launch_bounds__(kThreads) void value_compress_kernel(CompressArgs a
             const float y = 1.0f / scale;
             if (__builtin_isnormal(scale) && __builtin_isnormal(y)) {
                 // d = v - min >= 0 (or NaN) here, so round half away from
-                // zero is floor(quo + 0.5): the sum is exact below 256 (quo
-                // and quo + 0.5 share a binade or the sum lands on a power of
-                // two), and past 255.5 the clamp decides.  max(., 0) sends NaN
-                // to 0 (`as u8`), min(., 255) clamps.
+                // zero is floor(quo + 0.5) for quo >= 0.5 (checked against
+                // exact rounding for every float in [0.5, 300)) and 0 below;
+                // the only float below 0.5 where the sum rounds up to 1 is
+                // 0.5 - 2^-25.  max(., 0) sends NaN to 0 (`as u8`), min(., 255)
+                // clamps.
 #pragma unroll
                 for (int j4 = 0; j4 < N / 4; ++j4) {
                     uint32_t w = 0;
@@ -361,7 +362,7 @@ __global__ __launch_bounds__(kThreads) void value_compress_kernel(CompressArgs a
                         const float q0 = d * y;
                         const float rem = __builtin_fmaf(-q0, scale, d);
                         const float quo = __builtin_fmaf(rem, y, q0);
-                        float rq = __builtin_floorf(quo + 0.5f);
+                        float rq = quo < 0.5f ? 0.0f : __builtin_floorf(quo + 0.5f);
                         rq = __builtin_fminf(__builtin_fmaxf(rq, 0.0f), 255.0f);
                         w |= (uint32_t)rq << (8 * k);
                     }

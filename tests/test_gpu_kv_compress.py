@@ -47,6 +47,9 @@ def _edge_rows(d):
     rows.append(r)
     r = np.full(d, -0.0, np.float32); r[d // 2:] = 0.0
     rows.append(r)                                                    # -0 then +0: the last zero wins
+    r = np.zeros(d, np.float32); r[1] = 255.0                         # scale 1: codes round x itself
+    r[2:6] = [np.nextafter(np.float32(0.5), np.float32(0)), 0.5, np.nextafter(np.float32(1.5), np.float32(0)), 1.5]
+    rows.append(r)                                                    # just below / at the .5 ties
     return np.stack(rows)
 
 
