@@ -64,24 +64,35 @@ __device__ __forceinline__ float absmax_step(float m, float x) {
 
 // Rust `f32::round` then saturating `as i8` after a clamp to +-127
 // (src/kv_cache.rs:69): NaN -> 0.
+// Computed on the magnitude as pd_code below does, capped at 127 (checked
+// against the reference rule the same way).
 __device__ __forceinline__ int8_t q8_code(float x, float inv) {
 #pragma clang fp contract(off)
-    float r = roundf(x * inv);
-    if (r != r) return 0;
-    r = r < -127.0f ? -127.0f : (r > 127.0f ? 127.0f : r);
-    return (int8_t)(int)r;
+    const float y = x * inv;
+    const float a = __builtin_fabsf(y);
+    float r = !(a >= 0.5f) ? 0.0f : __builtin_floorf(a + 0.5f);
+    r = __builtin_fminf(r, 127.0f);
+    return (int8_t)(int)__builtin_copysignf(r, y);
 }
 
 // KvBlock::int8_quantize's code (src/pd_disagg.rs:78-80): Rust `f32::round`
 // then a saturating `as i8` with no clamp before it, so an infinite product
 // (1 / scale overflows when the block's absmax is subnormal) gives -128 or
 // 127, and NaN gives 0.
+// Computed on the magnitude: round half away from zero is 0 below 0.5 and
+// floor(|y| + 0.5) from there (equal to exact rounding for every float up to
+// 300; larger ones saturate anyway), a NaN fails the comparison and gives 0,
+// and the magnitude is capped at 128 before the sign goes back on (checked
+// against the reference rule for every float of magnitude below 300, the
+// special values and 2^24 random bit patterns).
 __device__ __forceinline__ int8_t pd_code(float x, float inv) {
 #pragma clang fp contract(off)
-    float r = roundf(x * inv);
-    if (r != r) return 0;
-    r = r < -128.0f ? -128.0f : (r > 127.0f ? 127.0f : r);
-    return (int8_t)(int)r;
+    const float y = x * inv;
+    const float a = __builtin_fabsf(y);
+    float r = !(a >= 0.5f) ? 0.0f : __builtin_floorf(a + 0.5f);
+    r = __builtin_fminf(r, 128.0f);
+    const int c = (int)__builtin_copysignf(r, y);
+    return (int8_t)(c > 127 ? 127 : c);
 }
 
 // Q8_0 scale from the group's absmax (src/kv_cache.rs:60-62).

@@ -207,15 +207,21 @@ def test_compress_blocks_matches_oracle(dtype):
     assert pool.error_count() == 0
 
 
-def test_compress_blocks_out_of_pool_ids_counted_and_zeroed():
+@pytest.mark.parametrize("n_kv", [2, 4])
+def test_compress_blocks_out_of_pool_ids_counted_and_zeroed(n_kv):
+    """32-row blocks take the row-by-row key codec, 64-row blocks the staged
+    one; out-of-pool ids are counted once and their rows come out zero."""
     torch = torch_mod()
-    pool = airkv.KvPool(8, 16, 2, 64, airkv.BF16)
+    pool = airkv.KvPool(8, 16, n_kv, 64, airkv.BF16)
+    pool.append(torch.randn(8 * 16, n_kv, 64, device="cuda"), torch.randn(8 * 16, n_kv, 64, device="cuda"),
+                torch.arange(8 * 16, dtype=torch.int64, device="cuda"))
     ids = torch.tensor([1, 99, -1], dtype=torch.int32, device="cuda")
     out = kc.compress_blocks(pool, ids)
     assert pool.error_count(reset=True) == 2
-    rows = 2 * 16
+    rows = n_kv * 16
     assert torch.all(out["key_magnitude"][rows:] == 0) and torch.all(out["value_codes"][rows:] == 0)
-    assert torch.all(out["value_scale"][rows:] == 0)
+    assert torch.all(out["value_scale"][rows:] == 0) and torch.all(out["key_mean"][rows:] == 0)
+    assert torch.all(out["key_magnitude"][:rows] > 0)
 
 
 def test_codec_argument_errors():
