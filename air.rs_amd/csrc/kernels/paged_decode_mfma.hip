@@ -654,16 +654,17 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = a.group;
     const int64_t max_len = (int64_t)a.max_blocks * a.block_size;
-    if (tid == 0 && kh == 0 && blockIdx.z == 0 && (a.lens[b] < 0 || a.lens[b] > max_len))
-        atomicAdd(a.errors, 1ull);
-    const int p0 = a.prefix[b], p1 = a.prefix[b + 1];
+    // every index the workgroup needs, loaded together (one round trip)
+    const int p0 = a.prefix[b], p1 = a.prefix[b + 1], ptot = a.prefix[a.batch];
+    const int len = a.lens[b];
+    if (tid == 0 && kh == 0 && blockIdx.z == 0 && (len < 0 || len > max_len)) atomicAdd(a.errors, 1ull);
     const int64_t obase = ((int64_t)b * a.n_q_heads + kh * G) * D;
     if (p0 == p1) {                                      // empty sequence: zeros
         if (blockIdx.z == 0)
             for (int idx = tid; idx < G * D; idx += kThreads) store_out(a, obase + idx, 0.0f);
         return;
     }
-    const int chunk = slice_chunk(a.prefix[a.batch], a.slices);
+    const int chunk = slice_chunk(ptot, a.slices);
     const int w0 = p0 / chunk, w1 = (p1 - 1) / chunk;
     if (w0 == w1) return;                                // written by its slice
     const int n = w1 - w0 + 1;
