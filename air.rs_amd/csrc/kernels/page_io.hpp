@@ -11,6 +11,15 @@
 
 namespace airkv {
 
+// Page rows are written with plain stores: the c2 append of 32768 tokens ran
+// in 70.4 us against 74.7 with non-temporal ones (same box, two runs each),
+// and wire unpacking was unchanged.  (Gather's contiguous outputs and the
+// block copies measured the other way and keep non-temporal stores.)
+template <typename T>
+__device__ __forceinline__ void pio_store(T v, T *p) {
+    *p = v;
+}
+
 typedef float pio_f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t pio_u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t pio_u32x2 __attribute__((ext_vector_type(2)));
@@ -65,8 +74,8 @@ __device__ __forceinline__ void store_row_chunk(const float (&x)[8], void *pages
     if constexpr (DT == AIR_KV_F32) {
         if (valid) {
             pio_f32x4 *o = reinterpret_cast<pio_f32x4 *>((float *)pages + elem);
-            __builtin_nontemporal_store(pio_f32x4{x[0], x[1], x[2], x[3]}, o);
-            __builtin_nontemporal_store(pio_f32x4{x[4], x[5], x[6], x[7]}, o + 1);
+            pio_store(pio_f32x4{x[0], x[1], x[2], x[3]}, o);
+            pio_store(pio_f32x4{x[4], x[5], x[6], x[7]}, o + 1);
         }
     } else if constexpr (DT == AIR_KV_BF16) {
         if (valid) {
@@ -75,7 +84,7 @@ __device__ __forceinline__ void store_row_chunk(const float (&x)[8], void *pages
             w[1] = (uint32_t)bf16_rne(x[2]) | ((uint32_t)bf16_rne(x[3]) << 16);
             w[2] = (uint32_t)bf16_rne(x[4]) | ((uint32_t)bf16_rne(x[5]) << 16);
             w[3] = (uint32_t)bf16_rne(x[6]) | ((uint32_t)bf16_rne(x[7]) << 16);
-            __builtin_nontemporal_store(w, reinterpret_cast<pio_u32x4 *>((uint16_t *)pages + elem));
+            pio_store(w, reinterpret_cast<pio_u32x4 *>((uint16_t *)pages + elem));
         }
     } else {
         // absmax fold from 0.0 with a NaN-ignoring max (src/kv_cache.rs:60,
@@ -106,7 +115,7 @@ __device__ __forceinline__ void store_row_chunk(const float (&x)[8], void *pages
             for (int j = 0; j < 4; ++j) hi |= (uint32_t)fp8_code(x[4 + j], scale) << (8 * j);
         }
         if (valid) {
-            __builtin_nontemporal_store(pio_u32x2{lo, hi}, reinterpret_cast<pio_u32x2 *>((uint8_t *)pages + elem));
+            pio_store(pio_u32x2{lo, hi}, reinterpret_cast<pio_u32x2 *>((uint8_t *)pages + elem));
             if (lead) scales[scale_idx] = scale;
         }
     }
