@@ -621,9 +621,10 @@ void decode_mfma_kernel(DecodeArgs a) {
 // head_dim columns 2l and 2l + 1.  A wave loads the (max, sum) and partial
 // outputs of kBatch pieces together and folds them with an online rescale,
 // so it spends one memory round trip per kBatch pieces (16, or 4 when
-// sequences average about two pieces: fewer registers, more resident waves).  The kernel is bound
-// by those round trips and by how many waves it launches, not by bytes, so
-// the host picks WH, the waves per query head: one wave per head when the
+// sequences average about two pieces: fewer registers, more resident
+// waves).  The kernel is bound by those round trips and by how many waves it
+// launches, not by bytes, so the host picks WH, the waves per query head:
+// one wave per head when the
 // batch's sequences have few pieces each (WH = 1, grid z covers groups above
 // four heads), and four waves per head when they have many (WH = 4, one
 // workgroup per head: wave w folds pieces w, w + 4, ... and the four parts
