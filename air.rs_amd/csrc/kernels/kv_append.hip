@@ -56,16 +56,19 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(AppendArgs a) {
     const bool valid = slot >= 0 && slot < a.num_slots;
     if (active && slot >= a.num_slots && c == 0 && h == 0) atomicAdd(a.errors, 1ull);
 
+    // the source rows are loaded whatever the slot turns out to be (every
+    // token's row exists), so their loads overlap the slot load instead of
+    // waiting for it
     float kx[8], vx[8];
-    if (valid) {
+    if (active) {
         const f32x4 *ks = reinterpret_cast<const f32x4 *>(a.k + row * a.head_dim + c * 8);
         const f32x4 *vs = reinterpret_cast<const f32x4 *>(a.v + row * a.head_dim + c * 8);
         const f32x4 k0 = __builtin_nontemporal_load(ks), k1 = __builtin_nontemporal_load(ks + 1);
         const f32x4 v0 = __builtin_nontemporal_load(vs), v1 = __builtin_nontemporal_load(vs + 1);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            kx[j] = k0[j]; kx[4 + j] = k1[j];
-            vx[j] = v0[j]; vx[4 + j] = v1[j];
+            kx[j] = valid ? k0[j] : 0.0f; kx[4 + j] = valid ? k1[j] : 0.0f;
+            vx[j] = valid ? v0[j] : 0.0f; vx[4 + j] = valid ? v1[j] : 0.0f;
         }
     } else {
 #pragma unroll
