@@ -37,9 +37,9 @@ class PoolDesc(ctypes.Structure):
                 ("dtype", ctypes.c_int32), ("scale_group", ctypes.c_int32)]
 
 
-READ_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint8),
+READ_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint8),
                            ctypes.c_size_t)
-WRITE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint8),
+WRITE_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint8),
                             ctypes.c_size_t)
 
 _P = ctypes.c_void_p
@@ -129,8 +129,8 @@ SIGNATURES = {
     "air_kv_copy_blocks": (_int, [_P, _P, _P, _P, _i32]),
     "air_kv_read_blocks": (_int, [_P, _P, _pi32, _i32, _P]),
     "air_kv_write_blocks": (_int, [_P, _P, _pi32, _i32, _P]),
-    "air_kv_pool_read_cb": (None, [_P, _u32, _P, _SZ]),
-    "air_kv_pool_write_cb": (None, [_P, _u32, _P, _SZ]),
+    "air_kv_pool_read_cb": (_int, [_P, _u32, _P, _SZ]),
+    "air_kv_pool_write_cb": (_int, [_P, _u32, _P, _SZ]),
     "air_kv_pool_error_count": (_int, [_P, _P, _pi64, _i32]),
 }
 

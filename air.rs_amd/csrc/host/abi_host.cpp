@@ -358,7 +358,7 @@ int air_kv_swap_evict(air_kv_swap *s, uint32_t seq, air_kv_block_read_fn read, v
     if (t && released && (int64_t)t->physical_blocks.size() > cap)
         return fail(AIR_KV_E_INVALID_ARG, "evict: cap %d below %zu blocks", cap, t->physical_blocks.size());
     std::vector<uint32_t> out;
-    int rc = s->impl.evict(seq, [&](uint32_t b, uint8_t *dst, size_t n) { read(ctx, b, dst, n); }, &out);
+    int rc = s->impl.evict(seq, [&](uint32_t b, uint8_t *dst, size_t n) { return read(ctx, b, dst, n); }, &out);
     if (rc) return rc;
     if (n_released) *n_released = (int32_t)out.size();
     if (released) std::memcpy(released, out.data(), out.size() * sizeof(uint32_t));
@@ -370,7 +370,7 @@ int air_kv_swap_restore(air_kv_swap *s, uint32_t seq, air_kv_block_write_fn writ
     if (!s || !write) return fail(AIR_KV_E_INVALID_ARG, "swap manager or write callback is NULL");
     std::vector<uint32_t> out;
     int rc = s->impl.restore(
-        seq, [&](uint32_t b, const uint8_t *src, size_t n) { write(ctx, b, src, n); }, &out);
+        seq, [&](uint32_t b, const uint8_t *src, size_t n) { return write(ctx, b, src, n); }, &out);
     if (rc) return rc;
     if (n_blocks) *n_blocks = (int32_t)out.size();
     if (blocks) {
@@ -398,7 +398,7 @@ int air_kv_swap_maybe_evict(air_kv_swap *s, uint32_t seq, int64_t free_threshold
     if (!s || !read) return fail(AIR_KV_E_INVALID_ARG, "swap manager or read callback is NULL");
     bool e = false;
     int rc = s->impl.maybe_evict(
-        seq, free_threshold, [&](uint32_t b, uint8_t *dst, size_t n) { read(ctx, b, dst, n); }, &e);
+        seq, free_threshold, [&](uint32_t b, uint8_t *dst, size_t n) { return read(ctx, b, dst, n); }, &e);
     if (evicted) *evicted = e ? 1 : 0;
     return rc;
 }

@@ -11,7 +11,9 @@ int KvSwapManager::evict(uint32_t seq, const ReadFn &read, std::vector<uint32_t>
     // copy device -> host before the blocks are released (:63-68)
     std::vector<uint32_t> blocks = t->physical_blocks;
     std::vector<uint8_t> buf(blocks.size() * block_bytes_);
-    for (size_t i = 0; i < blocks.size(); ++i) read(blocks[i], buf.data() + i * block_bytes_, block_bytes_);
+    for (size_t i = 0; i < blocks.size(); ++i)
+        if (int rc = read(blocks[i], buf.data() + i * block_bytes_, block_bytes_))
+            return rc < 0 ? rc : fail(AIR_KV_E_HIP, "evict: read of block %u failed (%d)", blocks[i], rc);
     int rc = seq_mgr_.swap_out(seq, released);
     if (rc) return rc;
     cpu_bytes_used_ += buf.size();
@@ -29,8 +31,17 @@ int KvSwapManager::restore(uint32_t seq, const WriteFn &write, std::vector<uint3
     size_t n = block_bytes_ ? buf.size() / block_bytes_ : 0;
     int rc = seq_mgr_.swap_in(seq, (int32_t)n, blocks);
     if (rc) return rc;
-    for (size_t i = 0; i < blocks->size(); ++i)
-        write((*blocks)[i], buf.data() + i * block_bytes_, block_bytes_);
+    for (size_t i = 0; i < blocks->size(); ++i) {
+        if (int wrc = write((*blocks)[i], buf.data() + i * block_bytes_, block_bytes_)) {
+            // back to the evicted state: the new blocks return to the free
+            // list and the saved bytes to the store
+            std::vector<uint32_t> undo;
+            (void)seq_mgr_.swap_out(seq, &undo);
+            cpu_store_[seq] = std::move(buf);
+            blocks->clear();
+            return wrc < 0 ? wrc : fail(AIR_KV_E_HIP, "restore: write of a block failed (%d)", wrc);
+        }
+    }
     cpu_bytes_used_ = cpu_bytes_used_ > buf.size() ? cpu_bytes_used_ - buf.size() : 0;
     return AIR_KV_OK;
 }
@@ -40,7 +51,11 @@ int KvSwapManager::maybe_evict(uint32_t seq, int64_t free_threshold, const ReadF
     *evicted = false;
     if (seq_mgr_.allocator().num_free_blocks() < free_threshold && !is_evicted(seq)) {
         std::vector<uint32_t> released;
-        *evicted = evict(seq, read, &released) == AIR_KV_OK;
+        const int rc = evict(seq, read, &released);
+        *evicted = rc == AIR_KV_OK;
+        // an unknown sequence is "not evicted", as in the reference; a
+        // failed device read is reported
+        if (rc != AIR_KV_OK && rc != AIR_KV_E_NOT_FOUND) return rc;
     }
     return AIR_KV_OK;
 }

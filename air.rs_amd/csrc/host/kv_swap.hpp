@@ -16,8 +16,13 @@ namespace airkv {
 
 class KvSwapManager {
 public:
-    using ReadFn = std::function<void(uint32_t block, uint8_t *dst, size_t bytes)>;
-    using WriteFn = std::function<void(uint32_t block, const uint8_t *src, size_t bytes)>;
+    // The copies return AIR_KV_OK or a negative status.  A failed read
+    // leaves the sequence resident and unchanged; a failed write puts the
+    // restored sequence back into the evicted state with its saved bytes.
+    // (The reference's closures return nothing, so a failed device copy
+    // there would be released or dropped unnoticed.)
+    using ReadFn = std::function<int(uint32_t block, uint8_t *dst, size_t bytes)>;
+    using WriteFn = std::function<int(uint32_t block, const uint8_t *src, size_t bytes)>;
 
     KvSwapManager(int64_t capacity, int32_t block_size, size_t block_bytes)
         : seq_mgr_(capacity, block_size, nullptr), block_bytes_(block_bytes) {}

@@ -127,10 +127,37 @@ int SequenceManager::cow_last_block(uint32_t seq, uint32_t *old_block, uint32_t 
         return fail(AIR_KV_E_NOT_FOUND, "sequence %u has no blocks", seq);
     uint32_t last = it->second.physical_blocks.back(), nid;
     if (!allocator_.cow_write(last, &nid)) return fail(AIR_KV_E_OOM, "out of memory — cow_write");
-    if (nid != last) it->second.physical_blocks.back() = nid;
+    if (nid != last) {
+        it->second.physical_blocks.back() = nid;
+        set_own_fill(it->second, it->second.physical_blocks.size() - 1);
+    }
     *old_block = last;
     *new_block = nid;
     return AIR_KV_OK;
+}
+
+// The private block that copy-on-write puts at table index `idx` holds this
+// sequence's tokens of that block, whatever the shared block's fill said: a
+// sequence truncated into a block it shares sees fewer tokens there than the
+// other owners (whose fill the shared block keeps), and so does one whose
+// co-owner appended into the shared block.  The reference copies the shared
+// block's metadata (src/paged_attention.rs:159-164); that agrees with this
+// whenever the sequence's own count equals the shared fill, which is every
+// case its own call sequences produce without truncation or a co-owner's
+// append into a shared block.
+void SequenceManager::set_own_fill(const BlockTable &t, size_t idx) {
+    const int64_t bs = block_size();
+    const int64_t own = t.num_tokens - (int64_t)idx * bs;
+    allocator_.set_fill(t.physical_blocks[idx], (int32_t)(own < 0 ? 0 : own > bs ? bs : own));
+}
+
+void SequenceManager::undo_cow(uint32_t seq, size_t idx, uint32_t old_block, uint32_t new_block) {
+    auto it = tables_.find(seq);
+    if (it == tables_.end() || idx >= it->second.physical_blocks.size()) return;
+    if (old_block == new_block || it->second.physical_blocks[idx] != new_block) return;
+    it->second.physical_blocks[idx] = old_block;
+    allocator_.share(old_block);
+    allocator_.release(new_block);
 }
 
 int SequenceManager::truncate(uint32_t seq, int64_t n_tokens) {
@@ -164,6 +191,7 @@ int SequenceManager::cow_block(uint32_t seq, int64_t index, uint32_t *old_block,
     uint32_t nid;
     if (!allocator_.cow_write(b, &nid)) return fail(AIR_KV_E_OOM, "out of memory — cow_write");
     blocks[(size_t)index] = nid;
+    if (nid != b) set_own_fill(it->second, (size_t)index);
     *old_block = b;
     *new_block = nid;
     return AIR_KV_OK;

@@ -9,9 +9,12 @@
 //  * release of a block whose refcount is already 0 is rejected (the
 //    reference pushes the id onto the free list a second time, :129-135);
 //  * append to a full block returns an error (the reference asserts, :172);
+//  * the private block copy-on-write makes for a sequence gets that
+//    sequence's own fill, not the shared block's (set_own_fill);
 //  * ids outside the pool are rejected (the reference indexes out of bounds).
 #pragma once
 
+#include <cstddef>
 #include <cstdint>
 #include <deque>
 #include <unordered_map>
@@ -97,8 +100,14 @@ public:
     //    reference's cow_last_block generalised to any index).
     int truncate(uint32_t seq, int64_t n_tokens);
     int cow_block(uint32_t seq, int64_t index, uint32_t *old_block, uint32_t *new_block);
+    //  * undo_cow: puts old_block back at table index idx in place of the
+    //    private copy new_block that cow_block made (the copy returns to the
+    //    free list), for a caller whose device copy could not be issued.
+    void undo_cow(uint32_t seq, size_t idx, uint32_t old_block, uint32_t new_block);
 
 private:
+    void set_own_fill(const BlockTable &t, size_t idx);
+
     BlockAllocator allocator_;
     std::unordered_map<uint32_t, BlockTable> tables_;
     uint32_t next_seq_id_ = 0;

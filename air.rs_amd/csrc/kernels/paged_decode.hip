@@ -357,7 +357,7 @@ int plan_decode(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int32_t 
         return plan_decode_mfma(p, n_q_heads, batch, max_blocks, max_splits, plan);
     plan->mfma = false;
     plan->dtype = p.desc.dtype;
-    plan->slices = plan->batch_per_launch = plan->slots = 0;
+    plan->slices = plan->slices_qf32 = plan->batch_per_launch = plan->slots = 0;
     const int64_t max_ctx = (int64_t)max_blocks * bs;
     int64_t parts = (max_ctx + kTargetPart - 1) / kTargetPart;
     parts = parts < 1 ? 1 : (parts > max_splits ? max_splits : parts);

@@ -769,14 +769,21 @@ int plan_decode_mfma(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int
     const int64_t tiles_per_seq = ((int64_t)max_blocks * bs + 15) / 16;
     if ((int64_t)nb * tiles_per_seq > INT32_MAX)
         return fail(AIR_KV_E_INVALID_ARG, "batch x max_blocks too large for one decode launch");
-    const int64_t machine_waves = (int64_t)p.cus * 4 * waves_per_simd(p.desc.dtype);
-    int64_t slices = (machine_waves + nkv - 1) / nkv;
     const int64_t cap = (int64_t)(nb > 0 ? nb : 1) * max_splits;
-    slices = slices > cap ? cap : slices;
+    auto slices_for = [&](int waves_per_simd) {
+        const int64_t machine_waves = (int64_t)p.cus * 4 * waves_per_simd;
+        const int64_t sl = (machine_waves + nkv - 1) / nkv;
+        return sl > cap ? cap : sl;
+    };
+    const int64_t slices = slices_for(waves_per_simd(p.desc.dtype));
     plan->mfma = true;
     plan->dtype = p.desc.dtype;
     plan->part_tokens = plan->num_parts = 0;
     plan->slices = (int32_t)slices;
+    // f32 queries on 1-byte pages run a kernel built for fewer waves per
+    // SIMD: their slices match what is resident at once, and the workspace
+    // (sized for plan->slices) holds them.
+    plan->slices_qf32 = (int32_t)slices_for(kernel_waves_per_simd(p.desc.dtype, true));
     plan->batch_per_launch = nb;
     plan->slots = (int32_t)(slices + nb);
     plan->ws_bytes = align256((size_t)(nb + 1) * 4) + align256((size_t)n_q_heads * plan->slots * 2 * 4) +
@@ -789,6 +796,9 @@ hipError_t launch_decode_mfma(const DecodeArgs &base, const DecodePlan &plan, vo
     for (int32_t b0 = 0; b0 < base.batch; b0 += plan.batch_per_launch) {
         DecodeArgs a = base;
         a.batch = base.batch - b0 < plan.batch_per_launch ? base.batch - b0 : plan.batch_per_launch;
+        // partial rows are laid out for plan.slots; fewer slices use a prefix of them
+        a.slices = base.q_dtype == AIR_KV_F32 ? plan.slices_qf32 : plan.slices;
+        a.slots = a.slices + plan.batch_per_launch;
         const int64_t q_row = (int64_t)b0 * a.n_q_heads * 128;
         a.q = (const char *)base.q + q_row * (base.q_dtype == AIR_KV_F32 ? 4 : 2);
         a.out = (char *)base.out + q_row * (base.out_dtype == AIR_KV_F32 ? 4 : 2);

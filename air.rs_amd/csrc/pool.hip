@@ -364,18 +364,24 @@ int air_kv_write_blocks(air_kv_pool *p, void *stream, const int32_t *ids, int32_
     return move_blocks(p, (hipStream_t)stream, ids, n, (uint8_t *)const_cast<void *>(host_src), false);
 }
 
-void air_kv_pool_read_cb(void *ctx, uint32_t block, uint8_t *dst, size_t bytes) {
+int air_kv_pool_read_cb(void *ctx, uint32_t block, uint8_t *dst, size_t bytes) {
     air_kv_pool *p = (air_kv_pool *)ctx;
-    if (!p || bytes != p->block_bytes) return;
+    if (!p) return fail(AIR_KV_E_INVALID_ARG, "read callback: pool is NULL");
+    if (bytes != p->block_bytes)
+        return fail(AIR_KV_E_INVALID_ARG, "read callback: %zu bytes asked, the pool's blocks hold %zu", bytes,
+                    p->block_bytes);
     int32_t id = (int32_t)block;
-    air_kv_read_blocks(p, nullptr, &id, 1, dst);
+    return air_kv_read_blocks(p, nullptr, &id, 1, dst);
 }
 
-void air_kv_pool_write_cb(void *ctx, uint32_t block, const uint8_t *src, size_t bytes) {
+int air_kv_pool_write_cb(void *ctx, uint32_t block, const uint8_t *src, size_t bytes) {
     air_kv_pool *p = (air_kv_pool *)ctx;
-    if (!p || bytes != p->block_bytes) return;
+    if (!p) return fail(AIR_KV_E_INVALID_ARG, "write callback: pool is NULL");
+    if (bytes != p->block_bytes)
+        return fail(AIR_KV_E_INVALID_ARG, "write callback: %zu bytes given, the pool's blocks hold %zu", bytes,
+                    p->block_bytes);
     int32_t id = (int32_t)block;
-    air_kv_write_blocks(p, nullptr, &id, 1, src);
+    return air_kv_write_blocks(p, nullptr, &id, 1, src);
 }
 
 int air_kv_pool_error_count(air_kv_pool *p, void *stream, int64_t *count, int32_t reset) {

@@ -53,8 +53,10 @@ int wait_stage(air_kv_session *s) {
     return AIR_KV_OK;
 }
 
-// Copies `bytes` of host data to the device staging buffer on `st`.
-int stage(air_kv_session *s, hipStream_t st, const void *src, size_t bytes, void **dev) {
+// Makes the staging buffers hold at least `bytes` (waiting for the last
+// launch that read them first).  After it succeeds, stage() of up to `bytes`
+// can fail only in the copy itself.
+int reserve_stage(air_kv_session *s, size_t bytes) {
     if (int rc = wait_stage(s)) return rc;
     if (bytes > s->stage_cap) {
         size_t cap = std::max<size_t>(bytes, 2 * s->stage_cap);
@@ -70,6 +72,12 @@ int stage(air_kv_session *s, hipStream_t st, const void *src, size_t bytes, void
         if (e != hipSuccess) return hip_fail(e, "session staging hipMalloc");
         s->stage_cap = cap;
     }
+    return AIR_KV_OK;
+}
+
+// Copies `bytes` of host data to the device staging buffer on `st`.
+int stage(air_kv_session *s, hipStream_t st, const void *src, size_t bytes, void **dev) {
+    if (int rc = reserve_stage(s, bytes)) return rc;
     std::memcpy(s->h_stage, src, bytes);
     hipError_t e = hipMemcpyAsync(s->d_stage, s->h_stage, bytes, hipMemcpyHostToDevice, st);
     if (e != hipSuccess) return hip_fail(e, "session staging copy");
@@ -194,34 +202,58 @@ int air_kv_session_append(air_kv_session *s, void *stream, int32_t layer, const 
     if (!t) return fail(AIR_KV_E_NOT_FOUND, "sequence not found (%u)", s->seq);
     const int64_t p0 = s->len[(size_t)layer], p1 = p0 + n_new;
     const int64_t had = t->num_tokens;
-
-    // Blocks that already exist and will be written are copied first if
-    // another sequence shares them; blocks past the table are allocated.
-    // Both draw on the free list, so capacity is checked before any change.
-    std::vector<int32_t> cow_src, cow_dst;
     const int64_t nb = (int64_t)t->physical_blocks.size();
+    if (nb < (had + bs - 1) / bs)
+        return fail(AIR_KV_E_STATE, "sequence %u holds %lld blocks for %lld tokens (swapped out?)", s->seq,
+                    (long long)nb, (long long)had);
+
+    // Everything that can fail without a HIP error is checked before the
+    // table changes: blocks that already exist and will be written are
+    // copied first if another sequence shares them, blocks past the table
+    // are allocated, and both draw on the free list; the staging buffers
+    // are sized for the slots and the copy lists.
     const int64_t last_written = std::min<int64_t>((p1 - 1) / bs, nb - 1);
-    int64_t need = std::max<int64_t>(0, (p1 + bs - 1) / bs - nb);
+    int64_t n_shared = 0;
     for (int64_t i = p0 / bs; i <= last_written; ++i)
-        if (m.allocator().ref_count(t->physical_blocks[(size_t)i]) > 1) ++need;
+        if (m.allocator().ref_count(t->physical_blocks[(size_t)i]) > 1) ++n_shared;
+    const int64_t need = n_shared + std::max<int64_t>(0, (p1 + bs - 1) / bs - nb);
     if (!m.allocator().can_allocate(need)) return fail(AIR_KV_E_OOM, "out of memory — no free blocks");
+    const size_t stage_bytes = (size_t)n_new * 8 + (size_t)n_shared * 8;
+    if (int rc = reserve_stage(s, stage_bytes)) return rc;
+
+    // Table changes: copy-on-write of shared blocks, then the new tokens
+    // (allocating on block boundaries).  Neither can fail after the checks
+    // above; `undo` puts the table back if a later step does.
+    std::vector<int32_t> cow_src, cow_dst;
+    std::vector<int64_t> cow_idx;
+    auto undo = [&]() {
+        m.truncate(s->seq, had);
+        for (size_t j = cow_idx.size(); j-- > 0;)
+            m.undo_cow(s->seq, (size_t)cow_idx[j], (uint32_t)cow_src[j], (uint32_t)cow_dst[j]);
+    };
     for (int64_t i = p0 / bs; i <= last_written; ++i) {
         const uint32_t b = m.table(s->seq)->physical_blocks[(size_t)i];
         if (m.allocator().ref_count(b) <= 1) continue;
         uint32_t o, nbk;
-        if (int rc = m.cow_block(s->seq, i, &o, &nbk)) return rc;
+        if (int rc = m.cow_block(s->seq, i, &o, &nbk)) {
+            undo();
+            return rc;
+        }
+        cow_idx.push_back(i);
         cow_src.push_back((int32_t)o);
         cow_dst.push_back((int32_t)nbk);
     }
-    // Tokens past the table's length: allocate (on block boundaries).
     for (int64_t p = had; p < p1; ++p) {
         uint32_t b;
-        if (int rc = m.append_token(s->seq, &b)) return rc;    // not reached: capacity checked
+        if (int rc = m.append_token(s->seq, &b)) {
+            undo();
+            return rc;
+        }
     }
     t = m.table(s->seq);
     // Stage slots (int64) then the copy lists (int32) in one transfer.
     const size_t n_cow = cow_src.size();
-    std::vector<char> host((size_t)n_new * 8 + n_cow * 8);
+    std::vector<char> host(stage_bytes);
     int64_t *slots = reinterpret_cast<int64_t *>(host.data());
     for (int64_t p = p0; p < p1; ++p)
         slots[p - p0] = (int64_t)t->physical_blocks[(size_t)(p / bs)] * bs + p % bs;
@@ -229,16 +261,25 @@ int air_kv_session_append(air_kv_session *s, void *stream, int32_t layer, const 
     std::copy(cow_src.begin(), cow_src.end(), lists);
     std::copy(cow_dst.begin(), cow_dst.end(), lists + n_cow);
     void *dev;
-    if (int rc = stage(s, st, host.data(), host.size(), &dev)) return rc;
+    if (int rc = stage(s, st, host.data(), host.size(), &dev)) {
+        undo();
+        return rc;
+    }
     const int64_t *d_slots = reinterpret_cast<const int64_t *>(dev);
     const int32_t *d_lists = reinterpret_cast<const int32_t *>((char *)dev + (size_t)n_new * 8);
+    int rc = AIR_KV_OK;
     if (n_cow) {
         for (air_kv_pool *p : s->pools)
-            if (int rc = air_kv_copy_blocks(p, stream, d_lists, d_lists + n_cow, (int32_t)n_cow)) return rc;
+            if ((rc = air_kv_copy_blocks(p, stream, d_lists, d_lists + n_cow, (int32_t)n_cow))) break;
     }
-    int rc = air_kv_append(s->pools[(size_t)layer], stream, k, v, d_slots, (int32_t)n_new);
-    if (int rc2 = mark_staged(s, st)) return rc ? rc : rc2;
-    if (rc) return rc;
+    if (!rc) rc = air_kv_append(s->pools[(size_t)layer], stream, k, v, d_slots, (int32_t)n_new);
+    const int rc2 = mark_staged(s, st);
+    if (rc || rc2) {
+        // The old blocks still hold their pages (copies only read them), so
+        // the table goes back to them and the new blocks to the free list.
+        undo();
+        return rc ? rc : rc2;
+    }
     s->len[(size_t)layer] = p1;
     return AIR_KV_OK;
 }

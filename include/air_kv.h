@@ -126,7 +126,10 @@ int air_seq_fork(air_seq_manager *m, uint32_t parent, uint32_t *child);
 int air_seq_free(air_seq_manager *m, uint32_t seq);
 /* cow_last_block (:327-335): AIR_KV_E_NOT_FOUND where the reference returns
  * None for a missing sequence or an empty table, AIR_KV_E_OOM for a failed
- * allocation.  *old_block / *new_block tell the caller which page to copy. */
+ * allocation.  *old_block / *new_block tell the caller which page to copy.
+ * A new private block gets this sequence's own fill of that block (the
+ * reference copies the shared block's fill, :159-164; the two differ only
+ * after a truncation into the shared block or a co-owner's append into it). */
 int air_seq_cow_last_block(air_seq_manager *m, uint32_t seq, uint32_t *old_block,
                            uint32_t *new_block);
 /* No counterpart in the reference (its dense cache rolls back with
@@ -136,7 +139,8 @@ int air_seq_cow_last_block(air_seq_manager *m, uint32_t seq, uint32_t *old_block
  * remains.  A no-op when n_tokens >= the sequence's length. */
 int air_seq_truncate(air_seq_manager *m, uint32_t seq, int64_t n_tokens);
 /* cow_last_block generalised to the block at table index `index` (no
- * counterpart in the reference): a private copy replaces a shared block. */
+ * counterpart in the reference): a private copy replaces a shared block and
+ * gets this sequence's own fill of it. */
 int air_seq_cow_block(air_seq_manager *m, uint32_t seq, int64_t index, uint32_t *old_block,
                       uint32_t *new_block);
 /* table (:322-324): copies up to `cap` block ids. */
@@ -157,9 +161,13 @@ int air_seq_swap_in(air_seq_manager *m, uint32_t seq, int32_t n_blocks, uint32_t
 
 /* Replaces KvSwapManager (src/kv_swap.rs:22-121).  The reference's
  * gpu_read / gpu_write closures (:55-57, :83-86) become callbacks; the pair
- * air_kv_pool_read_cb / air_kv_pool_write_cb binds them to a device pool. */
-typedef void (*air_kv_block_read_fn)(void *ctx, uint32_t block, uint8_t *dst, size_t bytes);
-typedef void (*air_kv_block_write_fn)(void *ctx, uint32_t block, const uint8_t *src, size_t bytes);
+ * air_kv_pool_read_cb / air_kv_pool_write_cb binds them to a device pool.
+ * Unlike the closures, a callback returns a status (AIR_KV_OK, or a negative
+ * AIR_KV_E_* code; a positive value is reported as AIR_KV_E_HIP): evict stops
+ * at a failed read before anything is released, and restore undoes its
+ * swap_in after a failed write, keeping the saved bytes for another try. */
+typedef int (*air_kv_block_read_fn)(void *ctx, uint32_t block, uint8_t *dst, size_t bytes);
+typedef int (*air_kv_block_write_fn)(void *ctx, uint32_t block, const uint8_t *src, size_t bytes);
 typedef struct air_kv_swap air_kv_swap;
 int air_kv_swap_create(int64_t capacity, int32_t block_size, size_t block_bytes, air_kv_swap **out);
 int air_kv_swap_destroy(air_kv_swap *s);
@@ -174,7 +182,9 @@ int air_kv_swap_restore(air_kv_swap *s, uint32_t seq, air_kv_block_write_fn writ
 int air_kv_swap_is_evicted(const air_kv_swap *s, uint32_t seq);
 int64_t air_kv_swap_evicted_count(const air_kv_swap *s);
 int64_t air_kv_swap_cpu_bytes_used(const air_kv_swap *s);
-/* maybe_evict (:112-121): *evicted = 1 when an eviction happened. */
+/* maybe_evict (:112-121): *evicted = 1 when an eviction happened.  An
+ * unknown sequence gives *evicted = 0 and AIR_KV_OK, as the reference's
+ * false; a failed read callback returns its status. */
 int air_kv_swap_maybe_evict(air_kv_swap *s, uint32_t seq, int64_t free_threshold,
                             air_kv_block_read_fn read, void *ctx, int32_t *evicted);
 
@@ -431,9 +441,11 @@ int air_kv_read_blocks(air_kv_pool *pool, void *stream, const int32_t *ids, int3
 int air_kv_write_blocks(air_kv_pool *pool, void *stream, const int32_t *ids, int32_t n,
                         const void *host_src);
 /* air_kv_block_read_fn / write_fn adapters over a pool (ctx = air_kv_pool*),
- * on the default stream. */
-void air_kv_pool_read_cb(void *ctx, uint32_t block, uint8_t *dst, size_t bytes);
-void air_kv_pool_write_cb(void *ctx, uint32_t block, const uint8_t *src, size_t bytes);
+ * on the default stream.  `bytes` must equal the pool's block_bytes (a swap
+ * manager created with another block size gets AIR_KV_E_INVALID_ARG, and its
+ * evict stops before releasing anything). */
+int air_kv_pool_read_cb(void *ctx, uint32_t block, uint8_t *dst, size_t bytes);
+int air_kv_pool_write_cb(void *ctx, uint32_t block, const uint8_t *src, size_t bytes);
 
 /* Number of out-of-range slots / table entries the kernels have skipped since
  * the pool was created or last reset.  Synchronises the stream. */

@@ -193,6 +193,56 @@ def test_fork_copy_on_write_isolation():
     assert mgr.allocator.num_free_blocks() == 32
 
 
+@pytest.mark.parametrize("dtype", [airkv.BF16, airkv.INT8])
+def test_fork_truncate_then_append(dtype):
+    """A fork rolled back into a block it shares with its parent, then
+    appended to: the shared block is copied with the fork's own fill, the
+    fork keeps its first tokens and gets the new ones after them, and the
+    parent is unchanged.  Repeated appends keep working."""
+    mgr, _, parent = _session(n_layers=2, dtype=dtype)
+    k, v = _rows(30, 30)
+    for layer in range(2):
+        parent.save(layer, k, v)
+    child = parent.fork()
+    child.truncate_to(5)
+    assert child.seq_len(0) == 5 and mgr.table(child.seq_id).physical_blocks == \
+        mgr.table(parent.seq_id).physical_blocks[:1]
+    kc, vc = _rows(20, 31)
+    for layer in range(2):
+        child.append(layer, kc[:3].contiguous(), vc[:3].contiguous())
+        child.append(layer, kc[3:].contiguous(), vc[3:].contiguous())
+    assert child.seq_len(0) == 25
+    t_child, t_parent = mgr.table(child.seq_id), mgr.table(parent.seq_id)
+    assert t_child.physical_blocks[0] != t_parent.physical_blocks[0]
+    assert len(t_child.physical_blocks) == 2
+    want_c = _expected(torch_mod().cat([k[:5], kc]), dtype)
+    want_cv = _expected(torch_mod().cat([v[:5], vc]), dtype)
+    want_p, want_pv = _expected(k, dtype), _expected(v, dtype)
+    for layer in range(2):
+        ck, cv = _load_np(child, layer)
+        pk, pv = _load_np(parent, layer)
+        assert np.array_equal(ck, want_c) and np.array_equal(cv, want_cv)
+        assert np.array_equal(pk, want_p) and np.array_equal(pv, want_pv)
+    child.close()
+    parent.close()
+    assert mgr.allocator.num_free_blocks() == 32
+
+
+def test_pool_callbacks_reject_a_foreign_block_size():
+    """A swap manager whose block_bytes differ from the pool's: the pool
+    callbacks refuse the copy, and evict stops before releasing anything."""
+    pool = airkv.KvPool(16, 16, NKV, D, airkv.BF16)
+    mgr = airkv.KvSwapManager(16, pool.block_bytes + 64, block_size=16)
+    sid = mgr.seq_mgr.create_sequence()
+    for _ in range(20):
+        mgr.seq_mgr.append_token(sid)
+    blocks = list(mgr.seq_mgr.table(sid).physical_blocks)
+    read, _write, ctx = airkv.pool_callbacks(pool)
+    with pytest.raises(airkv.AirKvError):
+        mgr.evict(sid, (read, ctx))
+    assert mgr.seq_mgr.table(sid).physical_blocks == blocks and not mgr.is_evicted(sid)
+
+
 def test_out_of_blocks_leaves_state_unchanged():
     """An append that needs more blocks than are free raises MemoryError and
     changes nothing (the reference's "out of memory — no free blocks")."""

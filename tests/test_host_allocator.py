@@ -247,6 +247,55 @@ def test_swap_bytes_round_trip_through_callbacks():
         assert data == bytes([(ob * 7 + i) & 0xFF for i in range(32)])
 
 
+def _failing(_block, _buf):
+    raise IOError("device copy failed")
+
+
+def test_evict_stops_on_a_failed_read():
+    """A read callback that fails leaves the sequence resident: nothing is
+    released and nothing is stored."""
+    mgr = airkv.KvSwapManager(8, 32)
+    sid = mgr.seq_mgr.create_sequence()
+    for _ in range(2 * BS):
+        mgr.seq_mgr.append_token(sid)
+    blocks = list(mgr.seq_mgr.table(sid).physical_blocks)
+    free = mgr.seq_mgr.allocator.num_free_blocks()
+    with pytest.raises(IOError):
+        mgr.evict(sid, _failing)
+    assert mgr.seq_mgr.table(sid).physical_blocks == blocks
+    assert mgr.seq_mgr.allocator.num_free_blocks() == free
+    assert not mgr.is_evicted(sid) and mgr.cpu_bytes_used == 0
+    with pytest.raises(IOError):
+        mgr.maybe_evict(sid, 100, _failing)
+    assert not mgr.is_evicted(sid)
+
+
+def test_restore_undoes_swap_in_on_a_failed_write():
+    """A write callback that fails puts the sequence back into the evicted
+    state with its bytes, so a second restore can succeed."""
+    mgr = airkv.KvSwapManager(8, 32)
+    sid = mgr.seq_mgr.create_sequence()
+    for _ in range(2 * BS):
+        mgr.seq_mgr.append_token(sid)
+
+    def read(b, buf):
+        buf[:] = bytes([(b + i) & 0xFF for i in range(len(buf))])
+
+    old = list(mgr.seq_mgr.table(sid).physical_blocks)
+    mgr.evict(sid, read)
+    free = mgr.seq_mgr.allocator.num_free_blocks()
+    used = mgr.cpu_bytes_used
+    with pytest.raises(IOError):
+        mgr.restore(sid, _failing)
+    assert mgr.is_evicted(sid) and mgr.cpu_bytes_used == used
+    assert mgr.seq_mgr.table(sid).physical_blocks == []
+    assert mgr.seq_mgr.allocator.num_free_blocks() == free
+    got = []
+    mgr.restore(sid, lambda b, data: got.append(data))
+    assert got == [bytes([(b + i) & 0xFF for i in range(32)]) for b in old]
+    assert not mgr.is_evicted(sid)
+
+
 # --- product-specific behaviour -----------------------------------------------
 
 def test_product_rejects_double_release():
@@ -469,6 +518,43 @@ def test_truncate_into_shared_block_keeps_its_fill():
     assert mgr.allocator.ref_count(first) == 2
     assert mgr.allocator.block_info(first) == (16, True)
     assert mgr.allocator.ref_count(mgr.table(s).physical_blocks[1]) == 1
+
+
+def test_fork_truncate_cow_then_append():
+    """A fork truncated into a block it shares: copy-on-write gives the
+    private block the fork's own fill (5 of 16), so the fork keeps appending
+    into it and the other owner's block is untouched."""
+    mgr = airkv.SequenceManager(8, block_size=16)
+    s = mgr.create_sequence()
+    mgr.append_slots(s, 30)
+    c = mgr.fork_sequence(s)
+    mgr.truncate(c, 5)
+    shared = mgr.table(s).physical_blocks[0]
+    old, new = mgr.cow_last_block(c)
+    assert old == shared and new != shared
+    assert mgr.allocator.block_info(new) == (5, False)
+    assert mgr.allocator.block_info(shared) == (16, True)
+    slots = mgr.append_slots(c, 11)          # fills the private block exactly
+    assert slots.tolist() == [new * 16 + p for p in range(5, 16)]
+    assert mgr.allocator.block_info(new) == (16, True)
+    nxt = mgr.append_token(c)                # then opens a fresh block
+    assert nxt not in (new, shared) and len(mgr.table(c).physical_blocks) == 2
+    assert mgr.allocator.ref_count(shared) == 1 and mgr.table(s).num_tokens == 30
+
+
+def test_fork_truncate_cow_block_then_append():
+    """The same through cow_block at an inner index: the private block holds
+    the fork's tokens of it (a full block stays full)."""
+    mgr = airkv.SequenceManager(8, block_size=16)
+    s = mgr.create_sequence()
+    mgr.append_slots(s, 40)
+    c = mgr.fork_sequence(s)
+    mgr.truncate(c, 20)                      # blocks 0 (full) and 1 (4 of 16), both shared
+    _, n0 = mgr.cow_block(c, 0)
+    _, n1 = mgr.cow_block(c, 1)
+    assert mgr.allocator.block_info(n0) == (16, True)
+    assert mgr.allocator.block_info(n1) == (4, False)
+    assert mgr.append_slots(c, 12).tolist() == [n1 * 16 + p for p in range(4, 16)]
 
 
 def test_cow_block_any_index():
