@@ -263,6 +263,25 @@ int air_paged_decode(air_kv_pool *pool, void *stream, const void *q, int32_t q_d
                      int32_t batch, int32_t max_blocks, float scale, int32_t max_splits,
                      void *workspace, size_t ws_bytes, void *out, int32_t out_dtype);
 
+/* Bytes of the file-scope device array air_paged_decode_noalloc uses as its
+ * workspace (one copy per GPU, held until the process ends). */
+#define AIR_KV_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): air_paged_decode with its workspace taken from a
+ * library-owned device array of AIR_KV_NOALLOC_SCRATCH_BYTES instead of a
+ * caller buffer.  Same arguments, kernels and results as air_paged_decode;
+ * it calls no hipMalloc / hipFree.  A launch whose
+ * air_paged_decode_workspace_size exceeds the array returns
+ * AIR_KV_E_INVALID_ARG (32 MiB holds configs c2-c5: c4 needs 17.3 MB).
+ * Every call on one GPU shares that GPU's array: calls that overlap in time
+ * on one GPU (other streams or threads) race and must be serialised. */
+int air_paged_decode_noalloc(air_kv_pool *pool, void *stream, const void *q, int32_t q_dtype,
+                             int32_t n_q_heads, const int32_t *block_tables, const int32_t *seq_lens,
+                             int32_t batch, int32_t max_blocks, float scale, int32_t max_splits,
+                             void *out, int32_t out_dtype);
+
 /* Paged prefill attention (chunked, causal): sequence b's q_len = cu_q[b + 1]
  * - cu_q[b] newest tokens, whose K/V are already appended, attend over its
  * seq_lens[b] cached tokens; query row r (0-based within the sequence) sits at
