@@ -12,6 +12,11 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG_DIR = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "libairkv.so")
+# AIRKV_HOST_LIB selects the host-only build of the C ABI (the allocator,
+# sequence manager and swap manager compiled under AddressSanitizer + UBSan,
+# `make -C air.rs_amd asan`) for the sanitizer test: it holds no device entry
+# points, and calling one raises.
+HOST_LIB_PATH = os.environ.get("AIRKV_HOST_LIB")
 
 AIR_KV_OK = 0
 AIR_KV_E_INVALID_ARG = -1
@@ -144,11 +149,16 @@ def load(path: str = LIB_PATH):
     global _lib
     if _lib is not None:
         return _lib
+    host_only = HOST_LIB_PATH is not None
+    if host_only:
+        path = HOST_LIB_PATH
     if not os.path.exists(path):
         raise ImportError(f"libairkv.so not built at {path}: run __graft_entry__.build() "
                           f"(make -C air.rs_amd)")
     L = ctypes.CDLL(path)
     for name, (res, args) in SIGNATURES.items():
+        if host_only and not hasattr(L, name):
+            continue
         fn = getattr(L, name)
         fn.restype = res
         fn.argtypes = args

@@ -65,6 +65,8 @@ class KvPool:
         self.n_kv_heads, self.head_dim = info.n_kv_heads, info.head_dim
         self.dtype, self.scale_group = info.dtype, info.scale_group
         self.block_bytes = bb.value
+        # device base pointers of the pool's arrays (k_pages, v_pages, k_scales, v_scales)
+        self.device_ptrs = tuple(p.value or 0 for p in ptrs)
         self.quantized = dtype in (INT8, FP8)
         rows = self.n_kv_heads * self.block_size
         self.slab_bytes = rows * self.head_dim * ELEM_BYTES[dtype]

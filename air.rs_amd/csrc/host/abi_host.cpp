@@ -316,7 +316,7 @@ int air_seq_swap_out(air_seq_manager *m, uint32_t seq, uint32_t *blocks, int32_t
     int rc = m->impl->swap_out(seq, &out);
     if (rc) return rc;
     if (n_blocks) *n_blocks = (int32_t)out.size();
-    if (blocks) std::memcpy(blocks, out.data(), out.size() * sizeof(uint32_t));
+    if (blocks && !out.empty()) std::memcpy(blocks, out.data(), out.size() * sizeof(uint32_t));
     return AIR_KV_OK;
 }
 
@@ -325,7 +325,7 @@ int air_seq_swap_in(air_seq_manager *m, uint32_t seq, int32_t n_blocks, uint32_t
     std::vector<uint32_t> out;
     int rc = m->impl->swap_in(seq, n_blocks, &out);
     if (rc) return rc;
-    if (blocks) std::memcpy(blocks, out.data(), out.size() * sizeof(uint32_t));
+    if (blocks && !out.empty()) std::memcpy(blocks, out.data(), out.size() * sizeof(uint32_t));
     return AIR_KV_OK;
 }
 
@@ -361,22 +361,23 @@ int air_kv_swap_evict(air_kv_swap *s, uint32_t seq, air_kv_block_read_fn read, v
     int rc = s->impl.evict(seq, [&](uint32_t b, uint8_t *dst, size_t n) { return read(ctx, b, dst, n); }, &out);
     if (rc) return rc;
     if (n_released) *n_released = (int32_t)out.size();
-    if (released) std::memcpy(released, out.data(), out.size() * sizeof(uint32_t));
+    if (released && !out.empty()) std::memcpy(released, out.data(), out.size() * sizeof(uint32_t));
     return AIR_KV_OK;
 }
 
 int air_kv_swap_restore(air_kv_swap *s, uint32_t seq, air_kv_block_write_fn write, void *ctx,
                         uint32_t *blocks, int32_t cap, int32_t *n_blocks) {
     if (!s || !write) return fail(AIR_KV_E_INVALID_ARG, "swap manager or write callback is NULL");
+    // the id buffer is checked before anything changes
+    const int64_t need = s->impl.evicted_blocks(seq);
+    if (blocks && need > cap)
+        return fail(AIR_KV_E_INVALID_ARG, "restore: cap %d below %lld blocks", cap, (long long)need);
     std::vector<uint32_t> out;
     int rc = s->impl.restore(
         seq, [&](uint32_t b, const uint8_t *src, size_t n) { return write(ctx, b, src, n); }, &out);
     if (rc) return rc;
     if (n_blocks) *n_blocks = (int32_t)out.size();
-    if (blocks) {
-        if ((int64_t)out.size() > cap) return fail(AIR_KV_E_INVALID_ARG, "restore: cap too small");
-        std::memcpy(blocks, out.data(), out.size() * sizeof(uint32_t));
-    }
+    if (blocks && !out.empty()) std::memcpy(blocks, out.data(), out.size() * sizeof(uint32_t));
     return AIR_KV_OK;
 }
 

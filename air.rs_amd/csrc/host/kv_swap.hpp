@@ -31,6 +31,11 @@ public:
     int evict(uint32_t seq, const ReadFn &read, std::vector<uint32_t> *released);   // :55-74
     int restore(uint32_t seq, const WriteFn &write, std::vector<uint32_t> *blocks); // :83-98
     bool is_evicted(uint32_t seq) const { return cpu_store_.count(seq) != 0; }
+    // blocks a restore of `seq` will allocate (0 when nothing is stored)
+    int64_t evicted_blocks(uint32_t seq) const {
+        auto it = cpu_store_.find(seq);
+        return it == cpu_store_.end() || !block_bytes_ ? 0 : (int64_t)(it->second.size() / block_bytes_);
+    }
     int64_t evicted_count() const { return (int64_t)cpu_store_.size(); }
     int64_t cpu_bytes_used() const { return (int64_t)cpu_bytes_used_; }
     int maybe_evict(uint32_t seq, int64_t free_threshold, const ReadFn &read, bool *evicted);

@@ -16,7 +16,9 @@ import threading
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libairkv_oracle.so")
+# AIRKV_ORACLE_LIB selects another build of the same sources (the
+# AddressSanitizer + UBSan build, `make -C oracle asan`, for the sanitizer test)
+LIB_PATH = os.environ.get("AIRKV_ORACLE_LIB") or os.path.join(HERE, "libairkv_oracle.so")
 
 F32, BF16, INT8, FP8 = 0, 1, 2, 3
 ELEM_BYTES = {F32: 4, BF16: 2, INT8: 1, FP8: 1}
