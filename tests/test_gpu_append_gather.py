@@ -103,6 +103,40 @@ def test_c1_append_gather_bitexact(dtype):
             assert_bits_equal(gk[offs[b]:offs[b] + n], oracle.q8_dequantize(q, s), "Q8Tensor pin")
 
 
+@pytest.mark.parametrize("name", ["f32", "bf16", "int8", "fp8"])
+def test_c1_against_committed_digests(name):
+    """The GPU's c1 pages, scales and gathered views hash to the digests the
+    oracle committed in tests/golden/c1_digests.json (inputs from the
+    reference LCG / Box-Muller streams), so an oracle and a kernel that
+    drifted together across commits would still be caught."""
+    import json
+    import os
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+    import c1_digests as c1
+    with open(c1.JSON_PATH) as f:
+        doc = json.load(f)["digests"]
+    log(f"c1 digests dtype={name}")
+    w, batches, tables, lens, k, v = c1.workload()
+    assert c1.sha(k) == doc["inputs"]["k_rows"] and c1.sha(v) == doc["inputs"]["v_rows"], \
+        "input generator differs on this host"
+    assert c1.sha(np.concatenate(batches)) == doc["inputs"]["slots"]
+    assert c1.sha(tables) == doc["inputs"]["tables"] and c1.sha(lens) == doc["inputs"]["lens"]
+    w.cfg = workloads.Config(w.cfg.name, 8, 8, 64, 16, c1.DTYPES[name], 4)
+    pool = device_pool_for(w)
+    run_appends(w, k, v, pool)
+    want = doc[name]
+    pk, pv, pks, pvs = pool.snapshot()
+    assert c1.sha(pk) == want["k_pages"] and c1.sha(pv) == want["v_pages"]
+    if "k_scales" in want:
+        assert c1.sha(pks) == want["k_scales"] and c1.sha(pvs) == want["v_scales"]
+    for od in c1.out_dtypes(name):
+        for layout in (airkv.LAYOUT_HEAD_MAJOR, airkv.LAYOUT_TOKEN_MAJOR):
+            gk, gv, _ = _gather(pool, tables, lens, c1.DTYPES[od], layout)
+            assert [c1.sha(gk), c1.sha(gv)] == want[f"gather_{od}_layout{layout}"], (od, layout)
+    assert pool.error_count() == 0
+
+
 def test_untouched_slots_keep_their_contents():
     """Every appended slot is written exactly once; all other bytes of the
     pool are left alone (pages pre-filled with a sentinel via write_blocks)."""
