@@ -1,0 +1,165 @@
+// HBM ceiling kernels for the benchmark (not part of libairkv.so): what this
+// GPU sustains for the access patterns of the paged-KV kernels, measured in
+// the same run as them, so their rates can be read against an achievable
+// bound as well as the 8 TB/s spec.
+//
+//   read      contiguous 16-byte loads, 64 bytes per thread (the decode's
+//             byte stream without its page scatter)
+//   page_read 4 KB pages in a shuffled order, one wave per page, K and V
+//             pools: the decode's access pattern
+//   write     contiguous 16-byte stores
+//   copy      read + write of equal sizes: the gather's and block copies'
+//             pattern (1 byte written per byte read)
+//   mix21     two bytes read per byte written: the append's pattern (f32
+//             rows in, bf16 page rows out)
+//
+// Each pattern has a plain and a non-temporal (`nt`: streaming) variant of
+// its loads and of its stores; the bench reports the faster.  Every thread
+// moves exactly 64 bytes of reads (and its share of writes) per launch, so a
+// 1 GiB buffer is 65536 workgroups of 256 threads.  Loads feed a value that
+// is stored only on an impossible condition, so nothing is optimised away.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kThreads = 256;
+
+template <bool NT>
+__device__ __forceinline__ u32x4 ld16(const u32x4 *p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    return *p;
+}
+
+template <bool NT>
+__device__ __forceinline__ void st16(u32x4 *p, u32x4 v) {
+    if constexpr (NT) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
+
+__device__ __forceinline__ uint32_t fold(u32x4 a, u32x4 b, u32x4 c, u32x4 d) {
+    const u32x4 x = (a ^ b) + (c ^ d);
+    return x[0] ^ x[1] ^ x[2] ^ x[3];
+}
+
+// Thread t reads 64 B as four 16-byte loads spread a wave apart (each load
+// instruction of a wave covers 1 KB of consecutive lines).
+template <bool NT>
+__global__ __launch_bounds__(kThreads) void read_kernel(const u32x4 *src, int64_t n16, uint32_t *sink) {
+    const int64_t base = (int64_t)blockIdx.x * kThreads * 4 + threadIdx.x;
+    if (base + 3 * kThreads >= n16) return;
+    const u32x4 a = ld16<NT>(src + base), b = ld16<NT>(src + base + kThreads);
+    const u32x4 c = ld16<NT>(src + base + 2 * kThreads), d = ld16<NT>(src + base + 3 * kThreads);
+    const uint32_t x = fold(a, b, c, d);
+    if (x == 0x9E3779B9u && threadIdx.x == 7) sink[0] = x;
+}
+
+template <bool NT>
+__global__ __launch_bounds__(kThreads) void write_kernel(u32x4 *dst, int64_t n16, uint32_t seed) {
+    const int64_t base = (int64_t)blockIdx.x * kThreads * 4 + threadIdx.x;
+    if (base + 3 * kThreads >= n16) return;
+    const u32x4 v = {seed, seed ^ 1u, seed ^ 2u, (uint32_t)base};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st16<NT>(dst + base + i * kThreads, v);
+}
+
+// Every load of a thread is issued before its stores.
+template <bool NTL, bool NTS>
+__global__ __launch_bounds__(kThreads) void copy_kernel(const u32x4 *src, u32x4 *dst, int64_t n16) {
+    const int64_t base = (int64_t)blockIdx.x * kThreads * 4 + threadIdx.x;
+    if (base + 3 * kThreads >= n16) return;
+    u32x4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = ld16<NTL>(src + base + i * kThreads);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st16<NTS>(dst + base + i * kThreads, v[i]);
+}
+
+// 64 B read, 32 B written per thread (contiguous both sides).
+template <bool NTL, bool NTS>
+__global__ __launch_bounds__(kThreads) void mix21_kernel(const u32x4 *src, u32x4 *dst, int64_t n16) {
+    const int64_t base = (int64_t)blockIdx.x * kThreads * 4 + threadIdx.x;
+    if (base + 3 * kThreads >= n16) return;
+    u32x4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = ld16<NTL>(src + base + i * kThreads);
+    const int64_t obase = (int64_t)blockIdx.x * kThreads * 2 + threadIdx.x;
+    st16<NTS>(dst + obase, v[0] ^ v[1]);
+    st16<NTS>(dst + obase + kThreads, v[2] ^ v[3]);
+}
+
+// One wave per (page, pool): a 4 KB page of K then the same page of V, 64 B
+// per lane as four 16-byte loads 1 KB apart.  pages[] is a shuffled list of
+// page indices into pools of n_pages pages each.
+template <bool NT>
+__global__ __launch_bounds__(kThreads) void page_read_kernel(const u32x4 *k, const u32x4 *v, const int32_t *pages,
+                                                             int64_t n_list, int64_t pool_pages, uint32_t *sink) {
+    const int64_t item = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    if (item >= 2 * n_list) return;
+    const int lane = threadIdx.x & 63;
+    const int64_t pg = pages[item >> 1];
+    if (pg < 0 || pg >= pool_pages) return;
+    const u32x4 *base = ((item & 1) ? v : k) + pg * 256 + lane;
+    const u32x4 a = ld16<NT>(base), b = ld16<NT>(base + 64), c = ld16<NT>(base + 128), d = ld16<NT>(base + 192);
+    const uint32_t x = fold(a, b, c, d);
+    if (x == 0x9E3779B9u && lane == 7) sink[0] = x;
+}
+
+dim3 grid_for(int64_t n16) { return dim3((unsigned)(n16 / (kThreads * 4))); }
+
+}  // namespace
+
+extern "C" {
+
+// kind: 0 read, 1 write, 2 copy, 3 mix21 (bytes = bytes read), 4 page_read
+// (src = K pool, dst = V pool, bytes = one pool's bytes, pages / n_pages =
+// the page list).  nt_load / nt_store pick the non-temporal variants.
+// Returns 0 or the hipError_t of the launch.
+int air_ceiling_launch(int kind, int nt_load, int nt_store, const void *src, void *dst, int64_t bytes,
+                       const int32_t *pages, int64_t n_pages, void *sink, void *stream) {
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t n16 = bytes / 16;
+    const u32x4 *in = (const u32x4 *)src;
+    u32x4 *out = (u32x4 *)dst;
+    uint32_t *sk = (uint32_t *)sink;
+    if (n16 < kThreads * 4) return (int)hipErrorInvalidValue;
+    const dim3 g = grid_for(n16), b(kThreads);
+    switch (kind) {
+    case 0:
+        if (nt_load) hipLaunchKernelGGL(read_kernel<true>, g, b, 0, s, in, n16, sk);
+        else hipLaunchKernelGGL(read_kernel<false>, g, b, 0, s, in, n16, sk);
+        break;
+    case 1:
+        if (nt_store) hipLaunchKernelGGL(write_kernel<true>, g, b, 0, s, out, n16, 0x5bd1e995u);
+        else hipLaunchKernelGGL(write_kernel<false>, g, b, 0, s, out, n16, 0x5bd1e995u);
+        break;
+    case 2:
+        if (nt_load && nt_store) hipLaunchKernelGGL((copy_kernel<true, true>), g, b, 0, s, in, out, n16);
+        else if (nt_load) hipLaunchKernelGGL((copy_kernel<true, false>), g, b, 0, s, in, out, n16);
+        else if (nt_store) hipLaunchKernelGGL((copy_kernel<false, true>), g, b, 0, s, in, out, n16);
+        else hipLaunchKernelGGL((copy_kernel<false, false>), g, b, 0, s, in, out, n16);
+        break;
+    case 3:
+        if (nt_load && nt_store) hipLaunchKernelGGL((mix21_kernel<true, true>), g, b, 0, s, in, out, n16);
+        else if (nt_load) hipLaunchKernelGGL((mix21_kernel<true, false>), g, b, 0, s, in, out, n16);
+        else if (nt_store) hipLaunchKernelGGL((mix21_kernel<false, true>), g, b, 0, s, in, out, n16);
+        else hipLaunchKernelGGL((mix21_kernel<false, false>), g, b, 0, s, in, out, n16);
+        break;
+    case 4: {
+        if (!pages || n_pages <= 0 || n_pages * 4096 > bytes) return (int)hipErrorInvalidValue;
+        const dim3 gp((unsigned)((2 * n_pages + kThreads / 64 - 1) / (kThreads / 64)));
+        const int64_t pool_pages = bytes / 4096;
+        if (nt_load)
+            hipLaunchKernelGGL(page_read_kernel<true>, gp, b, 0, s, in, (const u32x4 *)dst, pages, n_pages, pool_pages, sk);
+        else
+            hipLaunchKernelGGL(page_read_kernel<false>, gp, b, 0, s, in, (const u32x4 *)dst, pages, n_pages, pool_pages, sk);
+        break;
+    }
+    default:
+        return (int)hipErrorInvalidValue;
+    }
+    return (int)hipGetLastError();
+}
+
+}  // extern "C"

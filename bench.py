@@ -82,13 +82,127 @@ def timed_loop(torch, fn, iters, lead_sleep=True):
     return e0.elapsed_time(e1) / iters   # ms
 
 
+def twin_pool(torch, pool):
+    """A second pool of the same geometry holding the same bytes (device to
+    device copy of pages and scales), so timed calls can alternate between
+    two copies: no call then re-reads pages the previous call left in the
+    256 MB MALL."""
+    import ctypes
+
+    import airkv
+    twin = airkv.KvPool(pool.num_blocks, pool.block_size, pool.n_kv_heads, pool.head_dim, pool.dtype,
+                        pool.scale_group)
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+    slab = pool.num_blocks * pool.slab_bytes
+    sc = pool.num_blocks * pool.scale_slab_bytes
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for i, n in enumerate((slab, slab, sc, sc)):
+        if n:
+            rc = hip.hipMemcpyAsync(ctypes.c_void_p(twin.device_ptrs[i]), ctypes.c_void_p(pool.device_ptrs[i]),
+                                    n, 3, stream)     # hipMemcpyDeviceToDevice
+            assert rc == 0, f"hipMemcpyAsync failed ({rc})"
+    torch.cuda.synchronize()
+    return twin
+
+
+def alternating(fns):
+    """One call per invocation, cycling through fns (one per pool copy)."""
+    state = [0]
+
+    def call():
+        fns[state[0]]()
+        state[0] = (state[0] + 1) % len(fns)
+    return call
+
+
+def ceilings_leg(torch, iters=20):
+    """HBM ceilings of this GPU, measured in this run with the bench-only
+    kernels of air.rs_amd/csrc/bench/ceilings.hip on 1 GiB buffers (2 GiB for
+    the page pools): contiguous read, contiguous write, copy (1 byte written
+    per byte read), mix21 (2 bytes read per byte written), and page_read
+    (4 KB K and V pages in a shuffled order, one wave per page).  Each
+    pattern runs with plain and non-temporal loads / stores; the faster is
+    kept, with its variant."""
+    import ctypes
+
+    import numpy as np
+    lib = ctypes.CDLL(os.path.join(ROOT, "air.rs_amd", "airkv", "libairkv_ceilings.so"))
+    lib.air_ceiling_launch.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                       ctypes.c_void_p]
+    nbytes = 1 << 30
+    a = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    b = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    a.view(torch.int32).random_()
+    b.view(torch.int32).random_()
+    sink = torch.zeros(64, dtype=torch.int32, device="cuda")
+    pages = torch.from_numpy(np.random.default_rng(13).permutation(nbytes // 4096).astype(np.int32)).cuda()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    kinds = {  # name: (kind, bytes moved per launch, (load nt options), (store nt options), n_pages)
+        "read": (0, nbytes, (0, 1), (0,), 0),
+        "write": (1, nbytes, (0,), (0, 1), 0),
+        "copy": (2, 2 * nbytes, (0, 1), (0, 1), 0),
+        "mix21": (3, nbytes + nbytes // 2, (0, 1), (0, 1), 0),
+        "page_read": (4, 2 * nbytes, (0, 1), (0,), nbytes // 4096),
+    }
+    out = {}
+    for name, (kind, moved, lds, sts, npg) in kinds.items():
+        best = None
+        for ntl in lds:
+            for nts in sts:
+                def fn(kind=kind, ntl=ntl, nts=nts, npg=npg):
+                    rc = lib.air_ceiling_launch(kind, ntl, nts, P(a), P(b), nbytes, P(pages) if npg else None,
+                                                npg, P(sink), stream)
+                    assert rc == 0, f"ceiling launch {kind} failed ({rc})"
+                fn()
+                ms = timed_loop(torch, fn, iters)
+                gbps = moved / (ms * 1e-3) / 1e9
+                parts = []
+                if len(lds) > 1:
+                    parts.append(("nt" if ntl else "plain") + " loads")
+                if len(sts) > 1:
+                    parts.append(("nt" if nts else "plain") + " stores")
+                variant = ", ".join(parts)
+                if best is None or gbps > best["gbps"]:
+                    best = {"gbps": round(gbps, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4), "variant": variant}
+        out[name] = best
+    del a, b
+    return out
+
+
+def cpu_info():
+    """(threads to use, description): the process's CPU share on this host.
+    os.cpu_count() counts every CPU of the machine; the affinity mask and
+    OMP_NUM_THREADS say what this process may use (16 on the GPU boxes)."""
+    ncpu = os.cpu_count() or 1
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = ncpu
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = max(1, min(aff, omp) if omp > 0 else aff)
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return threads, {"cpu_model": model, "host_cpus": ncpu, "affinity_cpus": aff,
+                     "omp_num_threads": omp or None}
+
+
 def cpu_baseline(pool, w, tables, lens, q_f32, budget_s, decode_bytes_of):
     """The oracle's paged decode (gather + flash_decode with chunk 64 per query
     head, src/flash_decode.rs:153-173) on whole sequences of the same workload,
     on this host's cores: first on one thread (every sequence, or about
-    budget_s of work), then on up to 16 threads over every sequence (ctypes
-    releases the GIL, so the C oracle calls run in parallel).  GB/s counts the
-    same algorithmic bytes as the GPU figure."""
+    budget_s of work), then on every CPU this process may use (its affinity
+    mask, capped by OMP_NUM_THREADS: the GPU box's share of the host) over
+    every sequence (ctypes releases the GIL, so the C oracle calls run in
+    parallel).  GB/s counts the same algorithmic bytes as the GPU figure."""
     import concurrent.futures
 
     import numpy as np
@@ -112,7 +226,7 @@ def cpu_baseline(pool, w, tables, lens, q_f32, budget_s, decode_bytes_of):
             break
     t1 = time.perf_counter() - t0
     v1 = decode_bytes_of(lens[:done], done) / t1 / 1e9
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads, hostinfo = cpu_info()
     with concurrent.futures.ThreadPoolExecutor(threads) as ex:
         t0 = time.perf_counter()
         list(ex.map(one, range(batch)))
@@ -123,7 +237,7 @@ def cpu_baseline(pool, w, tables, lens, q_f32, budget_s, decode_bytes_of):
                       f"32 q heads each), oracle gather + flash_decode chunk 64 per query head, "
                       f"{threads} threads over sequences: {tn:.2f} s; one thread: {done} sequences "
                       f"in {t1:.2f} s",
-            "value_1core": v1, "seq_per_s": batch / tn}
+            "value_1core": v1, "seq_per_s": batch / tn, **hostinfo}
 
 
 def config_decode(torch, name, iters=20):
@@ -155,7 +269,8 @@ def config_decode(torch, name, iters=20):
     q = torch.randn(cfg.batch, cfg.n_q_heads, cfg.head_dim, device="cuda").to(torch.bfloat16)
     out = torch.empty_like(q)
     ws = pool.new_workspace(cfg.n_q_heads, cfg.batch, tables.shape[1], cfg.max_splits)
-    fn = pool.bind_decode(q, tt, lt, out, ws, max_splits=cfg.max_splits)
+    twin = twin_pool(torch, pool)
+    fn = alternating([p.bind_decode(q, tt, lt, out, ws, max_splits=cfg.max_splits) for p in (pool, twin)])
     fn()
     ms = timed_loop(torch, fn, iters)
     eb = {airkv.BF16: 2, airkv.INT8: 1, airkv.FP8: 1}[cfg.dtype]
@@ -165,7 +280,8 @@ def config_decode(torch, name, iters=20):
     tok = int(lens.astype(np.int64).sum())
     pages = int(((lens + cfg.block_size - 1) // cfg.block_size).sum())
     nbytes = tok * per_tok + 4 * pages + cfg.batch * cfg.n_q_heads * cfg.head_dim * 4
-    assert pool.error_count() == 0
+    assert pool.error_count() == 0 and twin.error_count() == 0
+    twin.close()
     res = {"decode_gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "decode_us": round(ms * 1e3, 1),
            "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4), "cached_tokens": tok,
            "batch": cfg.batch, "kv_dtype": {airkv.BF16: "bf16", airkv.INT8: "int8", airkv.FP8: "fp8"}[cfg.dtype],
@@ -397,7 +513,11 @@ def main():
     log(f"step {ms_step * 1e3:.1f} us, {value:.0f} GB/s")
 
     # ---- decode kernel alone, final state ---------------------------------
-    last = decodes[-1]
+    # calls alternate between the pool and a copy of it (same bytes, same
+    # tables), so no call finds pages the previous one left in the MALL
+    twin = twin_pool(torch, pool)
+    last = alternating([p.bind_decode(step_q[-1], tables, step_lens[-1], out, ws, max_splits=args.max_splits)
+                        for p in (pool, twin)])
     ms_dec = timed_loop(torch, last, args.kernel_iters)
     dec_bytes = decode_bytes(np.array(lens0) + n_steps)
     dec_gbps = dec_bytes / (ms_dec * 1e-3) / 1e9
@@ -411,7 +531,7 @@ def main():
         offs = torch.from_numpy(np.concatenate([[0], np.cumsum(per)[:-1]]).astype(np.int64)).to(dev)
         gk = torch.empty(int(per.sum()), dtype=torch.bfloat16, device=dev)
         gv = torch.empty_like(gk)
-        gather = pool.bind_gather(tables, step_lens[-1], offs, gk, gv)
+        gather = alternating([p.bind_gather(tables, step_lens[-1], offs, gk, gv) for p in (pool, twin)])
         ms_g = timed_loop(torch, gather, 20)
         g_bytes = int(per.sum()) * 2 * 2 * 2 + 4 * int(np.sum((lens_f + bs - 1) // bs))
         extra["gather_gbps"] = round(g_bytes / (ms_g * 1e-3) / 1e9, 1)
@@ -453,10 +573,23 @@ def main():
     del src, dst
     log(f"torch copy {extra['copy_gbps']} GB/s")
 
+    if not args.only_decode:
+        extra["ceilings"] = ceilings_leg(torch)
+        log(f"ceilings {extra['ceilings']}")
+        c = extra["ceilings"]
+        extra["frac_of_ceiling"] = {
+            "decode_vs_page_read": round(dec_gbps / c["page_read"]["gbps"], 4),
+            "gather_vs_copy": round(extra["gather_gbps"] / c["copy"]["gbps"], 4),
+            "append_vs_mix21": round(extra["append_gbps"] / c["mix21"]["gbps"], 4),
+        }
+
     if not args.no_configs and not args.only_decode:
         extra["other_configs"] = {}
         for name in ("c3", "c4", "c5"):
             extra["other_configs"][name] = config_decode(torch, name)
+            if "ceilings" in extra:
+                extra["other_configs"][name]["frac_of_page_read_ceiling"] = round(
+                    extra["other_configs"][name]["decode_gbps"] / extra["ceilings"]["page_read"]["gbps"], 4)
             log(f"{name} decode {extra['other_configs'][name]}")
         extra["prefill_c5"] = prefill_leg(torch)
         log(f"prefill {extra['prefill_c5']['tflops']} TFLOP/s")
@@ -510,6 +643,7 @@ def main():
     }
     result.update(extra)
     print(json.dumps(result), flush=True)
+    twin.close()
     pool.close()
 
 
