@@ -12,6 +12,10 @@
 //             pattern (1 byte written per byte read)
 //   mix21     two bytes read per byte written: the append's pattern (f32
 //             rows in, bf16 page rows out)
+//   page_copy 4 KB pages read in a shuffled order, written to consecutive
+//             4 KB slots: the gather's pattern
+//   page_mix21 8 KB of contiguous rows read per 4 KB page written in a
+//             shuffled order: the append's pattern
 //
 // Each pattern has a plain and a non-temporal (`nt`: streaming) variant of
 // its loads and of its stores; the bench reports the faster.  Every thread
@@ -106,6 +110,47 @@ __global__ __launch_bounds__(kThreads) void page_read_kernel(const u32x4 *k, con
     if (x == 0x9E3779B9u && lane == 7) sink[0] = x;
 }
 
+// The gather's pattern: 4 KB pages read in a shuffled order and written to
+// consecutive 4 KB slots of an output, one wave per page (K pool pages to
+// the first half of `out`, V pool pages to the second half).
+template <bool NTL, bool NTS>
+__global__ __launch_bounds__(kThreads) void page_copy_kernel(const u32x4 *k, const u32x4 *v, const int32_t *pages,
+                                                             int64_t n_list, int64_t pool_pages, u32x4 *out) {
+    const int64_t item = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    if (item >= 2 * n_list) return;
+    const int lane = threadIdx.x & 63;
+    const int64_t pg = pages[item >> 1];
+    if (pg < 0 || pg >= pool_pages) return;
+    const u32x4 *src = ((item & 1) ? v : k) + pg * 256 + lane;
+    u32x4 *dst = out + ((item & 1) * n_list + (item >> 1)) * 256 + lane;
+    u32x4 x[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = ld16<NTL>(src + 64 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st16<NTS>(dst + 64 * i, x[i]);
+}
+
+// The append's pattern: 8 KB of contiguous rows read per 4 KB page written,
+// the pages in a shuffled order, one wave per page (K pool pages from the
+// first half of `src`'s rows, V from the second).
+template <bool NTL, bool NTS>
+__global__ __launch_bounds__(kThreads) void page_mix21_kernel(const u32x4 *src, u32x4 *k, u32x4 *v,
+                                                              const int32_t *pages, int64_t n_list,
+                                                              int64_t pool_pages) {
+    const int64_t item = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    if (item >= 2 * n_list) return;
+    const int lane = threadIdx.x & 63;
+    const int64_t pg = pages[item >> 1];
+    if (pg < 0 || pg >= pool_pages) return;
+    const u32x4 *in = src + ((item & 1) * n_list + (item >> 1)) * 512 + lane;
+    u32x4 *dst = ((item & 1) ? v : k) + pg * 256 + lane;
+    u32x4 x[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = ld16<NTL>(in + 64 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st16<NTS>(dst + 64 * i, x[2 * i] ^ x[2 * i + 1]);
+}
+
 dim3 grid_for(int64_t n16) { return dim3((unsigned)(n16 / (kThreads * 4))); }
 
 }  // namespace
@@ -114,7 +159,9 @@ extern "C" {
 
 // kind: 0 read, 1 write, 2 copy, 3 mix21 (bytes = bytes read), 4 page_read
 // (src = K pool, dst = V pool, bytes = one pool's bytes, pages / n_pages =
-// the page list).  nt_load / nt_store pick the non-temporal variants.
+// the page list), 5 page_copy (as page_read, written to `sink`, which holds
+// 2 * n_pages * 4 KB), 6 page_mix21 (src holds 2 * n_pages * 8 KB of rows,
+// dst = K pool, sink = V pool).  nt_load / nt_store pick the non-temporal variants.
 // Returns 0 or the hipError_t of the launch.
 int air_ceiling_launch(int kind, int nt_load, int nt_store, const void *src, void *dst, int64_t bytes,
                        const int32_t *pages, int64_t n_pages, void *sink, void *stream) {
@@ -154,6 +201,39 @@ int air_ceiling_launch(int kind, int nt_load, int nt_store, const void *src, voi
             hipLaunchKernelGGL(page_read_kernel<true>, gp, b, 0, s, in, (const u32x4 *)dst, pages, n_pages, pool_pages, sk);
         else
             hipLaunchKernelGGL(page_read_kernel<false>, gp, b, 0, s, in, (const u32x4 *)dst, pages, n_pages, pool_pages, sk);
+        break;
+    }
+    case 5: {
+        // src = K pool, dst = V pool (bytes each), sink = output of 2 * n_pages * 4 KB
+        if (!pages || n_pages <= 0 || n_pages * 4096 > bytes) return (int)hipErrorInvalidValue;
+        const dim3 gp((unsigned)((2 * n_pages + kThreads / 64 - 1) / (kThreads / 64)));
+        const int64_t pool_pages = bytes / 4096;
+        u32x4 *o = (u32x4 *)sink;
+        const u32x4 *vv = (const u32x4 *)dst;
+        if (nt_load && nt_store)
+            hipLaunchKernelGGL((page_copy_kernel<true, true>), gp, b, 0, s, in, vv, pages, n_pages, pool_pages, o);
+        else if (nt_load)
+            hipLaunchKernelGGL((page_copy_kernel<true, false>), gp, b, 0, s, in, vv, pages, n_pages, pool_pages, o);
+        else if (nt_store)
+            hipLaunchKernelGGL((page_copy_kernel<false, true>), gp, b, 0, s, in, vv, pages, n_pages, pool_pages, o);
+        else
+            hipLaunchKernelGGL((page_copy_kernel<false, false>), gp, b, 0, s, in, vv, pages, n_pages, pool_pages, o);
+        break;
+    }
+    case 6: {
+        // src = 2 * n_pages * 8 KB of rows, dst = K pool, sink = V pool (bytes each)
+        if (!pages || n_pages <= 0 || n_pages * 4096 > bytes) return (int)hipErrorInvalidValue;
+        const dim3 gp((unsigned)((2 * n_pages + kThreads / 64 - 1) / (kThreads / 64)));
+        const int64_t pool_pages = bytes / 4096;
+        u32x4 *vp = (u32x4 *)sink;
+        if (nt_load && nt_store)
+            hipLaunchKernelGGL((page_mix21_kernel<true, true>), gp, b, 0, s, in, out, vp, pages, n_pages, pool_pages);
+        else if (nt_load)
+            hipLaunchKernelGGL((page_mix21_kernel<true, false>), gp, b, 0, s, in, out, vp, pages, n_pages, pool_pages);
+        else if (nt_store)
+            hipLaunchKernelGGL((page_mix21_kernel<false, true>), gp, b, 0, s, in, out, vp, pages, n_pages, pool_pages);
+        else
+            hipLaunchKernelGGL((page_mix21_kernel<false, false>), gp, b, 0, s, in, out, vp, pages, n_pages, pool_pages);
         break;
     }
     default:

@@ -121,7 +121,10 @@ def ceilings_leg(torch, iters=20):
     kernels of air.rs_amd/csrc/bench/ceilings.hip on 1 GiB buffers (2 GiB for
     the page pools): contiguous read, contiguous write, copy (1 byte written
     per byte read), mix21 (2 bytes read per byte written), and page_read
-    (4 KB K and V pages in a shuffled order, one wave per page).  Each
+    (4 KB K and V pages in a shuffled order, one wave per page), and
+    page_copy (half of those pages copied to consecutive 4 KB slots: the
+    gather's pattern) and page_mix21 (a quarter of them written from 8 KB
+    of contiguous rows each: the append's pattern).  Each
     pattern runs with plain and non-temporal loads / stores; the faster is
     kept, with its variant."""
     import ctypes
@@ -138,6 +141,11 @@ def ceilings_leg(torch, iters=20):
     b.view(torch.int32).random_()
     sink = torch.zeros(64, dtype=torch.int32, device="cuda")
     pages = torch.from_numpy(np.random.default_rng(13).permutation(nbytes // 4096).astype(np.int32)).cuda()
+    # page_copy: half of each pool's pages (shuffled) into a 1 GiB output
+    half = pages[: nbytes // 8192].contiguous()
+    # page_mix21: a quarter of each pool's pages written from 1 GiB of rows
+    quarter = pages[: nbytes // 16384].contiguous()
+    pc_out = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     kinds = {  # name: (kind, bytes moved per launch, (load nt options), (store nt options), n_pages)
@@ -146,6 +154,8 @@ def ceilings_leg(torch, iters=20):
         "copy": (2, 2 * nbytes, (0, 1), (0, 1), 0),
         "mix21": (3, nbytes + nbytes // 2, (0, 1), (0, 1), 0),
         "page_read": (4, 2 * nbytes, (0, 1), (0,), nbytes // 4096),
+        "page_copy": (5, 2 * nbytes, (0, 1), (0, 1), nbytes // 8192),
+        "page_mix21": (6, nbytes // 2 * 3, (0, 1), (0, 1), nbytes // 16384),
     }
     out = {}
     for name, (kind, moved, lds, sts, npg) in kinds.items():
@@ -153,8 +163,14 @@ def ceilings_leg(torch, iters=20):
         for ntl in lds:
             for nts in sts:
                 def fn(kind=kind, ntl=ntl, nts=nts, npg=npg):
-                    rc = lib.air_ceiling_launch(kind, ntl, nts, P(a), P(b), nbytes, P(pages) if npg else None,
-                                                npg, P(sink), stream)
+                    if kind == 5:      # K / V pools a, b -> pc_out
+                        args = (P(a), P(b), P(half), P(pc_out))
+                    elif kind == 6:    # rows in pc_out -> K / V pools a, b
+                        args = (P(pc_out), P(a), P(quarter), P(b))
+                    else:
+                        args = (P(a), P(b), P(pages) if npg else None, P(sink))
+                    rc = lib.air_ceiling_launch(kind, ntl, nts, args[0], args[1], nbytes, args[2], npg, args[3],
+                                                stream)
                     assert rc == 0, f"ceiling launch {kind} failed ({rc})"
                 fn()
                 ms = timed_loop(torch, fn, iters)
@@ -168,7 +184,7 @@ def ceilings_leg(torch, iters=20):
                 if best is None or gbps > best["gbps"]:
                     best = {"gbps": round(gbps, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4), "variant": variant}
         out[name] = best
-    del a, b
+    del a, b, pc_out
     return out
 
 
@@ -580,7 +596,9 @@ def main():
         extra["frac_of_ceiling"] = {
             "decode_vs_page_read": round(dec_gbps / c["page_read"]["gbps"], 4),
             "gather_vs_copy": round(extra["gather_gbps"] / c["copy"]["gbps"], 4),
+            "gather_vs_page_copy": round(extra["gather_gbps"] / c["page_copy"]["gbps"], 4),
             "append_vs_mix21": round(extra["append_gbps"] / c["mix21"]["gbps"], 4),
+            "append_vs_page_mix21": round(extra["append_gbps"] / c["page_mix21"]["gbps"], 4),
         }
 
     if not args.no_configs and not args.only_decode:
