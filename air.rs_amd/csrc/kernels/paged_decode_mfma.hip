@@ -80,6 +80,9 @@ constexpr int kMinChunk = 4;               // tiles per slice at least
 #ifndef AIRKV_DECODE_NT_LOADS
 #define AIRKV_DECODE_NT_LOADS 1            // non-temporal K/V loads, bf16 pages
 #endif
+#ifndef AIRKV_DECODE_K16
+#define AIRKV_DECODE_K16 1                 // 1-byte pages: K as 16-byte loads re-paired across lanes (else 8-byte loads)
+#endif
 #ifndef AIRKV_DECODE_QNT_LOADS
 #define AIRKV_DECODE_QNT_LOADS 0           // the same for 1-byte pages (plain loads measured faster)
 #endif
@@ -210,10 +213,14 @@ __device__ __forceinline__ int seq_of_tile(const int32_t *pre, int B, int t) {
 // Raw registers of one 16-token tile as loaded, before any conversion.
 // bf16 pages: K in the MFMA A-operand layout (lane: row r16, head_dim 8*g4 +
 // 32*ks .. +8 for step ks) and four 16-byte V chunks.  1-byte pages (int8
-// Q8_0 codes, fp8): lane holds 32 contiguous codes -- exactly one scale group
-// of 32 -- of one K row and one V row, plus the two f32 scales.
+// Q8_0 codes, fp8): K in the same layout (8 codes per step: k-step ks is
+// head_dim 32*ks .. +32, one scale group), the lane's own K row scale (row
+// r16, head_dim 32*g4), and 32 contiguous codes -- one scale group -- of one
+// V row with its scale.
 template <int DT> struct Tile {
-    u32x4 k[2], v[2];
+    u32x2 k[4];          // 8-byte K loads: step ks
+    u32x4 k16[2];        // 16-byte K loads: head_dim 64*m + 16*g4 .. +16
+    u32x4 v[2];
     uint32_t ks, vs;
 };
 template <> struct Tile<AIR_KV_BF16> {
@@ -246,6 +253,29 @@ __device__ __forceinline__ u32x2 dequant4(uint32_t w, float s) {
     }
     return u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2)),
                  __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2))};
+}
+
+// Eight 1-byte K codes as four bf16 pairs, exactly (element 0 in the low
+// half of word 0).  int8: the code biased to an unsigned byte, q + 128 (x ^
+// 0x80), whose value 1..255 bf16 holds exactly; the bias is taken out of the
+// product by starting the accumulator at -128 * (sum of the query's elements
+// over the step).  fp8: the hardware's OCP E4M3 -> bf16 conversion at unit
+// scale, exact for every code the reference encoder emits (every E4M3 value
+// is a bf16 value; zero exponent fields only as +-0, 0xFF never).
+template <int DT>
+__device__ __forceinline__ u32x4 codes_bf16(u32x2 w) {
+    if constexpr (DT == AIR_KV_INT8) {
+        const uint32_t u0 = w[0] ^ 0x80808080u, u1 = w[1] ^ 0x80808080u;
+        return u32x4{bf16_pair((float)(u0 & 0xFFu), (float)((u0 >> 8) & 0xFFu)),
+                     bf16_pair((float)((u0 >> 16) & 0xFFu), (float)(u0 >> 24)),
+                     bf16_pair((float)(u1 & 0xFFu), (float)((u1 >> 8) & 0xFFu)),
+                     bf16_pair((float)((u1 >> 16) & 0xFFu), (float)(u1 >> 24))};
+    } else {
+        return u32x4{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[0], 1.0f, false)),
+                     __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[0], 1.0f, true)),
+                     __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[1], 1.0f, false)),
+                     __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[1], 1.0f, true))};
+    }
 }
 
 // Waves per SIMD the slice kernel is built for (its register budget) and
@@ -281,6 +311,9 @@ void decode_mfma_kernel(DecodeArgs a) {
     __shared__ int32_t s_pre[kMaxBatch + 1];
     __shared__ int32_t s_wsum[kWaves];
     __shared__ __align__(16) uint16_t s_v[kWaves * VTILE];
+    // 1-byte pages: the tile's K scales [k-step][token] per wave (lane (r16,
+    // g4) holds row r16's scale of step g4; the S rows it needs are 4*g4..+3)
+    __shared__ __align__(16) float s_ksc[kWaves][QUANT ? 64 : 4];
 
     tile_prefix<BS>(a, s_pre, s_wsum);
     const int B = a.batch;
@@ -322,24 +355,30 @@ void decode_mfma_kernel(DecodeArgs a) {
     };
 
     // ---- Q^T in the B-operand layout.  The QK contraction runs over head_dim
-    // in an order of our choosing as long as K and Q agree: bf16 pages use
-    // d = 32*ks + 8*g4 + j (16 contiguous K bytes per lane and step), 1-byte
-    // pages d = 32*g4 + 8*ks + j (a lane's four steps cover one 32-element
-    // scale group, loaded as 32 contiguous codes).
+    // as d = 32*ks + 8*g4 + j: lane (r16, g4) holds 8 consecutive elements
+    // of K row r16 per step (16 bytes of bf16 pages, 8 codes of 1-byte
+    // pages), and step ks is head_dim 32*ks .. +32, one scale group of
+    // 1-byte pages.
     // The loads go through a buffer descriptor that spans exactly the group's
     // G query rows: lanes of heads >= G fall outside it and read zeros, so
     // there is no branch (a branch around a load inside the tile loop costs
     // the compiler ~50 extra registers).
     u32x4 qhi[KSTEPS], qlo[KSTEPS];
+    float qbias[KSTEPS];                     // int8 pages: -128 * sum of q over step ks (head r16)
     auto load_q = [&](int bq) {
         constexpr int QB = QF32 ? 4 : 2;
         const char *qg = (const char *)a.q + ((int64_t)bq * a.n_q_heads + kh * G) * D * QB;
         const __amdgpu_buffer_rsrc_t rq =
             __builtin_amdgcn_make_buffer_rsrc((void *)qg, (short)0, G * D * QB, kBufferWord3);
-        const int qoff = (r16 * D + (QUANT ? 32 : 8) * g4) * QB;
-        constexpr int step = (QUANT ? 8 : 32) * QB;
+        constexpr int step = 32 * QB;
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
+            // the step's element order (see the K operands): 1-byte pages
+            // with 16-byte K loads hold, in slot g4, head_dim 32*ks +
+            // 16*(g4 & 1) + 8*((g4 >> 1) ^ (ks & 1)) .. +8
+            const int qoff = (QUANT && AIRKV_DECODE_K16)
+                                 ? (r16 * D + 16 * (g4 & 1) + 8 * ((g4 >> 1) ^ (ks & 1))) * QB
+                                 : (r16 * D + 8 * g4) * QB;
             if constexpr (QF32) {
                 const u32x4 x0 = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + step * ks, 0, 0);
                 const u32x4 x1 = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + step * ks + 16, 0, 0);
@@ -355,6 +394,21 @@ void decode_mfma_kernel(DecodeArgs a) {
             } else {
                 qhi[ks] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + step * ks, 0, 0);
                 qlo[ks] = u32x4{0, 0, 0, 0};
+            }
+        }
+        if constexpr (DT == AIR_KV_INT8) {
+#pragma unroll
+            for (int ks = 0; ks < KSTEPS; ++ks) {
+                float sum = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    sum += __uint_as_float(qhi[ks][j] << 16) + __uint_as_float(qhi[ks][j] & 0xFFFF0000u);
+                    if constexpr (QF32)
+                        sum += __uint_as_float(qlo[ks][j] << 16) + __uint_as_float(qlo[ks][j] & 0xFFFF0000u);
+                }
+                sum += __shfl_xor(sum, 16);
+                sum += __shfl_xor(sum, 32);
+                qbias[ks] = -128.0f * sum;
             }
         }
         // Q is loaded on a branch (a new sequence), so at the QK products the
@@ -376,7 +430,7 @@ void decode_mfma_kernel(DecodeArgs a) {
     // row lane / 4, 32 codes from column 32 * g4 (K) or 32 * (lane % 4) (V).
     const int vrow = QUANT ? lane >> 2 : lane >> 4;
     const int vcol = QUANT ? 32 * (lane & 3) : 8 * (lane & 15);
-    const int k_boff = QUANT ? r16 * D + 32 * g4 : (r16 * D + 8 * g4) * 2;
+    const int k_boff = (QUANT && AIRKV_DECODE_K16) ? r16 * D + 16 * g4 : (r16 * D + 8 * g4) * EB;
     const int v_boff = (vrow * D + vcol) * EB;
     const int n_sc = QUANT ? D / a.scale_group : 0;              // scales per row
     const int k_soff = QUANT ? (r16 * n_sc + (32 * g4) / a.scale_group) * 4 : 0;
@@ -400,11 +454,18 @@ void decode_mfma_kernel(DecodeArgs a) {
         const __amdgpu_buffer_rsrc_t rv =
             __builtin_amdgcn_make_buffer_rsrc((void *)(vp + row0 * D * EB), (short)0, 16 * D * EB, kBufferWord3);
         if constexpr (QUANT) {
+            if constexpr (AIRKV_DECODE_K16) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                t.k[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, k_boff + 16 * i, 0, kQLoadAux);
-                t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, v_boff + 16 * i, 0, kQLoadAux);
+                for (int m = 0; m < 2; ++m)
+                    t.k16[m] = __builtin_amdgcn_raw_buffer_load_b128(rk, k_boff + 64 * m, 0, kQLoadAux);
+            } else {
+#pragma unroll
+                for (int ks = 0; ks < KSTEPS; ++ks)
+                    t.k[ks] = __builtin_amdgcn_raw_buffer_load_b64(rk, k_boff + 32 * ks, 0, kQLoadAux);
             }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, v_boff + 16 * i, 0, kQLoadAux);
             const int64_t srow = row0 * n_sc;
             const __amdgpu_buffer_rsrc_t rks = __builtin_amdgcn_make_buffer_rsrc(
                 (void *)(a.k_scales + srow), (short)0, 16 * n_sc * 4, kBufferWord3);
@@ -461,29 +522,57 @@ void decode_mfma_kernel(DecodeArgs a) {
         // consumed on all paths and the loads in flight never need draining.
         if (!ok && lane == 0) atomicAdd(a.errors, 1ull);
         const int nv = ok ? __builtin_amdgcn_readlane(nv_l, idx) : 0;   // valid tokens
-        u32x4 kop[KSTEPS];                   // K as bf16 A operands
-        if constexpr (QUANT) {
-            const float ksc = __uint_as_float(t.ks);
-#pragma unroll
-            for (int ks = 0; ks < KSTEPS; ++ks) {
-                const u32x2 x = dequant4<DT>(t.k[ks >> 1][(ks & 1) * 2], ksc);
-                const u32x2 y = dequant4<DT>(t.k[ks >> 1][(ks & 1) * 2 + 1], ksc);
-                kop[ks] = u32x4{x[0], x[1], y[0], y[1]};
-            }
-        } else {
-#pragma unroll
-            for (int ks = 0; ks < KSTEPS; ++ks) kop[ks] = t.k[ks];
-        }
-        f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) {
-            s = mfma_qk(kop[ks], qhi[ks], s);
-            if constexpr (QF32) s = mfma_qk(kop[ks], qlo[ks], s);
-        }
         // lane holds S[token 4*g4 + i][head r16]
         float sc[4];
+        if constexpr (QUANT) {
+            // 1-byte pages: the codes themselves are the A operands (exact in
+            // bf16) and each k-step is one scale group, so the products are
+            // exact and the group scales apply to the step sums afterwards:
+            // S[t] = sum_ks scale[t][ks] * (codes[t] . q over step ks)
+            s_ksc[wave][g4 * 16 + r16] = __uint_as_float(t.ks);
+            // The step's 8 codes of row r16 for slot g4.  16-byte loads give
+            // lane (r16, g4) head_dim 64*m + 16*g4 .. +16, so steps 2m and
+            // 2m + 1 (groups 2m, 2m + 1) sit in lanes g4 < 2 and g4 >= 2
+            // respectively, 16 codes each: every lane keeps its first 8 for
+            // its own group's step and hands its last 8 to the lane 32 away
+            // for the same step.
+            u32x2 kc[KSTEPS];
+            if constexpr (AIRKV_DECODE_K16) {
+                const bool lower = g4 < 2;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sc[i] = s[i] * a.scale_log2;
+                for (int m = 0; m < 2; ++m) {
+                    const u32x4 w = t.k16[m];
+                    const uint32_t p2 = __shfl_xor(w[2], 32), p3 = __shfl_xor(w[3], 32);
+                    kc[2 * m] = lower ? u32x2{w[0], w[1]} : u32x2{p2, p3};
+                    kc[2 * m + 1] = lower ? u32x2{p2, p3} : u32x2{w[0], w[1]};
+                }
+            } else {
+#pragma unroll
+                for (int ks = 0; ks < KSTEPS; ++ks) kc[ks] = t.k[ks];
+            }
+            f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < KSTEPS; ++ks) {
+                const float b0 = DT == AIR_KV_INT8 ? qbias[ks] : 0.0f;
+                f32x4 p = mfma_qk(codes_bf16<DT>(kc[ks]), qhi[ks], f32x4{b0, b0, b0, b0});
+                if constexpr (QF32) p = mfma_qk(codes_bf16<DT>(kc[ks]), qlo[ks], p);
+                // the step's scales of this lane's tokens 4*g4 .. +3
+                const f32x4 ksc = *reinterpret_cast<const f32x4 *>(&s_ksc[wave][ks * 16 + 4 * g4]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s[i] = __builtin_fmaf(ksc[i], p[i], s[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[i] = s[i] * a.scale_log2;
+        } else {
+            f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < KSTEPS; ++ks) {
+                s = mfma_qk(t.k[ks], qhi[ks], s);
+                if constexpr (QF32) s = mfma_qk(t.k[ks], qlo[ks], s);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[i] = s[i] * a.scale_log2;
+        }
         // only a sequence's last tile (or a tile of an out-of-pool block) is
         // partial: the masks run on those tiles alone (nv is uniform)
         const bool full = nv == 16;
