@@ -137,6 +137,28 @@ __device__ __forceinline__ uint32_t bf16_pair(float x, float y) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{x, y}), bf16x2));
 }
 
+// Reductions across the lanes 16 and 32 apart with the gfx950 lane-swap
+// instructions instead of LDS permutes.  permlane16_swap(v, v) returns
+// {v[l & ~16], v[l | 16]} in lane l, permlane32_swap(v, v) returns
+// {v[l & ~32], v[l | 32]}: the two halves of each pair, in the same order
+// in both lanes, so both lanes compute the same bits.
+__device__ __forceinline__ float max_x16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_x32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_x16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_x32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ void store_out(const DecodeArgs &a, int64_t idx, float v) {
     if (a.out_dtype == AIR_KV_F32) ((float *)a.out)[idx] = v;
     else ((uint16_t *)a.out)[idx] = bf16_rne(v);
@@ -375,10 +397,9 @@ void decode_mfma_kernel(DecodeArgs a) {
         for (int ks = 0; ks < KSTEPS; ++ks) {
             // the step's element order (see the K operands): 1-byte pages
             // with 16-byte K loads hold, in slot g4, head_dim 32*ks +
-            // 16*(g4 & 1) + 8*((g4 >> 1) ^ (ks & 1)) .. +8
-            const int qoff = (QUANT && AIRKV_DECODE_K16)
-                                 ? (r16 * D + 16 * (g4 & 1) + 8 * ((g4 >> 1) ^ (ks & 1))) * QB
-                                 : (r16 * D + 8 * g4) * QB;
+            // 16*(g4 & 1) + 8*(g4 >> 1) .. +8
+            const int qoff = (QUANT && AIRKV_DECODE_K16) ? (r16 * D + 16 * (g4 & 1) + 8 * (g4 >> 1)) * QB
+                                                         : (r16 * D + 8 * g4) * QB;
             if constexpr (QF32) {
                 const u32x4 x0 = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + step * ks, 0, 0);
                 const u32x4 x1 = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + step * ks + 16, 0, 0);
@@ -486,8 +507,7 @@ void decode_mfma_kernel(DecodeArgs a) {
 
     // The piece of sequence bq held by this wave ends: write it out.
     auto emit = [&](int bq) {
-        float l = l_run + __shfl_xor(l_run, 16);
-        l += __shfl_xor(l, 32);
+        const float l = sum_x32(sum_x16(l_run));
         const int w0 = s_pre[bq] / chunk, w1 = (s_pre[bq + 1] - 1) / chunk;
         if (r16 < G) {
             if (w0 == w1) {                  // the whole sequence: final output
@@ -531,20 +551,23 @@ void decode_mfma_kernel(DecodeArgs a) {
             // S[t] = sum_ks scale[t][ks] * (codes[t] . q over step ks)
             s_ksc[wave][g4 * 16 + r16] = __uint_as_float(t.ks);
             // The step's 8 codes of row r16 for slot g4.  16-byte loads give
-            // lane (r16, g4) head_dim 64*m + 16*g4 .. +16, so steps 2m and
-            // 2m + 1 (groups 2m, 2m + 1) sit in lanes g4 < 2 and g4 >= 2
-            // respectively, 16 codes each: every lane keeps its first 8 for
-            // its own group's step and hands its last 8 to the lane 32 away
-            // for the same step.
+            // lane (r16, g4) head_dim 64*m + 16*g4 .. +16 (codes w0..w3), so
+            // group 2m sits in lanes g4 < 2 and group 2m + 1 in lanes g4 >= 2,
+            // 16 codes each.  One lane swap of (w0, w2) -- and of (w1, w3) --
+            // across the two halves of the wave gives step 2m the lower
+            // lanes' own w0, w1 and, in the upper lanes, the lower partner's
+            // w2, w3, and gives step 2m + 1 the upper partner's w0, w1 in the
+            // lower lanes and the upper lanes' own w2, w3: in both steps slot
+            // g4 holds head_dim 16*(g4 & 1) + 8*(g4 >> 1) .. +8 of the group.
             u32x2 kc[KSTEPS];
             if constexpr (AIRKV_DECODE_K16) {
-                const bool lower = g4 < 2;
 #pragma unroll
                 for (int m = 0; m < 2; ++m) {
                     const u32x4 w = t.k16[m];
-                    const uint32_t p2 = __shfl_xor(w[2], 32), p3 = __shfl_xor(w[3], 32);
-                    kc[2 * m] = lower ? u32x2{w[0], w[1]} : u32x2{p2, p3};
-                    kc[2 * m + 1] = lower ? u32x2{p2, p3} : u32x2{w[0], w[1]};
+                    const auto s0 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+                    const auto s1 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+                    kc[2 * m] = u32x2{s0[0], s1[0]};
+                    kc[2 * m + 1] = u32x2{s0[1], s1[1]};
                 }
             } else {
 #pragma unroll
@@ -581,8 +604,7 @@ void decode_mfma_kernel(DecodeArgs a) {
             for (int i = 0; i < 4; ++i) sc[i] = 4 * g4 + i < nv ? sc[i] : -INFINITY;
         }
         float mt = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-        mt = fmaxf(mt, __shfl_xor(mt, 16));
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        mt = max_x32(max_x16(mt));
         // The running max is raised only when some head's tile max exceeds it
         // by more than 2^8 (and on the first tile): probabilities then stay
         // below 256, exact in the hi + lo split, and most tiles skip the
