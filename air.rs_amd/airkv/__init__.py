@@ -14,6 +14,8 @@ from .paged_attention import (BLOCK_SIZE, MAX_BLOCKS, BlockAllocator, BlockTable
                               SequenceManager, num_blocks_for_tokens)
 from .pool import KvPool, wire_int8_quantize
 from .session import PagedSessionCache
+from . import pd_wire
+from .pd_wire import KvBlock
 
 __all__ = [
     "AIR_KV_OK", "AIR_KV_E_INVALID_ARG", "AIR_KV_E_OOM", "AIR_KV_E_NOT_FOUND", "AIR_KV_E_HIP",
@@ -21,5 +23,5 @@ __all__ = [
     "LIB_PATH", "SIGNATURES", "AirKvError", "last_error", "load", "KvSwapManager",
     "pool_callbacks", "BLOCK_SIZE", "MAX_BLOCKS", "BlockAllocator", "BlockTable",
     "SequenceManager", "num_blocks_for_tokens", "KvPool", "PagedSessionCache", "wire_int8_quantize",
-    "kv_compress",
+    "kv_compress", "pd_wire", "KvBlock",
 ]

@@ -143,7 +143,8 @@ int air_seq_truncate(air_seq_manager *m, uint32_t seq, int64_t n_tokens);
  * gets this sequence's own fill of it. */
 int air_seq_cow_block(air_seq_manager *m, uint32_t seq, int64_t index, uint32_t *old_block,
                       uint32_t *new_block);
-/* table (:322-324): copies up to `cap` block ids. */
+/* table (:322-324): copies the block ids (at most `cap`; `blocks` may be
+ * NULL to ask only for the counts). */
 int air_seq_table(const air_seq_manager *m, uint32_t seq, uint32_t *blocks, int32_t cap,
                   int32_t *n_blocks, int64_t *n_tokens);
 /* Flattened int32 block tables [n][max_blocks] (unused entries = -1) and
@@ -385,6 +386,48 @@ int air_kv_wire_int8_quantize(void *stream, const void *wire, int32_t n_blocks,
  * codes + i * wire_bytes / 2 and scales[i] for block ids[i]. */
 int air_kv_pack_blocks_int8(air_kv_pool *pool, void *stream, const int32_t *ids, int32_t n,
                             int8_t *codes, float *scales);
+
+/* Host-side framing around the wire data (plain host memory, no device
+ * work; every integer little-endian, as the reference's to_le_bytes).       */
+
+/* KvBlock::serialise (src/pd_disagg.rs:52-62): [block_id:4][layer_idx:2]
+ * [data_len:4][data], 10 + data_len bytes; out must hold them (cap). */
+size_t air_kv_block_frame_bytes(size_t data_len);
+int air_kv_block_serialise(uint32_t block_id, uint16_t layer_idx, const void *data, size_t data_len,
+                           void *out, size_t cap, size_t *written);
+/* KvBlock::deserialise (src/pd_disagg.rs:85-104): AIR_KV_E_INVALID_ARG where
+ * the reference returns None (fewer than 10 bytes, or fewer than 10 +
+ * data_len); *data points into buf. */
+int air_kv_block_deserialise(const void *buf, size_t len, uint32_t *block_id, uint16_t *layer_idx,
+                             const void **data, size_t *data_len);
+/* n frames back to back, frame i for block_ids[i] with the block_bytes of
+ * wire data at data + i * block_bytes (air_kv_pack_blocks' output copied to
+ * the host): n * (10 + block_bytes) bytes. */
+int air_kv_block_serialise_n(const uint32_t *block_ids, uint16_t layer_idx, const void *data,
+                             size_t block_bytes, int32_t n, void *out);
+/* The int8 transfer payload of TcpKvConnector::send_blocks
+ * (src/pd_disagg.rs:267-276): [block_id:4][layer_idx:2][scale:4, f32]
+ * [len:4][codes], 14 + n_codes bytes.  (The reference's receiver parses every
+ * payload with KvBlock::deserialise, which reads the scale's bits as data_len;
+ * air_kv_int8_payload_deserialise reads the layout the sender writes.) */
+size_t air_kv_int8_payload_bytes(size_t n_codes);
+int air_kv_int8_payload_serialise(uint32_t block_id, uint16_t layer_idx, float scale, const int8_t *codes,
+                                  size_t n_codes, void *out, size_t cap, size_t *written);
+int air_kv_int8_payload_deserialise(const void *buf, size_t len, uint32_t *block_id, uint16_t *layer_idx,
+                                    float *scale, const int8_t **codes, size_t *n_codes);
+/* n payloads back to back from air_kv_pack_blocks_int8's codes and scales
+ * (copied to the host): n * (14 + codes_per_block) bytes. */
+int air_kv_int8_payload_serialise_n(const uint32_t *block_ids, uint16_t layer_idx, const float *scales,
+                                    const int8_t *codes, size_t codes_per_block, int32_t n, void *out);
+/* The per-payload record header of the TCP / RDMA streams
+ * (src/pd_disagg.rs:277-279, :539-541): [seq_id:8][payload_len:4]. */
+int air_kv_stream_record_header(uint64_t seq_id, uint32_t payload_len, uint8_t out[12]);
+/* WarpHeader::serialise / deserialise (src/warp_protocol.rs:30-63):
+ * ["WARP"][version:2 = 0x0101][features:8][body_len:4]; deserialise rejects
+ * another magic or major version with AIR_KV_E_INVALID_ARG. */
+int air_kv_warp_header_serialise(uint64_t features, uint32_t body_len, uint8_t out[18]);
+int air_kv_warp_header_deserialise(const uint8_t *buf, size_t len, uint64_t *features, uint32_t *body_len,
+                                   uint16_t *version);
 
 /* ------------------------------------------------------------------------ */
 /* kv_compress warm-tier codecs (src/kv_compress.rs)                          */

@@ -64,6 +64,10 @@ def lib():
                 "orc_q8_dequantize": (None, [_P, _P, _SZ, _P]),
                 "orc_fp8_quantize_group": (_f32, [_P, _i32, _P]),
                 "orc_pd_int8_quantize": (_f32, [_P, _SZ, _P]),
+                "orc_kvblock_serialise": (_SZ, [ctypes.c_uint32, ctypes.c_uint16, _P, ctypes.c_uint32, _P]),
+                "orc_kvblock_deserialise": (_i32, [_P, _SZ, _P, _P, _P]),
+                "orc_tcp_int8_payload": (_SZ, [ctypes.c_uint32, ctypes.c_uint16, _P, _SZ, _P]),
+                "orc_warp_header_serialise": (None, [_u64, ctypes.c_uint32, _P]),
                 "orc_kv_append": (_i32, [_i32, _i32, _i32, _i32, _i32, _i64, _P, _P, _P, _i32,
                                          _P, _P, _P, _P]),
                 "orc_kv_gather": (_i32, [_i32, _i32, _i32, _i32, _i32, _i64, _P, _P, _P, _P,
@@ -192,6 +196,40 @@ def pd_int8_quantize(bf16_bits):
     q = np.empty(len(b), np.int8)
     s = lib().orc_pd_int8_quantize(_ptr(b), len(b), _ptr(q))
     return q, np.float32(s)
+
+
+def kvblock_serialise(block_id, layer_idx, data: bytes) -> bytes:
+    """KvBlock::serialise (src/pd_disagg.rs:52-62)."""
+    d = np.frombuffer(bytes(data), np.uint8)
+    out = np.empty(10 + len(d), np.uint8)
+    n = lib().orc_kvblock_serialise(block_id, layer_idx, _ptr(d) if len(d) else None, len(d), _ptr(out))
+    return out[:n].tobytes()
+
+
+def kvblock_deserialise(buf: bytes):
+    """KvBlock::deserialise (src/pd_disagg.rs:85-104): None or
+    (block_id, layer_idx, data)."""
+    b = np.frombuffer(bytes(buf), np.uint8)
+    bid, layer, n = ctypes.c_uint32(), ctypes.c_uint16(), ctypes.c_uint32()
+    ok = lib().orc_kvblock_deserialise(_ptr(b) if len(b) else None, len(b), ctypes.byref(bid),
+                                       ctypes.byref(layer), ctypes.byref(n))
+    if not ok:
+        return None
+    return bid.value, layer.value, b[10:10 + n.value].tobytes()
+
+
+def tcp_int8_payload(block_id, layer_idx, bf16_bits) -> bytes:
+    """The int8 payload TcpKvConnector::send_blocks writes (src/pd_disagg.rs:267-276)."""
+    b = _c(bf16_bits, np.uint16).ravel()
+    out = np.empty(14 + len(b), np.uint8)
+    n = lib().orc_tcp_int8_payload(block_id, layer_idx, _ptr(b), len(b), _ptr(out))
+    return out[:n].tobytes()
+
+
+def warp_header_serialise(features, body_len) -> bytes:
+    out = np.empty(18, np.uint8)
+    lib().orc_warp_header_serialise(features, body_len, _ptr(out))
+    return out.tobytes()
 
 
 # --------------------------------------------------------------------------

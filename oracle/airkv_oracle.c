@@ -194,6 +194,64 @@ float orc_pd_int8_quantize(const uint16_t *bf16, size_t n, int8_t *q) {
     return scale;
 }
 
+/* KvBlock::serialise, src/pd_disagg.rs:52-62: block_id.to_le_bytes(),
+ * layer_idx.to_le_bytes(), (data.len() as u32).to_le_bytes(), data.  The
+ * bytes are assembled one at a time from the integers (no host byte-order
+ * assumption).  Returns the frame length. */
+size_t orc_kvblock_serialise(uint32_t block_id, uint16_t layer_idx, const uint8_t *data, uint32_t n,
+                             uint8_t *out) {
+    size_t o = 0;
+    for (int i = 0; i < 4; ++i) out[o++] = (uint8_t)(block_id >> (8 * i));
+    for (int i = 0; i < 2; ++i) out[o++] = (uint8_t)(layer_idx >> (8 * i));
+    for (int i = 0; i < 4; ++i) out[o++] = (uint8_t)(n >> (8 * i));
+    for (uint32_t i = 0; i < n; ++i) out[o++] = data[i];
+    return o;
+}
+
+/* KvBlock::deserialise, src/pd_disagg.rs:85-104: None (returns 0) when the
+ * buffer is shorter than 10 bytes or than 10 + data_len; else 1, with the
+ * fields and the data offset (10). */
+int orc_kvblock_deserialise(const uint8_t *buf, size_t len, uint32_t *block_id, uint16_t *layer_idx,
+                            uint32_t *data_len) {
+    if (len < 10) return 0;
+    uint32_t id = 0, n = 0;
+    for (int i = 0; i < 4; ++i) id |= (uint32_t)buf[i] << (8 * i);
+    const uint16_t layer = (uint16_t)(buf[4] | (buf[5] << 8));
+    for (int i = 0; i < 4; ++i) n |= (uint32_t)buf[6 + i] << (8 * i);
+    if (len < 10 + (size_t)n) return 0;
+    *block_id = id;
+    *layer_idx = layer;
+    *data_len = n;
+    return 1;
+}
+
+/* The int8 payload of TcpKvConnector::send_blocks, src/pd_disagg.rs:267-276:
+ * KvBlock::int8_quantize of the block's bf16 data, then block_id, layer_idx,
+ * scale (f32 bits), (q.len() as u32), the codes as bytes.  Returns the
+ * payload length. */
+size_t orc_tcp_int8_payload(uint32_t block_id, uint16_t layer_idx, const uint16_t *bf16, size_t n,
+                            uint8_t *out) {
+    int8_t *q = (int8_t *)(out + 14);
+    const float scale = orc_pd_int8_quantize(bf16, n, q);
+    uint32_t sbits;
+    memcpy(&sbits, &scale, 4);
+    size_t o = 0;
+    for (int i = 0; i < 4; ++i) out[o++] = (uint8_t)(block_id >> (8 * i));
+    for (int i = 0; i < 2; ++i) out[o++] = (uint8_t)(layer_idx >> (8 * i));
+    for (int i = 0; i < 4; ++i) out[o++] = (uint8_t)(sbits >> (8 * i));
+    for (int i = 0; i < 4; ++i) out[o++] = (uint8_t)((uint32_t)n >> (8 * i));
+    return o + n;
+}
+
+/* WarpHeader::serialise, src/warp_protocol.rs:30-38: "WARP", version 0x0101,
+ * features, body_len, little-endian; 18 bytes. */
+void orc_warp_header_serialise(uint64_t features, uint32_t body_len, uint8_t *out) {
+    out[0] = 'W'; out[1] = 'A'; out[2] = 'R'; out[3] = 'P';
+    out[4] = 0x01; out[5] = 0x01;
+    for (int i = 0; i < 8; ++i) out[6 + i] = (uint8_t)(features >> (8 * i));
+    for (int i = 0; i < 4; ++i) out[14 + i] = (uint8_t)(body_len >> (8 * i));
+}
+
 /* ------------------------------------------------------------------------ */
 /* Paged pool: append and gather                                            */
 /* ------------------------------------------------------------------------ */

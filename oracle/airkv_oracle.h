@@ -47,6 +47,13 @@ void orc_q8_dequantize(const int8_t *q, const float *scales, size_t n, float *ou
 float orc_fp8_quantize_group(const float *x, int n, uint8_t *q);
 /* KvBlock::int8_quantize over a bf16 buffer (src/pd_disagg.rs:65-83). */
 float orc_pd_int8_quantize(const uint16_t *bf16, size_t n, int8_t *q);
+size_t orc_kvblock_serialise(uint32_t block_id, uint16_t layer_idx, const uint8_t *data, uint32_t n,
+                             uint8_t *out);
+int orc_kvblock_deserialise(const uint8_t *buf, size_t len, uint32_t *block_id, uint16_t *layer_idx,
+                            uint32_t *data_len);
+size_t orc_tcp_int8_payload(uint32_t block_id, uint16_t layer_idx, const uint16_t *bf16, size_t n,
+                            uint8_t *out);
+void orc_warp_header_serialise(uint64_t features, uint32_t body_len, uint8_t *out);
 
 /* ---- paged pool operations (definitional) -------------------------------- */
 /* Append n_tokens rows src[t][h][d] (f32) into the pool at slot_mapping[t].

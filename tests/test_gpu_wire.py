@@ -154,3 +154,26 @@ def test_bf16_roundtrip_and_bad_ids():
     torch.cuda.synchronize()
     assert pool.error_count() == 3
     log("wire bad ids counted")
+
+
+@pytest.mark.parametrize("dtype", [airkv.BF16, airkv.INT8])
+def test_frames_of_device_pages_match_oracle(dtype):
+    """Serialised KvBlocks of device-packed pages (the send side of
+    src/pd_disagg.rs:534 and :267-276) equal the oracle's frames of the
+    oracle's wire data, byte for byte, for both the plain and the int8
+    payloads; the frames parse back to the same blocks."""
+    from airkv import pd_wire
+    pool = _filled_pool(dtype, seed=40 + int(dtype))
+    ids = np.array([3, 17, 0, 9], np.int32)
+    wire = _expected_wire(pool, ids)                       # bf16 bits [n][elems]
+    got = pd_wire.frames_from_pool(pool, ids, layer_idx=5)
+    want = b"".join(oracle.kvblock_serialise(int(i), 5, w.tobytes()) for i, w in zip(ids, wire))
+    assert got == want
+    step = 10 + wire.shape[1] * 2
+    for j, i in enumerate(ids):
+        blk = airkv.KvBlock.deserialise(got[j * step:(j + 1) * step])
+        assert blk.block_id == i and blk.layer_idx == 5 and blk.data == wire[j].tobytes()
+    got8 = pd_wire.int8_payloads_from_pool(pool, ids, layer_idx=5)
+    want8 = b"".join(oracle.tcp_int8_payload(int(i), 5, w) for i, w in zip(ids, wire))
+    assert got8 == want8
+    log(f"frames dtype={dtype}: {len(got)} + {len(got8)} bytes byte-exact")

@@ -17,7 +17,7 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 SUITES = ["tests/test_host_allocator.py", "tests/test_oracle_attention.py", "tests/test_oracle_codecs.py",
-          "tests/test_oracle_kv_compress.py", "tests/test_golden_c1.py"]
+          "tests/test_oracle_kv_compress.py", "tests/test_golden_c1.py", "tests/test_wire_frames.py"]
 
 
 def _libasan():
