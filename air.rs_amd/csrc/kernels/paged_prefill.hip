@@ -35,8 +35,9 @@
 //                   leave ~1e-3 relative error at these lengths.
 //
 // K and V tiles are staged row-major in three LDS stages (1-byte codes
-// dequantized to bf16 on the way, exactly as the decode kernel does, and
-// their probabilities then take the hi bf16 half only); the V^T operand comes
+// dequantized on the way: keys as hi + lo bf16 halves that take two S^T
+// products, values as one bf16 rounding, whose probabilities then take the
+// hi bf16 half only); the V^T operand comes
 // from two transposing reads (ds_read_b64_tr_b16) per 16 keys.  The loop is
 // software-pipelined: the S^T product of tile t + 1 is issued before the
 // softmax and PV products of tile t, tile t + 2 is written to LDS after them,
@@ -163,6 +164,41 @@ __device__ __forceinline__ u32x4 to_bf16x8(const Raw8<DT> &r) {
             o[2 * h + 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2));
         }
         return o;
+    }
+}
+
+// Eight 1-byte codes dequantized as to_bf16x8 does, as hi + lo bf16 halves:
+// hi the bf16 rounding of the f32 value x, lo that of x - hi (exact in f32),
+// so hi + lo carries x to ~2^-17.
+template <int DT>
+__device__ __forceinline__ void to_bf16x8_split(const Raw8<DT> &r, u32x4 &hi, u32x4 &lo) {
+    if constexpr (DT == AIR_KV_BF16) {
+        hi = r.w;
+        lo = u32x4{0, 0, 0, 0};
+    } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t w = r.w[h];
+            f32x2 a, b;
+            if constexpr (DT == AIR_KV_INT8) {
+                const uint32_t u = w ^ 0x80808080u;
+                const float off = -128.0f * r.s;
+                a = f32x2{__builtin_fmaf((float)(u & 0xFFu), r.s, off),
+                          __builtin_fmaf((float)((u >> 8) & 0xFFu), r.s, off)};
+                b = f32x2{__builtin_fmaf((float)((u >> 16) & 0xFFu), r.s, off),
+                          __builtin_fmaf((float)(u >> 24), r.s, off)};
+            } else {
+                a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false) * r.s;
+                b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true) * r.s;
+            }
+            uint32_t h0, l0, h1, l1;
+            split_pair(a[0], a[1], h0, l0);
+            split_pair(b[0], b[1], h1, l1);
+            hi[2 * h] = h0;
+            lo[2 * h] = l0;
+            hi[2 * h + 1] = h1;
+            lo[2 * h + 1] = l1;
+        }
     }
 }
 
@@ -351,9 +387,25 @@ template <int N> struct Int { static constexpr int value = N; };
 // groups), V rows 320 bytes (rows start 16 banks apart, so the 4 rows x 64
 // bytes of a transposing read cover the 64 banks once).  Every LDS address
 // is then one per-lane register plus an immediate.
-constexpr int KPITCH = D * 2 + 16, VPITCH = D * 2 + 64;
-constexpr int KTILE_BYTES = kKeys * KPITCH, VTILE_BYTES = kKeys * VPITCH;
-constexpr int STAGE_BYTES = KTILE_BYTES + VTILE_BYTES;   // K then V
+//
+// 1-byte pages stage each dequantized key as two bf16 halves, hi + lo (hi the
+// bf16 rounding of code * scale, lo that of the remainder: ~16 significant
+// bits), in one 528-byte row (hi at 0, lo at 256; rows still 4 banks apart)
+// and take a second QK^T product with the lo half.  One bf16 rounding of the
+// keys moves logits by up to 2^-9 of each q_d * k_d term, which the outlier
+// channels of quantized caches (20x the others) turn into >2e-2 output
+// errors; the split leaves ~2^-17.  Three stages of the wider tile take
+// 81408 bytes: two workgroups still fit a CU's 160 KB.
+constexpr int VPITCH = D * 2 + 64;
+constexpr int VTILE_BYTES = kKeys * VPITCH;
+template <int DT> struct Lds {
+    static constexpr bool kSplitK = DT != AIR_KV_BF16;
+    static constexpr int KPITCH = D * 2 * (kSplitK ? 2 : 1) + 16;
+    static constexpr int KTILE_BYTES = kKeys * KPITCH;
+    static constexpr int STAGE_BYTES = KTILE_BYTES + VTILE_BYTES;   // K then V
+    static constexpr int BYTES = kStages * STAGE_BYTES;
+};
+static_assert(2 * Lds<AIR_KV_INT8>::BYTES <= 160 * 1024, "two workgroups per CU");
 
 
 template <int BS, bool QF32, int DT>
@@ -363,7 +415,10 @@ void prefill_pipe_kernel(PrefillArgs a) {
     // bf16 pages: P as hi + lo bf16 halves; 1-byte pages, whose V operand is
     // already a bf16 rounding of code * scale, take the hi half only
     constexpr bool kSplitP = DT == AIR_KV_BF16;
-    __shared__ __align__(16) uint8_t smem[kStages * STAGE_BYTES];
+    constexpr bool kSplitK = Lds<DT>::kSplitK;
+    constexpr int KPITCH = Lds<DT>::KPITCH, KTILE_BYTES = Lds<DT>::KTILE_BYTES;
+    constexpr int STAGE_BYTES = Lds<DT>::STAGE_BYTES;
+    __shared__ __align__(16) uint8_t smem[Lds<DT>::BYTES];
     static_assert(sizeof(smem) >= kRankLdsBytes, "dispatch ranking needs the tile LDS");
     const PrefillSlot sl = prefill_slot(a, reinterpret_cast<int *>(smem));
     const int b = sl.b, kh = sl.kh;
@@ -457,9 +512,10 @@ void prefill_pipe_kernel(PrefillArgs a) {
             }
             return;
         }
+        u32x4 kl[2];                              // lo halves of the keys
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            kb[i] = to_bf16x8<DT>(R.k[i]);
+            to_bf16x8_split<DT>(R.k[i], kb[i], kl[i]);
             vb[i] = to_bf16x8<DT>(R.v[i]);
         }
         if (!(R.ok0 && R.ok1 && R.kt + kKeys <= kend)) {
@@ -469,6 +525,7 @@ void prefill_pipe_kernel(PrefillArgs a) {
                 const bool okp = (BS == 16 && i == 1) ? R.ok1 : R.ok0;
                 const bool live = R.kt + (tid >> 4) + 16 * i < kend && okp;
                 kb[i] = live ? kb[i] : zero;
+                kl[i] = live ? kl[i] : zero;
                 vb[i] = live ? vb[i] : zero;
             }
         }
@@ -476,6 +533,7 @@ void prefill_pipe_kernel(PrefillArgs a) {
         for (int i = 0; i < 2; ++i) {
             const int row = (tid >> 4) + 16 * i;
             *reinterpret_cast<u32x4 *>(ks + row * KPITCH + (tid & 15) * 16) = kb[i];
+            *reinterpret_cast<u32x4 *>(ks + row * KPITCH + D * 2 + (tid & 15) * 16) = kl[i];
             *reinterpret_cast<u32x4 *>(vs + row * VPITCH + (tid & 15) * 16) = vb[i];
         }
     };
@@ -544,6 +602,11 @@ void prefill_pipe_kernel(PrefillArgs a) {
                 const u32x4 kA = *reinterpret_cast<const u32x4 *>(ks_ + r32 * KPITCH + (2 * ks + hh) * 16);
                 s = mfma32(kA, qhi[ks], s);
                 if constexpr (QF32) s = mfma32(kA, qlo[ks], s);
+                if constexpr (kSplitK) {
+                    const u32x4 kL =
+                        *reinterpret_cast<const u32x4 *>(ks_ + r32 * KPITCH + D * 2 + (2 * ks + hh) * 16);
+                    s = mfma32(kL, qhi[ks], s);
+                }
             }
             return s;
         };
@@ -647,11 +710,12 @@ void prefill_pipe_kernel(PrefillArgs a) {
             softmax_head(t, s_cur);
             s_next = qk((S + 1) % kStages);
             softmax_pv(S, s_cur);
+            constexpr int kQk = kSplitK ? 16 : 8;      // K operand reads per tile
             __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < kQk; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 48 / kQk, 0);
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
             constexpr int kPv = kSplitP ? 16 : 8;      // PV products per tile

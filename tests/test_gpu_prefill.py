@@ -204,6 +204,62 @@ def test_prefill_full_c5_shape_vs_torch_fp32():
     assert worst <= 1e-3
 
 
+@pytest.mark.parametrize("dtype,bs", [(airkv.INT8, 16), (airkv.FP8, 32)])
+def test_prefill_full_70b_geometry_quantized_vs_torch_fp32(dtype, bs):
+    """Quantized pages at the configs[2] / configs[3] head geometry (64 q /
+    8 kv, d 128) with 1% of channels x20: eight sequences of 8192 cached
+    tokens whose last 512 are the chunk, against a float32 torch causal
+    attention over the dequantized cache (the D3 comparison), tolerance 2e-2."""
+    torch = torch_mod()
+    NQ, NKV, D, L, C = 64, 8, 128, 8192, 512
+    cfg = workloads.Config("p70b", NQ, NKV, D, bs, dtype, 8)
+    w = workloads.build_prefill_decode(cfg, [L] * 8, 95, decode_steps=0)
+    outl = workloads.outlier_channels(NKV, D, seed=3)
+    gen = workloads.kv_rows(10 ** 12, NKV, D, seed=96, device="cuda", chunk_rows=1 << 16, outliers=outl)
+    pool = device_pool_for(w)
+    for slots in w.batches:
+        st = torch.from_numpy(slots).cuda()
+        done = 0
+        while done < len(slots):
+            k, v = next(gen)
+            n = min(len(slots) - done, k.shape[0])
+            pool.append(k[:n].contiguous(), v[:n].contiguous(), st[done:done + n].contiguous())
+            done += n
+    tables, lens = w.tables()
+    cu = np.arange(9, dtype=np.int32) * C
+    g = torch.Generator(device="cuda")
+    g.manual_seed(97)
+    q = torch.randn((8 * C, NQ, D), generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty((8 * C, NQ, D), device="cuda")
+    tt, lt = torch.from_numpy(tables).cuda(), torch.from_numpy(lens).cuda()
+    pool.paged_prefill(q, torch.from_numpy(cu).cuda(), tt, lt, out, max_q_len=C)
+    offs = np.zeros(9, np.int64)
+    offs[1:] = np.cumsum(np.array(lens, np.int64) * NKV * D)
+    gk = torch.empty(int(offs[-1]), device="cuda")
+    gv = torch.empty_like(gk)
+    pool.gather(tt, lt, torch.from_numpy(offs[:-1]).cuda(), gk, gv, out_dtype=airkv.F32,
+                layout=airkv.LAYOUT_TOKEN_MAJOR)
+    assert pool.error_count() == 0
+    torch.backends.cuda.matmul.allow_tf32 = False
+    worst = 0.0
+    grp = NQ // NKV
+    for b in range(8):
+        kb = gk[offs[b]:offs[b + 1]].view(L, NKV, D).permute(1, 0, 2).contiguous()
+        vb = gv[offs[b]:offs[b + 1]].view(L, NKV, D).permute(1, 0, 2).contiguous()
+        qb = q[C * b:C * (b + 1)].float().permute(1, 0, 2).contiguous()            # [NQ][C][D]
+        kr = kb.repeat_interleave(grp, dim=0)
+        vr = vb.repeat_interleave(grp, dim=0)
+        s = torch.bmm(qb, kr.transpose(1, 2).contiguous()) / np.sqrt(float(D))
+        qpos = torch.arange(L - C, L, device="cuda")[:, None]
+        kpos = torch.arange(L, device="cuda")[None, :]
+        s = s.masked_fill(kpos > qpos, float("-inf"))
+        ref = torch.bmm(torch.softmax(s, dim=-1), vr).permute(1, 0, 2)
+        got = out[C * b:C * (b + 1)]
+        worst = max(worst, float((got - ref).abs().max() / ref.abs().max()))
+    log(f"prefill 70B geometry dtype={dtype} bs={bs}: worst rel err {worst:.2e}")
+    assert worst <= 2e-2
+
+
 def test_prefill_invalid_sequences_counted_and_zeroed():
     """A chunk longer than its sequence and an out-of-range seq_len are
     counted and their rows zero-filled; the valid sequence is unaffected; an
