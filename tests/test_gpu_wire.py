@@ -84,6 +84,39 @@ def test_pack_blocks_int8_bitexact(dtype):
         assert np.array_equal(codes[i].cpu().numpy(), want_q)
 
 
+def test_pack_blocks_int8_bf16_special_blocks():
+    """The fused int8 pack of a bf16 pool on blocks with the edge cases of
+    KvBlock::int8_quantize: all zeros, NaN elements, an infinity, a subnormal
+    absmax, .5 ties of x * inv, signed zeros, and random blocks, taken by more
+    blocks than the kernel's persistent workgroups so each one runs several
+    blocks in a row.  Codes and scales equal the oracle's quantization of the
+    expected wire blocks."""
+    torch = torch_mod()
+    nb = 600
+    pool = airkv.KvPool(nb, BS, NKV, D, airkv.BF16)
+    rng = np.random.default_rng(61)
+    f = (rng.standard_normal((nb, 2, NKV, BS, D)) * 3).astype(np.float32)
+    f[1] = 0.0
+    f[2].reshape(-1)[::97] = np.nan
+    f[3].reshape(-1)[1234] = np.inf
+    f[4] = f[4] * np.float32(1e-39)                             # subnormal absmax
+    f[5] = (np.float32(127.0) * np.linspace(-1, 1, f[5].size, dtype=np.float32)).reshape(f[5].shape)
+    f[6] = -0.0
+    f[7].reshape(-1)[::5] = -np.inf
+    raw = oracle.bf16_from_f32(f.reshape(-1)).reshape(nb, -1)
+    pool.write_blocks(np.arange(nb, dtype=np.int32), raw.view(np.uint8))
+    ids = np.concatenate([np.arange(1, 8), rng.permutation(nb)]).astype(np.int32)
+    codes, scales = pool.pack_blocks_int8(torch.from_numpy(ids).cuda())
+    torch.cuda.synchronize()
+    want_wire = _expected_wire(pool, ids)
+    got_c, got_s = codes.cpu().numpy(), scales.cpu().numpy()
+    for i in range(len(ids)):
+        want_q, want_s = oracle.pd_int8_quantize(want_wire[i])
+        assert got_s[i].view(np.uint32) == np.float32(want_s).view(np.uint32), (i, ids[i])
+        assert np.array_equal(got_c[i], want_q), (i, ids[i])
+    assert pool.error_count() == 0
+
+
 def test_wire_int8_quantize_special_blocks():
     """Whole wire buffers with the edge cases of the reference arithmetic:
     an all-zero block (scale 1.0, codes 0), NaN elements (ignored by the
@@ -136,6 +169,43 @@ def test_unpack_blocks_matches_oracle_append(dtype):
     if host.k_scales is not None:
         assert_bits_equal(gks, host.k_scales, "unpack K scales")
         assert_bits_equal(gvs, host.v_scales, "unpack V scales")
+
+
+@pytest.mark.parametrize("geom", [(16, 8, 128), (32, 3, 64), (16, 5, 32)])
+def test_bf16_special_bits_and_geometries(geom):
+    """bf16 pools of several geometries (head counts that are not powers of
+    two, head_dim 32..128) whose pages hold the special bit patterns:
+    signalling and quiet NaNs of both signs, infinities, signed zeros,
+    subnormals and the largest finite values.  pack gives bf16_from_f32 of
+    each page element (a signalling NaN gains its quiet bit, everything else
+    keeps its bits) in the wire layout; unpack of that wire into other blocks
+    gives the same bits back in the pages."""
+    torch = torch_mod()
+    bs, nkv, d = geom
+    nb = 12
+    pool = airkv.KvPool(nb, bs, nkv, d, airkv.BF16)
+    rng = np.random.default_rng(40 + nkv)
+    raw = rng.integers(0, 1 << 16, size=(nb, 2, nkv, bs, d), dtype=np.uint16)
+    special = np.array([0x7F81, 0xFF81, 0x7FC1, 0xFFC0, 0x7F80, 0xFF80, 0x0000, 0x8000, 0x0001, 0x807F,
+                        0x7F7F, 0xFF7F, 0x7FFF, 0xFFFF], np.uint16)
+    flat = raw.reshape(-1)
+    flat[rng.choice(flat.size, size=4 * special.size, replace=False)] = np.tile(special, 4)
+    pool.write_blocks(np.arange(nb, dtype=np.int32), raw.reshape(nb, -1).view(np.uint8))
+    src = np.array([3, 0, 7, 11], np.int32)
+    wire = pool.pack_blocks(torch.from_numpy(src).cuda())
+    torch.cuda.synchronize()
+    k, v = raw[src, 0], raw[src, 1]                                     # [n][h][t][d]
+    kv = np.stack([k.transpose(0, 2, 1, 3), v.transpose(0, 2, 1, 3)], axis=-1)
+    want = oracle.bf16_from_f32(oracle.bf16_to_f32(kv.reshape(-1))).reshape(len(src), -1)
+    assert_bits_equal(wire.cpu().numpy().view(np.uint16).reshape(len(src), -1), want, f"pack {geom}")
+    dst = np.array([5, 6, 8, 9], np.int32)
+    pool.unpack_blocks(torch.from_numpy(dst).cuda(), wire)
+    gk, gv, _, _ = pool.snapshot()
+    quiet = oracle.bf16_from_f32(oracle.bf16_to_f32(raw.reshape(-1))).reshape(raw.shape)
+    assert_bits_equal(gk[dst].view(np.uint16), quiet[src, 0], f"unpack K {geom}")
+    assert_bits_equal(gv[dst].view(np.uint16), quiet[src, 1], f"unpack V {geom}")
+    assert_bits_equal(gk[[1, 2, 4, 10]].view(np.uint16), raw[[1, 2, 4, 10], 0], "untouched blocks")
+    assert pool.error_count() == 0
 
 
 def test_bf16_roundtrip_and_bad_ids():
