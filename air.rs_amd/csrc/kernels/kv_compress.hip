@@ -217,6 +217,7 @@ __global__ __launch_bounds__(kThreads) void key_compress_staged_kernel(CompressA
 #pragma unroll
                 for (int j = 0; j < 4; ++j) raw[(p * PB + 16 * ch) / 4 + j] = v[j];
             }
+            __builtin_amdgcn_sched_barrier(0);           // one pass's chunks live at a time
         }
         if (r >= a.n_rows) continue;
         if (!live && a.errors && (r % a.src.rows_per_block) == 0) atomicAdd(a.errors, 1ull);
@@ -249,6 +250,9 @@ __global__ __launch_bounds__(kThreads) void key_compress_staged_kernel(CompressA
                 const float q = x * x;
                 s += x;
                 ss += q;
+                // the folds are sequential: hoisting the products far ahead
+                // only holds them in registers (and halves the waves per SIMD)
+                if (j % 8 == 7) __builtin_amdgcn_sched_barrier(0);
             }
             mean = s / (float)D;
             mag = sqrtf(ss);
@@ -258,9 +262,19 @@ __global__ __launch_bounds__(kThreads) void key_compress_staged_kernel(CompressA
 #pragma unroll
             for (int w = 0; w < W; ++w) {
                 uint64_t word = 0;
+                // bit j = (x_j >= mean) (:95-100), each 32-bit half built from
+                // its top bit down: shift-or, no per-bit mask constants
 #pragma unroll
-                for (int j = 0; j < 64 && 64 * w + j < D; ++j)
-                    word |= (uint64_t)(xv(64 * w + j) >= mean) << j;   // (:95-100)
+                for (int h = 1; h >= 0; --h) {
+                    uint32_t half = 0;
+#pragma unroll
+                    for (int j = 31; j >= 0; --j) {
+                        const int e = 64 * w + 32 * h + j;
+                        if (e < D) half = (half << 1) | (uint32_t)(xv(e) >= mean);
+                        if (j % 8 == 0) __builtin_amdgcn_sched_barrier(0);
+                    }
+                    word = (word << 32) | half;
+                }
                 bits[w] = word;
             }
         }
@@ -347,12 +361,13 @@ __global__ __launch_bounds__(kThreads) void value_compress_kernel(CompressArgs a
             // infinite scale, i.e. tiny or non-finite data) divide exactly.
             const float y = 1.0f / scale;
             if (__builtin_isnormal(scale) && __builtin_isnormal(y)) {
-                // d = v - min >= 0 (or NaN) here, so round half away from
-                // zero is floor(quo + 0.5) for quo >= 0.5 (checked against
-                // exact rounding for every float in [0.5, 300)) and 0 below;
-                // the only float below 0.5 where the sum rounds up to 1 is
-                // 0.5 - 2^-25.  max(., 0) sends NaN to 0 (`as u8`), min(., 255)
-                // clamps.
+                // d = v - min >= 0 (or NaN) here.  max(., 0) sends NaN to 0
+                // (`as u8`) and min(., 255) clamps; on [0, 255] round half away
+                // from zero is the truncation of quo + (0.5 - 2^-25): the sum
+                // reaches the next integer exactly when quo reaches the half
+                // (ties land on it, anything below stays an ulp short), and
+                // below 0.5 it stays under 1 (0.5 itself would round 0.5 - 2^-25
+                // up to 1).
 #pragma unroll
                 for (int j4 = 0; j4 < N / 4; ++j4) {
                     uint32_t w = 0;
@@ -362,9 +377,8 @@ __global__ __launch_bounds__(kThreads) void value_compress_kernel(CompressArgs a
                         const float q0 = d * y;
                         const float rem = __builtin_fmaf(-q0, scale, d);
                         const float quo = __builtin_fmaf(rem, y, q0);
-                        float rq = quo < 0.5f ? 0.0f : __builtin_floorf(quo + 0.5f);
-                        rq = __builtin_fminf(__builtin_fmaxf(rq, 0.0f), 255.0f);
-                        w |= (uint32_t)rq << (8 * k);
+                        const float cq = __builtin_fminf(__builtin_fmaxf(quo, 0.0f), 255.0f);
+                        w |= (uint32_t)(cq + 0.49999997f) << (8 * k);
                     }
                     q[j4] = w;
                 }
