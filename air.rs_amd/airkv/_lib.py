@@ -108,7 +108,8 @@ SIGNATURES = {
     "air_paged_decode_noalloc": (_int, [_P, _P, _P, _i32, _i32, _P, _P, _i32, _i32, ctypes.c_float, _i32,
                                         _P, _i32]),
     "air_paged_prefill": (_int, [_P, _P, _P, _i32, _i32, _P, _i32, _i32, _P, _P, _i32, _i32,
-                                 ctypes.c_float, _P, _i32]),
+                                 ctypes.c_float, _P, _SZ, _P, _i32]),
+    "air_paged_prefill_workspace_size": (_int, [_P, _i32, _i32, _i32, ctypes.POINTER(_SZ)]),
     "air_kv_session_create": (_int, [_P, ctypes.POINTER(_P), _i32, ctypes.POINTER(_P)]),
     "air_kv_session_destroy": (_int, [_P]),
     "air_kv_session_fork": (_int, [_P, ctypes.POINTER(_P)]),

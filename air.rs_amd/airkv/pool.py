@@ -189,7 +189,16 @@ class KvPool:
                 _lib.check(rc, "air_paged_decode")
         return launch
 
-    def _prefill_args(self, q, cu_q, block_tables, seq_lens, out, max_q_len, scale, stream):
+    def prefill_workspace_size(self, n_q_heads, batch, max_q_len):
+        """Bytes of the key-split workspace air_paged_prefill takes for this shape."""
+        n = ctypes.c_size_t(0)
+        _lib.check(_lib.load().air_paged_prefill_workspace_size(self.handle, n_q_heads, batch, max_q_len,
+                                                                ctypes.byref(n)),
+                   "air_paged_prefill_workspace_size")
+        return n.value
+
+    def _prefill_args(self, q, cu_q, block_tables, seq_lens, out, max_q_len, scale, stream, workspace,
+                      split):
         torch = _torch()
         total_q, n_q, d = q.shape
         if d != self.head_dim:
@@ -211,25 +220,38 @@ class KvPool:
             scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
         qdt = F32 if q.dtype == torch.float32 else BF16
         odt = F32 if out.dtype == torch.float32 else BF16
+        if split and workspace is None and batch:
+            n = self.prefill_workspace_size(n_q, batch, max_q_len)
+            if n:
+                workspace = torch.empty(n, dtype=torch.uint8, device="cuda")
+        if not split:
+            workspace = None
+        ws_ptr = ctypes.c_void_p(workspace.data_ptr()) if workspace is not None else None
+        ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+        # the workspace tensor rides along in the tuple so a bound launcher keeps it alive
         return (self.handle, _stream_ptr(stream), ctypes.c_void_p(q.data_ptr()), qdt, n_q,
                 ctypes.c_void_p(cu_q.data_ptr()), total_q, max_q_len,
                 ctypes.c_void_p(block_tables.data_ptr()), ctypes.c_void_p(seq_lens.data_ptr()), batch,
-                block_tables.shape[1], scale, ctypes.c_void_p(out.data_ptr()), odt)
+                block_tables.shape[1], scale, ws_ptr, ws_bytes, ctypes.c_void_p(out.data_ptr()), odt), workspace
 
     def paged_prefill(self, q, cu_q, block_tables, seq_lens, out, max_q_len=None, scale=None,
-                      stream=None):
+                      stream=None, workspace=None, split=True):
         """Causal attention of each sequence's newest cu_q[b+1] - cu_q[b]
         tokens over its pages (air_paged_prefill).  q / out: [total_q][n_q][d];
         cu_q int32 [batch + 1]; max_q_len defaults to the largest q_len (read
-        back from cu_q, which synchronises)."""
-        args = self._prefill_args(q, cu_q, block_tables, seq_lens, out, max_q_len, scale, stream)
+        back from cu_q, which synchronises).  With split (the default) long
+        work groups' keys are cut over several workgroups through a workspace
+        (allocated here when none is given); split=False passes none."""
+        args, _ws = self._prefill_args(q, cu_q, block_tables, seq_lens, out, max_q_len, scale, stream,
+                                       workspace, split)
         _lib.check(_lib.load().air_paged_prefill(*args), "air_paged_prefill")
         return out
 
     def bind_prefill(self, q, cu_q, block_tables, seq_lens, out, max_q_len=None, scale=None,
-                     stream=None):
+                     stream=None, workspace=None, split=True):
         """Validate once, return a zero-argument prefill launcher."""
-        args = self._prefill_args(q, cu_q, block_tables, seq_lens, out, max_q_len, scale, stream)
+        args, ws = self._prefill_args(q, cu_q, block_tables, seq_lens, out, max_q_len, scale, stream,
+                                      workspace, split)
         fn = _lib.load().air_paged_prefill
         _lib.check(fn(*args), "air_paged_prefill")
 
@@ -237,6 +259,7 @@ class KvPool:
             rc = fn(*args)
             if rc:
                 _lib.check(rc, "air_paged_prefill")
+        launch.workspace = ws
         return launch
 
     def bind_append(self, k, v, slot_mapping, stream=None):

@@ -48,6 +48,7 @@
 // (stale page bytes may hold non-finite values).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 
 #include "../host/status.hpp"
@@ -203,21 +204,35 @@ __device__ __forceinline__ void to_bf16x8_split(const Raw8<DT> &r, u32x4 &hi, u3
 }
 
 // Dispatch order.  The grid is one-dimensional: n_kv_heads workgroups for
-// each of the batch * nz (sequence, slot) items, and the hardware starts
-// workgroups in index order.  Slot z of sequence b serves that sequence's
-// work group n_wg - 1 - z (and every nz-th one below it), whose heaviest wave
-// needs the keys up to its last query row.  Grid row r takes the item of
-// rank r when items are ordered by that key count, decreasing (in buckets of
-// an eighth of an octave; ties by sequence, then slot), so long work starts
-// first and short work fills the launch's tail.  Every item gets exactly one
-// rank whatever the lengths hold.  Batches above kRankCap sequences or
-// kRankItems items are taken slot by slot (slot slowest), without ranking.
+// each of the batch * nz * ns_max (sequence, slot, piece) items, and the
+// hardware starts workgroups in index order.  Slot z of sequence b serves
+// that sequence's work group n_wg - 1 - z (and every nz-th one below it),
+// whose heaviest wave needs the keys up to its last query row.
+//
+// Key split.  With a workspace (ns_max > 1), a slot that serves a single
+// work group longer than the balanced load -- the batch's key tiles over the
+// grid's resident workgroup slots, a.slots -- has its key tiles cut into
+// ns = min(ns_max, ceil(tiles / T)) consecutive ranges, piece p taking range
+// p; the pieces write unnormalised partial outputs (acc, running max, sum)
+// to the workspace and prefill_merge_kernel combines them by log-sum-exp.
+// Split slots get ordinals in index order; when more slots are that long
+// than the workspace holds, T is raised until they fit.  Every workgroup
+// derives the same T, pieces and ordinals from the lengths.
+//
+// Ranking.  Grid row r takes the item of rank r when items are ordered by
+// the keys of their heaviest wave (a piece: its share), decreasing (in
+// buckets of an eighth of an octave; ties by sequence, slot, piece), so long
+// work starts first and short work fills the launch's tail.  Every item
+// gets exactly one rank whatever the lengths hold.  Batches above kRankCap
+// sequences or kRankItems items are taken slot by slot (slot slowest),
+// without ranking or splitting.
 constexpr int kRankCap = 2048;
 constexpr int kRankItems = 64 * kThreads;
-constexpr int kRankLdsBytes = (kThreads + kWaves + 2 + 2 * kRankCap) * 4;
+constexpr int kRankLdsBytes = (kThreads + kWaves + 8 + 2 * kRankCap) * 4;
 
 struct PrefillSlot {
     int b, kh, z, nz;
+    int p, ns, ord;            // piece, pieces of the slot (1: not split), split ordinal (-1: none)
 };
 
 __device__ __forceinline__ int len_bucket(int64_t len) {   // 0 .. 248, monotone in len
@@ -258,14 +273,48 @@ __device__ __forceinline__ int64_t slot_keys(int64_t len, int64_t qlen, int G, i
     return len - qlen + (rows < qlen ? rows : qlen);
 }
 
-// lds: at least kThreads + kWaves + 2 + 2 * kRankCap ints, free for the duration.
+// Whether slot z of a sequence serves exactly one work group (splittable).
+__device__ __forceinline__ bool single_unit(int64_t qlen, int G, int nz) {
+    const int64_t n_items = (qlen + kRows - 1) / kRows * G;
+    return (n_items + kWaves - 1) / kWaves <= nz;
+}
+
+__device__ __forceinline__ int slot_pieces(int64_t tiles, int64_t T, int ns_max) {
+    if (tiles <= T) return 1;
+    const int64_t n = (tiles + T - 1) / T;
+    return (int)(n < ns_max ? n : ns_max);
+}
+
+// The plan of a split launch: one int2 per grid row {item, slot info}.
+__device__ __forceinline__ int2 *prefill_plan_table(const PrefillArgs &a) {
+    return reinterpret_cast<int2 *>((uint8_t *)a.ws + 64 + 16 * (int64_t)a.ws_units);
+}
+
+// Split launches (ns_max > 1) read their item from the plan that
+// prefill_plan_kernel wrote to the workspace; others rank in every
+// workgroup.  lds: at least kThreads + kWaves + 8 + 2 * kRankCap ints, free
+// for the duration.
 __device__ PrefillSlot prefill_slot(const PrefillArgs &a, int *lds) {
     const int tid = threadIdx.x;
-    const int nz = (int)(gridDim.x / ((unsigned)a.batch * (unsigned)a.n_kv_heads));
+    const int nz = a.nz, nsm = a.ns_max;
     const int row = (int)(blockIdx.x / (unsigned)a.n_kv_heads);
     PrefillSlot sl;
     sl.kh = (int)(blockIdx.x % (unsigned)a.n_kv_heads);
     sl.nz = nz;
+    sl.p = 0;
+    sl.ns = 1;
+    sl.ord = -1;
+    if (nsm > 1) {
+        const int2 e = prefill_plan_table(a)[row];
+        const int si = e.x / nsm;
+        sl.p = e.x - si * nsm;
+        sl.b = si / nz;
+        sl.z = si - sl.b * nz;
+        sl.ns = e.y & 15;
+        sl.ord = (e.y >> 4) - 1;
+        if (sl.p >= sl.ns) sl.b = -1;                   // no such piece: the workgroup exits
+        return sl;
+    }
     if (a.batch == 1 || a.batch > kRankCap || (int64_t)a.batch * nz > kRankItems) {
         // (one sequence: its slots are already in decreasing order)
         sl.b = row % a.batch;
@@ -273,7 +322,7 @@ __device__ PrefillSlot prefill_slot(const PrefillArgs &a, int *lds) {
         return sl;
     }
     int *hist = lds, *wsum = lds + kThreads, *sel = lds + kThreads + kWaves;
-    int *slen = sel + 2, *sq = slen + kRankCap;
+    int *slen = sel + 8, *sq = slen + kRankCap;
     hist[tid] = 0;
     for (int i = tid; i < a.batch; i += kThreads) {
         slen[i] = a.lens[i];
@@ -317,6 +366,121 @@ __device__ PrefillSlot prefill_slot(const PrefillArgs &a, int *lds) {
     return sl;
 }
 
+// The plan of a split launch, once per launch (one workgroup of 1024
+// threads): the split threshold T and each slot's pieces and ordinal (as
+// above), every (sequence, slot, piece) item's rank by the keys of its
+// heaviest wave (its share for a piece), decreasing in buckets of an eighth
+// of an octave -- the order within a bucket is free, any order covers each
+// item once -- and the descriptors of the split slots for the merge.
+constexpr int kPlanThreads = 1024;
+
+__device__ __forceinline__ int plan_scan(int v, int *red, int &total) {   // exclusive, 1024 threads
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
+    }
+    if (lane == 63) red[wave] = incl;
+    __syncthreads();
+    int base = 0, tot = 0;
+    for (int w = 0; w < kPlanThreads / 64; ++w) {
+        base += w < wave ? red[w] : 0;
+        tot += red[w];
+    }
+    __syncthreads();
+    total = tot;
+    return base + incl - v;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillArgs a) {
+    __shared__ int slen[kRankCap], sq[kRankCap];
+    __shared__ int info[kRankItems / 2];               // per slot: pieces | (ordinal + 1) << 4
+    __shared__ int hist[256], cnt[256], red[kPlanThreads / 64];
+    const int tid = threadIdx.x;
+    const int nz = a.nz, nsm = a.ns_max;
+    for (int i = tid; i < a.batch; i += kPlanThreads) {
+        slen[i] = a.lens[i];
+        const int64_t ql = (int64_t)a.cu_q[i + 1] - a.cu_q[i];
+        sq[i] = ql < 0 ? 0 : ql > 0x7fffffff ? 0x7fffffff : (int)ql;
+    }
+    if (tid < 256) hist[tid] = cnt[tid] = 0;
+    __syncthreads();
+    const int n_slots = a.batch * nz;
+    auto tiles_of = [&](int si) -> int64_t {
+        const int bb = si / nz;
+        return (slot_keys(slen[bb], sq[bb], a.group, si - bb * nz) + kKeys - 1) / kKeys;
+    };
+    auto splittable = [&](int si) { return single_unit(sq[si / nz], a.group, nz); };
+    // T: the balanced load (clamped terms: a balance target only), raised
+    // until the split slots fit the workspace
+    int part = 0, tot = 0;
+    for (int si = tid; si < n_slots; si += kPlanThreads) {
+        const int64_t t = tiles_of(si);
+        part += (int)(t < (1 << 16) ? t : (1 << 16));
+    }
+    (void)plan_scan(part, red, tot);
+    int64_t T = ((int64_t)tot * a.n_kv_heads + a.slots - 1) / a.slots;
+    T = T < 8 ? 8 : T;                                  // pieces of at least 8 tiles
+    for (;;) {
+        int c = 0, n = 0;
+        for (int si = tid; si < n_slots; si += kPlanThreads) c += splittable(si) && tiles_of(si) > T;
+        (void)plan_scan(c, red, n);
+        if (n <= a.ws_units) break;
+        T += (T >> 2) + 1;
+    }
+    // pieces and ordinals (index order) of the slots: thread t owns a chunk
+    const int chunk = (n_slots + kPlanThreads - 1) / kPlanThreads;
+    const int s0 = tid * chunk, s1 = s0 + chunk < n_slots ? s0 + chunk : n_slots;
+    int nsplit = 0;
+    for (int si = s0; si < s1; ++si) {
+        const int64_t t = tiles_of(si);
+        const int ns = splittable(si) ? slot_pieces(t, T, nsm) : 1;
+        info[si] = ns;
+        nsplit += ns > 1;
+    }
+    int n_split = 0;
+    int ord = plan_scan(nsplit, red, n_split);
+    int32_t *hdr = reinterpret_cast<int32_t *>(a.ws);
+    for (int si = s0; si < s1; ++si) {
+        if (info[si] > 1) {
+            int32_t *d = hdr + 16 + 4 * ord;
+            d[0] = si / nz;
+            d[1] = si % nz;
+            d[2] = info[si];
+            info[si] |= (ord + 1) << 4;
+            ++ord;
+        }
+    }
+    if (tid == 0) hdr[0] = n_split;
+    __syncthreads();
+    // rank every item: bucket histogram, descending starts, placement
+    const int n_it = n_slots * nsm;
+    auto bucket_of = [&](int i) {
+        const int si = i / nsm, pp = i - si * nsm;
+        const int ns = info[si] & 15;
+        if (pp >= ns) return 0;
+        if (ns == 1) {
+            const int bb = si / nz;
+            return len_bucket(slot_keys(slen[bb], sq[bb], a.group, si - bb * nz));
+        }
+        return len_bucket((tiles_of(si) + ns - 1) / ns * kKeys);
+    };
+    for (int i = tid; i < n_it; i += kPlanThreads) atomicAdd(&hist[bucket_of(i)], 1);
+    __syncthreads();
+    const int bk = tid < 256 ? 255 - tid : 0;           // thread t: bucket 255 - t (decreasing)
+    int all = 0;
+    const int st = plan_scan(tid < 256 ? hist[bk] : 0, red, all);
+    if (tid < 256) cnt[bk] = st;
+    __syncthreads();
+    int2 *plan = prefill_plan_table(a);
+    for (int i = tid; i < n_it; i += kPlanThreads) {
+        const int r = atomicAdd(&cnt[bucket_of(i)], 1);
+        plan[r] = int2{i, info[i / nsm]};
+    }
+}
+
 // Per-(sequence, kv head) setup shared by the prefill kernels: reads the
 // sequence's rows and length, counts (once) an inconsistent sequence and
 // every out-of-pool table entry within its length, zero-fills the rows of an
@@ -334,7 +498,7 @@ __device__ bool prefill_begin(const PrefillArgs &a, const PrefillSlot &sl, int32
     const bool rows_ok = q0 >= 0 && q1 >= q0 && q1 <= a.total_q;
     const bool seq_ok = rows_ok && len >= 0 && len <= max_len && qlen <= len;
     const int32_t *tbl = a.tables + (int64_t)b * a.max_blocks;
-    if (sl.z == 0 && kh == 0) {
+    if (sl.z == 0 && sl.p == 0 && kh == 0) {
         if (!seq_ok) {
             if (tid == 0) atomicAdd(a.errors, 1ull);
         } else if (qlen > 0) {
@@ -346,7 +510,7 @@ __device__ bool prefill_begin(const PrefillArgs &a, const PrefillSlot &sl, int32
     }
     if (!seq_ok) {
         // rows of a sequence whose lengths are inconsistent become zeros
-        if (rows_ok && sl.z == 0) {
+        if (rows_ok && sl.z == 0 && sl.p == 0) {
             const int64_t n = (int64_t)qlen * G * D;
             for (int64_t i = tid; i < n; i += kThreads) {
                 const int64_t r = i / (G * D), e = i % (G * D);
@@ -408,6 +572,90 @@ template <int DT> struct Lds {
 static_assert(2 * Lds<AIR_KV_INT8>::BYTES <= 160 * 1024, "two workgroups per CU");
 
 
+// Partial output of piece p of split slot `ord`, kv head kh (layout in
+// prefill_common.hpp).
+__device__ __forceinline__ uint8_t *piece_base(const PrefillArgs &a, int ord, int kh, int p) {
+    return (uint8_t *)a.ws + prefill_ws_header(a.ws_units, (int64_t)a.batch * a.nz * a.ns_max) +
+           (((int64_t)ord * a.n_kv_heads + kh) * a.ns_max + p) * kPrefillPieceBytes;
+}
+__device__ __forceinline__ f32x4 *piece_acc(const PrefillArgs &a, int ord, int kh, int p, int wave) {
+    return reinterpret_cast<f32x4 *>(piece_base(a, ord, kh, p)) + wave * 16 * 64;
+}
+__device__ __forceinline__ float *piece_ml(const PrefillArgs &a, int ord, int kh, int p) {
+    return reinterpret_cast<float *>(piece_base(a, ord, kh, p) + kPrefillPieceAccBytes);
+}
+
+// One lane's 64 outputs (acc * inv) of query row r32, head_dim 32 n + 8 i4 +
+// 4 hh + 0..3 (acc[n][4 * i4 .. + 4]), as out_dtype.
+__device__ __forceinline__ void store_out(const PrefillArgs &a, const f32x16 (&acc)[D / 32], float inv,
+                                          int64_t orow) {
+    if (a.out_dtype == AIR_KV_F32) {
+#pragma unroll
+        for (int n = 0; n < D / 32; ++n)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4)
+                *reinterpret_cast<f32x4 *>((float *)a.out + orow + 32 * n + 8 * i4) =
+                    f32x4{acc[n][4 * i4], acc[n][4 * i4 + 1], acc[n][4 * i4 + 2], acc[n][4 * i4 + 3]} * inv;
+    } else {
+#pragma unroll
+        for (int n = 0; n < D / 32; ++n)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const f32x2 x = f32x2{acc[n][4 * i4], acc[n][4 * i4 + 1]} * inv;
+                const f32x2 y = f32x2{acc[n][4 * i4 + 2], acc[n][4 * i4 + 3]} * inv;
+                *reinterpret_cast<u32x2 *>((uint16_t *)a.out + orow + 32 * n + 8 * i4) =
+                    u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2)),
+                          __builtin_bit_cast(uint32_t, __builtin_convertvector(y, bf16x2))};
+            }
+    }
+}
+
+// Log-sum-exp merge of the pieces of split slot blockIdx.x / n_kv_heads, kv
+// head blockIdx.x % n_kv_heads: lane for lane the partials the pieces wrote,
+// weighted by 2^(m_p - max m), then divided by the weighted sum of the sums
+// (the two lane halves of a query row hold halves of its keys).
+__global__ __launch_bounds__(kThreads) void prefill_merge_kernel(PrefillArgs a) {
+    const int ord = (int)(blockIdx.x / (unsigned)a.n_kv_heads), kh = (int)(blockIdx.x % (unsigned)a.n_kv_heads);
+    const int32_t *hdr = (const int32_t *)a.ws;
+    if (ord >= hdr[0] || ord >= a.ws_units) return;
+    const int32_t *d = hdr + 16 + 4 * ord;
+    const int b = d[0], z = d[1], ns = d[2];
+    if (b < 0 || b >= a.batch || z < 0 || z >= a.nz || ns < 2 || ns > a.ns_max) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = a.group;
+    const int32_t q0 = a.cu_q[b];
+    const int qlen = a.cu_q[b + 1] - q0;
+    const int n_items = (qlen + kRows - 1) / kRows * G;
+    const int n_wg = (n_items + kWaves - 1) / kWaves;
+    const int item = (n_wg - 1 - z) * kWaves + wave;
+    if (item >= n_items) return;                        // uniform per wave
+    const int tb = item / G, h = kh * G + item % G, r0 = tb * kRows;
+    const int r32 = lane & 31, hh = lane >> 5;
+    float M = -INFINITY;
+    for (int p = 0; p < ns; ++p) M = fmaxf(M, piece_ml(a, ord, kh, p)[wave * 64 + lane]);
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int n = 0; n < D / 32; ++n)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[n][i] = 0.0f;
+    float L = 0.0f;
+    for (int p = 0; p < ns; ++p) {
+        const float *ml = piece_ml(a, ord, kh, p);
+        const float w = __builtin_amdgcn_exp2f(ml[wave * 64 + lane] - M);   // a piece with no visible key: 0
+        L += ml[kThreads + wave * 64 + lane] * w;
+        const f32x4 *pa = piece_acc(a, ord, kh, p, wave);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const f32x4 v = pa[q * 64 + lane] * w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[q / 4][4 * (q % 4) + e] += v[e];
+        }
+    }
+    L += __shfl_xor(L, 32);
+    if (r0 + r32 < qlen)
+        store_out(a, o, 1.0f / L, ((int64_t)(q0 + r0 + r32) * a.n_q_heads + h) * D + 4 * hh);
+}
+
 template <int BS, bool QF32, int DT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AIRKV_PREFILL_WAVES_PER_EU)))
 void prefill_pipe_kernel(PrefillArgs a) {
@@ -420,7 +668,14 @@ void prefill_pipe_kernel(PrefillArgs a) {
     constexpr int STAGE_BYTES = Lds<DT>::STAGE_BYTES;
     __shared__ __align__(16) uint8_t smem[Lds<DT>::BYTES];
     static_assert(sizeof(smem) >= kRankLdsBytes, "dispatch ranking needs the tile LDS");
-    const PrefillSlot sl = prefill_slot(a, reinterpret_cast<int *>(smem));
+    PrefillSlot sl = prefill_slot(a, reinterpret_cast<int *>(smem));
+    if (sl.b < 0) return;                               // a piece this launch does not use
+    // uniform per workgroup: scalar registers
+    sl.b = __builtin_amdgcn_readfirstlane(sl.b);
+    sl.z = __builtin_amdgcn_readfirstlane(sl.z);
+    sl.p = __builtin_amdgcn_readfirstlane(sl.p);
+    sl.ns = __builtin_amdgcn_readfirstlane(sl.ns);
+    sl.ord = __builtin_amdgcn_readfirstlane(sl.ord);
     const int b = sl.b, kh = sl.kh;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -454,16 +709,17 @@ void prefill_pipe_kernel(PrefillArgs a) {
         bool ok0, ok1;
     };
     int32_t nb0 = 0, nb1 = 0;          // block ids of the next tile to load (fetched a tile ahead)
+    int tile0 = 0;                     // first key tile of the piece (0 unless split)
     auto fetch_ids = [&](int t, int kend) {
         const int last = (kend - 1) / BS;
-        const int j0 = (t * kKeys) / BS;
+        const int j0 = ((tile0 + t) * kKeys) / BS;
         nb0 = tbl[j0 < last ? j0 : last];
         if constexpr (BS == 16) nb1 = tbl[j0 + 1 < last ? j0 + 1 : last];
         else nb1 = nb0;
     };
     auto load_tile = [&](int t, TileRegs &R) {
         const int32_t b0 = __builtin_amdgcn_readfirstlane(nb0), b1 = __builtin_amdgcn_readfirstlane(nb1);
-        R.kt = t * kKeys;
+        R.kt = (tile0 + t) * kKeys;
         R.ok0 = b0 >= 0 && b0 < a.num_blocks;
         R.ok1 = b1 >= 0 && b1 < a.num_blocks;
         const int64_t row0 = ((int64_t)(R.ok0 ? b0 : 0) * a.n_kv_heads + kh) * BS;
@@ -552,7 +808,10 @@ void prefill_pipe_kernel(PrefillArgs a) {
         const int kend = q_offset + rows_last;          // keys the workgroup needs (<= len)
         // uniform per workgroup / wave: kept in scalar registers so the
         // guards below are scalar branches
-        const int nt = __builtin_amdgcn_readfirstlane((kend + kKeys - 1) / kKeys);
+        // the piece's key tiles: [tile0, tile0 + nt) of the unit's nt_all
+        const int nt_all = (kend + kKeys - 1) / kKeys;
+        tile0 = __builtin_amdgcn_readfirstlane(sl.ns > 1 ? sl.p * nt_all / sl.ns : 0);
+        const int nt = __builtin_amdgcn_readfirstlane(sl.ns > 1 ? (sl.p + 1) * nt_all / sl.ns - tile0 : nt_all);
         const int diag_kt = __builtin_amdgcn_readfirstlane(q_offset + r0 - kKeys + 1);   // first masked tile start
 
         const int qrow = r0 + r32 < qlen ? r0 + r32 : qlen - 1;
@@ -613,7 +872,7 @@ void prefill_pipe_kernel(PrefillArgs a) {
         // softmax of tile t (scores s, S^T layout), first half: causal mask,
         // tile max, lazy rescale
         auto softmax_head = [&](int t, f32x16 &sc) {
-            const int kt = t * kKeys;
+            const int kt = (tile0 + t) * kKeys;
             if (kt > diag_kt) {   // masked in place: keys past the query's position
                 const int kq = qpos - kt - 4 * hh;
 #pragma unroll
@@ -743,29 +1002,22 @@ void prefill_pipe_kernel(PrefillArgs a) {
             if (t + 5 < nt) step(t + 5, Int<2>{}, sb, sa);
         }
 
-        if (wvalid && r0 + r32 < qlen) {
+        if (sl.ns > 1) {
+            // a piece of a split slot: the unnormalised partial (acc, running
+            // max, this lane's sum) of every lane, in lane order
+            f32x4 *pa = piece_acc(a, sl.ord, kh, sl.p, wave);
+#pragma unroll
+            for (int n = 0; n < D / 32; ++n)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4)
+                    pa[(4 * n + i4) * 64 + lane] =
+                        f32x4{acc[n][4 * i4], acc[n][4 * i4 + 1], acc[n][4 * i4 + 2], acc[n][4 * i4 + 3]};
+            float *pml = piece_ml(a, sl.ord, kh, sl.p);
+            pml[wave * 64 + lane] = m_run;
+            pml[kThreads + wave * 64 + lane] = l_run;
+        } else if (wvalid && r0 + r32 < qlen) {
             const float l = l_run + __shfl_xor(l_run, 32);
-            const float inv = 1.0f / l;
-            const int64_t orow = ((int64_t)(q0 + r0 + r32) * a.n_q_heads + h) * D + 4 * hh;
-            if (a.out_dtype == AIR_KV_F32) {
-#pragma unroll
-                for (int n = 0; n < D / 32; ++n)
-#pragma unroll
-                    for (int i4 = 0; i4 < 4; ++i4)
-                        *reinterpret_cast<f32x4 *>((float *)a.out + orow + 32 * n + 8 * i4) =
-                            f32x4{acc[n][4 * i4], acc[n][4 * i4 + 1], acc[n][4 * i4 + 2], acc[n][4 * i4 + 3]} * inv;
-            } else {
-#pragma unroll
-                for (int n = 0; n < D / 32; ++n)
-#pragma unroll
-                    for (int i4 = 0; i4 < 4; ++i4) {
-                        const f32x2 x = f32x2{acc[n][4 * i4], acc[n][4 * i4 + 1]} * inv;
-                        const f32x2 y = f32x2{acc[n][4 * i4 + 2], acc[n][4 * i4 + 3]} * inv;
-                        *reinterpret_cast<u32x2 *>((uint16_t *)a.out + orow + 32 * n + 8 * i4) =
-                            u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2)),
-                                  __builtin_bit_cast(uint32_t, __builtin_convertvector(y, bf16x2))};
-                    }
-            }
+            store_out(a, acc, 1.0f / l, ((int64_t)(q0 + r0 + r32) * a.n_q_heads + h) * D + 4 * hh);
         }
         __syncthreads();      // the next work item restages every LDS buffer
     }
@@ -798,20 +1050,70 @@ bool prefill_supported(int dtype, int head_dim, int block_size, int scale_group)
     return (dtype == AIR_KV_INT8 || dtype == AIR_KV_FP8) && scale_group >= 8;
 }
 
-hipError_t launch_prefill(const PrefillArgs &a, int dtype, int block_size, int32_t max_q_len,
-                          hipStream_t s) {
-    // one-dimensional grid, n_kv_heads workgroups per (sequence, slot), nz
-    // slots per sequence sized for max_q_len; the kernel strides over its
-    // slots, so a sequence longer than max_q_len is still covered completely.
+PrefillPlan prefill_plan(int32_t batch, int32_t n_kv_heads, int32_t group, int32_t max_q_len, int cus) {
+    PrefillPlan pl;
+    // nz slots per sequence sized for max_q_len; the kernel strides over its
+    // slots, so a sequence longer than max_q_len is still covered completely
     const int64_t ntb = ((int64_t)(max_q_len > 0 ? max_q_len : 1) + kRows - 1) / kRows;
-    int64_t nz = (ntb * a.group + kWaves - 1) / kWaves;
+    int64_t nz = (ntb * group + kWaves - 1) / kWaves;
+    const int64_t units_all = (int64_t)batch * n_kv_heads * nz;
+    const int64_t slots = 2 * (int64_t)cus;             // two resident workgroups per CU
+    // The key split pays where the launch has fewer work groups than
+    // resident workgroup slots (one 32K-token sequence: 274 -> 495 TFLOP/s;
+    // two of 16K: +18%).  With more, the longest groups start first and the
+    // tail runs them on emptier CUs: at the c5 chunk mix (1024 groups on 512
+    // slots) splitting gained 3% in the main kernel and lost more to the plan
+    // and the merge.  Pieces per slot: enough for two per resident slot, 2..8.
+    int64_t ns = 1;
+    if (units_all < slots) {
+        ns = (2 * slots + units_all - 1) / (units_all > 0 ? units_all : 1);
+        ns = ns < 2 ? 2 : ns > 8 ? 8 : ns;
+    }
     // a dispatch counts its work-items in 32 bits: at most 2^32 / 256 - 1
     // workgroups (fewer slots per sequence only lengthen each slot's stride)
-    const int64_t cap = ((int64_t)0xffffffff / kThreads) / ((int64_t)a.batch * a.n_kv_heads);
+    const int64_t cap = ((int64_t)0xffffffff / kThreads) / ((int64_t)batch * n_kv_heads * ns);
     nz = nz > cap ? cap : nz;
-    if (nz < 1) return hipErrorInvalidConfiguration;
-    const dim3 grid((unsigned)((int64_t)a.batch * a.n_kv_heads * nz));
-    return block_size == 16 ? launch_bs<16>(a, dtype, s, grid) : launch_bs<32>(a, dtype, s, grid);
+    pl.nz = (int32_t)nz;
+    pl.ns_max = (int32_t)ns;
+    // split slots are longer than the balanced load, so at most slots / n_kv_heads of them
+    const int64_t units = std::min<int64_t>((int64_t)batch * nz, std::max<int64_t>(1, slots / n_kv_heads));
+    const bool ranked = batch <= kRankCap && (int64_t)batch * nz * ns <= kRankItems &&
+                        (int64_t)batch * nz <= kRankItems / 2;
+    if (ns == 1 || !ranked) {                           // the key split rides on the ranked plan
+        pl.ns_max = 1;
+        pl.units = 0;
+        pl.ws_bytes = 0;
+        return pl;
+    }
+    pl.units = (int32_t)units;
+    pl.ws_bytes = prefill_ws_header(units, (int64_t)batch * nz * ns) + units * n_kv_heads * ns * kPrefillPieceBytes;
+    return pl;
+}
+
+hipError_t launch_prefill(PrefillArgs a, int dtype, int block_size, int32_t max_q_len, int cus,
+                          hipStream_t s) {
+    const PrefillPlan pl = prefill_plan(a.batch, a.n_kv_heads, a.group, max_q_len, cus);
+    if (pl.nz < 1) return hipErrorInvalidConfiguration;
+    a.nz = pl.nz;
+    a.slots = 2 * cus;
+    if (!a.ws || a.ws_units < 1 || pl.ns_max == 1) {
+        a.ns_max = 1;
+        a.ws = nullptr;
+        a.ws_units = 0;
+    } else {
+        a.ns_max = pl.ns_max;
+    }
+    if (a.ns_max > 1) {
+        hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, a);
+        const hipError_t pe = hipGetLastError();
+        if (pe != hipSuccess) return pe;
+    }
+    const dim3 grid((unsigned)((int64_t)a.batch * a.n_kv_heads * a.nz * a.ns_max));
+    hipError_t e = block_size == 16 ? launch_bs<16>(a, dtype, s, grid) : launch_bs<32>(a, dtype, s, grid);
+    if (e != hipSuccess || a.ns_max == 1) return e;
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((int64_t)a.ws_units * a.n_kv_heads)), dim3(kThreads),
+                       0, s, a);
+    return hipGetLastError();
 }
 
 }  // namespace airkv

@@ -174,10 +174,28 @@ int air_paged_decode(air_kv_pool *p, void *stream, const void *q, int32_t q_dtyp
     return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "air_paged_decode launch");
 }
 
+int air_paged_prefill_workspace_size(const air_kv_pool *p, int32_t n_q_heads, int32_t batch,
+                                     int32_t max_q_len, size_t *bytes) {
+    if (!p || !bytes) return fail(AIR_KV_E_INVALID_ARG, "pool or bytes is NULL");
+    if (n_q_heads <= 0 || n_q_heads % p->desc.n_kv_heads)
+        return fail(AIR_KV_E_INVALID_ARG, "n_q_heads %d is not a multiple of n_kv_heads %d", n_q_heads,
+                    p->desc.n_kv_heads);
+    if (batch < 0 || max_q_len < 0) return fail(AIR_KV_E_INVALID_ARG, "negative batch or max_q_len");
+    if (batch == 0) {
+        *bytes = 0;
+        return AIR_KV_OK;
+    }
+    const airkv::PrefillPlan pl =
+        airkv::prefill_plan(batch, p->desc.n_kv_heads, n_q_heads / p->desc.n_kv_heads, max_q_len, p->cus);
+    *bytes = (size_t)pl.ws_bytes;
+    return AIR_KV_OK;
+}
+
 int air_paged_prefill(air_kv_pool *p, void *stream, const void *q, int32_t q_dtype, int32_t n_q_heads,
                       const int32_t *cu_q, int32_t total_q, int32_t max_q_len,
                       const int32_t *block_tables, const int32_t *seq_lens, int32_t batch,
-                      int32_t max_blocks, float scale, void *out, int32_t out_dtype) {
+                      int32_t max_blocks, float scale, void *workspace, size_t ws_bytes, void *out,
+                      int32_t out_dtype) {
     if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
     const air_kv_pool_desc &d = p->desc;
     if (!airkv::prefill_supported(d.dtype, d.head_dim, d.block_size, d.scale_group))
@@ -210,7 +228,19 @@ int air_paged_prefill(air_kv_pool *p, void *stream, const void *q, int32_t q_dty
     a.k_pages = p->k_pages; a.v_pages = p->v_pages; a.k_scales = p->k_scales; a.v_scales = p->v_scales;
     a.out = out; a.out_dtype = out_dtype;
     a.errors = p->errors;
-    hipError_t e = airkv::launch_prefill(a, d.dtype, d.block_size, max_q_len, (hipStream_t)stream);
+    a.ws = nullptr;
+    a.ws_units = 0;
+    const airkv::PrefillPlan pl =
+        airkv::prefill_plan(batch, d.n_kv_heads, n_q_heads / d.n_kv_heads, max_q_len, p->cus);
+    if (workspace && pl.ws_bytes > 0) {
+        if (ws_bytes < (size_t)pl.ws_bytes)
+            return fail(AIR_KV_E_INVALID_ARG, "prefill workspace of %zu bytes, %lld needed", ws_bytes,
+                        (long long)pl.ws_bytes);
+        if ((uintptr_t)workspace % 16) return fail(AIR_KV_E_INVALID_ARG, "prefill workspace must be 16-byte aligned");
+        a.ws = workspace;
+        a.ws_units = pl.units;
+    }
+    hipError_t e = airkv::launch_prefill(a, d.dtype, d.block_size, max_q_len, p->cus, (hipStream_t)stream);
     return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "air_paged_prefill launch");
 }
 

@@ -303,11 +303,28 @@ int air_paged_decode_noalloc(air_kv_pool *pool, void *stream, const void *q, int
  * whose q_len exceeds its seq_len is counted (air_kv_pool_error_count) and its
  * rows (when they lie in [0, total_q]) are zero-filled; out-of-pool table
  * entries within a sequence's length are counted and read as zero keys and
- * values.  No workspace; rows of different sequences must not overlap. */
+ * values.  Rows of different sequences must not overlap.  workspace may be
+ * NULL (every work group then walks all of its keys).  When the launch has
+ * fewer work groups (32 query rows x one GQA group of heads) than its GPU
+ * keeps resident, a 16-byte aligned device buffer of at least
+ * air_paged_prefill_workspace_size bytes (no initialisation needed) lets
+ * work groups longer than the batch's balanced load be cut into key ranges
+ * on several workgroups and merged by log-sum-exp (kernels before and after
+ * on the same stream), the combination flash_decode's split-K uses
+ * (src/flash_decode.rs:114-142); for other launches the size is 0 and any
+ * workspace is ignored.  Calls that share a workspace must be ordered (same
+ * stream). */
 int air_paged_prefill(air_kv_pool *pool, void *stream, const void *q, int32_t q_dtype,
                       int32_t n_q_heads, const int32_t *cu_q, int32_t total_q, int32_t max_q_len,
                       const int32_t *block_tables, const int32_t *seq_lens, int32_t batch,
-                      int32_t max_blocks, float scale, void *out, int32_t out_dtype);
+                      int32_t max_blocks, float scale, void *workspace, size_t ws_bytes, void *out,
+                      int32_t out_dtype);
+
+/* Workspace bytes air_paged_prefill's key split needs for this launch shape
+ * (0: the launch does not split).  It depends on the pool's device: the
+ * resident-slot count follows its compute units. */
+int air_paged_prefill_workspace_size(const air_kv_pool *pool, int32_t n_q_heads, int32_t batch,
+                                     int32_t max_q_len, size_t *bytes);
 
 /* ------------------------------------------------------------------------ */
 /* SessionKvCache over pages                                                 */

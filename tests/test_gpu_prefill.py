@@ -311,10 +311,69 @@ def test_prefill_rejects_unsupported_pools_and_args():
     pb = airkv.KvPool(8, 16, 2, 128, airkv.BF16)
     rc = L.air_paged_prefill(pb.handle, None, ctypes.c_void_p(q.data_ptr()), airkv.F32, 7,
                              ctypes.c_void_p(cu.data_ptr()), 4, 4, ctypes.c_void_p(tb.data_ptr()),
-                             ctypes.c_void_p(ln.data_ptr()), 1, 1, 0.1, ctypes.c_void_p(q.data_ptr()),
+                             ctypes.c_void_p(ln.data_ptr()), 1, 1, 0.1, None, 0, ctypes.c_void_p(q.data_ptr()),
                              airkv.F32)
     assert rc == airkv.AIR_KV_E_INVALID_ARG
     # the scale must be finite and > 0
     for bad in (0.0, -0.5, float("inf")):
         with pytest.raises(airkv.AirKvError):
             pb.paged_prefill(q, cu, tb, ln, torch.empty_like(q), scale=bad)
+
+
+@pytest.mark.parametrize("dtype,bs,nq,qf32", [(airkv.BF16, 32, 32, False), (airkv.INT8, 16, 64, False),
+                                              (airkv.BF16, 16, 32, True)])
+def test_prefill_key_split_long_sequence_vs_torch_fp32(dtype, bs, nq, qf32):
+    """One sequence of 12288 cached tokens whose last 512 are the chunk: far
+    fewer work groups than resident workgroups, so the launch cuts long
+    groups' keys over several workgroups and merges them by log-sum-exp.  The
+    workspace header must report split slots; the split and the unsplit
+    launch both match a float32 torch causal attention over the gathered
+    cache (1e-3 for bf16 pages, 2e-2 for int8 pages)."""
+    torch = torch_mod()
+    NKV, D, L, C = 8, 128, 12288, 512
+    cfg = workloads.Config("split", nq, NKV, D, bs, dtype, 1)
+    w = workloads.build_prefill_decode(cfg, [L], 131, decode_steps=0)
+    k, v = next(workloads.kv_rows(w.n_rows, NKV, D, seed=132, device="cuda", chunk_rows=1 << 24))
+    pool = device_pool_for(w)
+    off = 0
+    for slots in w.batches:
+        n = len(slots)
+        pool.append(k[off:off + n].contiguous(), v[off:off + n].contiguous(), torch.from_numpy(slots).cuda())
+        off += n
+    tables, lens = w.tables()
+    tt, lt = torch.from_numpy(tables).cuda(), torch.from_numpy(lens).cuda()
+    cu = torch.tensor([0, C], dtype=torch.int32, device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(133)
+    q = torch.randn((C, nq, D), generator=g, device="cuda")
+    if not qf32:
+        q = q.to(torch.bfloat16)
+    ws_bytes = pool.prefill_workspace_size(nq, 1, C)
+    assert ws_bytes > 0
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device="cuda")
+    out_split = torch.empty((C, nq, D), device="cuda")
+    out_plain = torch.empty_like(out_split)
+    pool.paged_prefill(q, cu, tt, lt, out_split, max_q_len=C, workspace=ws)
+    pool.paged_prefill(q, cu, tt, lt, out_plain, max_q_len=C, split=False)
+    n_split = int(ws[:4].view(torch.int32).item())
+    offs = np.array([0, L * NKV * D], np.int64)
+    gk = torch.empty(int(offs[-1]), device="cuda")
+    gv = torch.empty_like(gk)
+    pool.gather(tt, lt, torch.from_numpy(offs[:-1]).cuda(), gk, gv, out_dtype=airkv.F32,
+                layout=airkv.LAYOUT_TOKEN_MAJOR)
+    assert pool.error_count() == 0
+    torch.backends.cuda.matmul.allow_tf32 = False
+    kb = gk.view(L, NKV, D).permute(1, 0, 2).contiguous().repeat_interleave(nq // NKV, dim=0)
+    vb = gv.view(L, NKV, D).permute(1, 0, 2).contiguous().repeat_interleave(nq // NKV, dim=0)
+    qb = q.float().permute(1, 0, 2).contiguous()
+    s = torch.bmm(qb, kb.transpose(1, 2).contiguous()) / np.sqrt(float(D))
+    qpos = torch.arange(L - C, L, device="cuda")[:, None]
+    kpos = torch.arange(L, device="cuda")[None, :]
+    s = s.masked_fill(kpos > qpos, float("-inf"))
+    ref = torch.bmm(torch.softmax(s, dim=-1), vb).permute(1, 0, 2)
+    tol = 1e-3 if dtype == airkv.BF16 else 2e-2
+    es = float((out_split - ref).abs().max() / ref.abs().max())
+    ep = float((out_plain - ref).abs().max() / ref.abs().max())
+    log(f"key split dtype={dtype} nq={nq} qf32={qf32}: {n_split} split slots, err split {es:.2e} plain {ep:.2e}")
+    assert n_split > 0
+    assert es <= tol and ep <= tol
