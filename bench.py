@@ -306,18 +306,21 @@ def config_decode(torch, name, iters=20):
     return res
 
 
-def prefill_leg(torch, iters=20):
-    """Paged prefill at the configs[4] geometry: eight 512-token chunks (32 q /
-    8 kv heads, d 128, bs 32, bf16 pages and queries) over prefixes drawn
-    from the lognormal context mix.  Algorithmic flops count QK^T and PV over
-    the causal keys only: 4 * d per (query row, head, key)."""
+def prefill_leg(torch, iters=20, prefix=None):
+    """Paged prefill at the configs[4] geometry: 512-token chunks (32 q / 8 kv
+    heads, d 128, bs 32, bf16 pages and queries) over given prefixes (default:
+    eight drawn from the lognormal context mix).  Algorithmic flops count
+    QK^T and PV over the causal keys only: 4 * d per (query row, head, key).
+    The launch gets the key-split workspace the library asks for (none for
+    the c5 chunk mix; one for a single long sequence)."""
     import numpy as np
 
     import airkv
     from airkv import workloads
-    cfg = workloads.Config("c5-prefill", 32, 8, 128, 32, airkv.BF16, 8)
     chunk = 512
-    prefix = workloads.c5_lengths(cfg.batch, seed=5)
+    if prefix is None:
+        prefix = workloads.c5_lengths(8, seed=5)
+    cfg = workloads.Config("c5-prefill", 32, 8, 128, 32, airkv.BF16, len(prefix))
     w = workloads.build_prefill_decode(cfg, [p + chunk for p in prefix], seed=5, decode_steps=0)
     pool = airkv.KvPool(w.num_blocks, cfg.block_size, cfg.n_kv_heads, cfg.head_dim, cfg.dtype)
     gen = workloads.kv_rows(10 ** 12, cfg.n_kv_heads, cfg.head_dim, seed=6, device="cuda", chunk_rows=32768)
@@ -335,6 +338,7 @@ def prefill_leg(torch, iters=20):
     out = torch.empty_like(q)
     fn = pool.bind_prefill(q, cu, torch.from_numpy(tables).cuda(), torch.from_numpy(lens).cuda(), out,
                            max_q_len=chunk)
+    ws = fn.workspace
     ms = timed_loop(torch, fn, iters)
     keys = sum(sum(int(L) - chunk + r + 1 for r in range(chunk)) for L in lens)
     flops = keys * cfg.n_q_heads * 4 * cfg.head_dim
@@ -343,7 +347,7 @@ def prefill_leg(torch, iters=20):
     pool.close()
     return {"tflops": round(tf, 1), "us": round(ms * 1e3, 1), "frac_of_bf16_mfma": round(tf / 2500.0, 4),
             "prefix_tokens": [int(x) for x in prefix], "chunk": chunk, "q_rows": cfg.batch * chunk,
-            "flops": int(flops)}
+            "flops": int(flops), "key_split_workspace_bytes": 0 if ws is None else int(ws.numel())}
 
 
 def compress_leg(torch, iters=10):
@@ -611,6 +615,8 @@ def main():
             log(f"{name} decode {extra['other_configs'][name]}")
         extra["prefill_c5"] = prefill_leg(torch)
         log(f"prefill {extra['prefill_c5']['tflops']} TFLOP/s")
+        extra["prefill_one_sequence_32k"] = prefill_leg(torch, iters=5, prefix=[32256])
+        log(f"prefill one sequence {extra['prefill_one_sequence_32k']['tflops']} TFLOP/s")
         extra["kv_compress_blocks"] = compress_leg(torch)
         log(f"compress blocks {extra['kv_compress_blocks']['gbps']} GB/s")
         extra["kv_blocks"] = blocks_leg(torch)
