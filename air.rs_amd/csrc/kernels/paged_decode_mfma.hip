@@ -84,18 +84,24 @@ constexpr int kMinChunk = 4;               // tiles per slice at least
 #define AIRKV_DECODE_K16 1                 // 1-byte pages: K as 16-byte loads re-paired across lanes (else 8-byte loads)
 #endif
 #ifndef AIRKV_DECODE_QNT_LOADS
-#define AIRKV_DECODE_QNT_LOADS 0           // the same for 1-byte pages (plain loads measured faster)
+#define AIRKV_DECODE_QNT_LOADS 0           // 1-byte pages: every K/V/scale load nt (else the per-stream policy below)
 #endif
 
 // Buffer descriptor word 3 for raw (untyped) buffer access on gfx9-class
 // GPUs, and the cache-policy bits of the K/V loads: 2 = nt, streaming.  K/V
 // bytes are read exactly once, and on MI355X random 4 KB page reads run at
 // ~6.85 TB/s with nt against ~6.05 TB/s without (measured); the bf16 decode
-// keeps that ratio (c2 105 against 118 us), while 1-byte pages (2 KB slabs)
-// measured 3% faster with plain loads.
+// keeps that ratio (c2 105 against 118 us).
 constexpr int kBufferWord3 = 0x00020000;
 constexpr int kLoadAux = AIRKV_DECODE_NT_LOADS ? 2 : 0;
-constexpr int kQLoadAux = AIRKV_DECODE_QNT_LOADS ? 2 : 0;
+
+// 1-byte pages pick the policy per stream (whole c3 / c4 call, three runs
+// each, one box): nt scale loads 124.0 -> 120.6 us (c3) and 371.2 -> 360.7 us
+// (c4); nt int8 K loads on top 119.4 us for c3, while nt fp8 K loads gave
+// c4 367.7 us; nt V loads were slower on both (125.0 and 413 us).
+template <int DT> constexpr int k_code_aux() { return (AIRKV_DECODE_QNT_LOADS || DT == AIR_KV_INT8) ? 2 : 0; }
+constexpr int kVCodeAux = AIRKV_DECODE_QNT_LOADS ? 2 : 0;
+constexpr int kScaleAux = 2;
 
 __device__ __forceinline__ f32x4 mfma_qk(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
@@ -478,22 +484,22 @@ void decode_mfma_kernel(DecodeArgs a) {
             if constexpr (AIRKV_DECODE_K16) {
 #pragma unroll
                 for (int m = 0; m < 2; ++m)
-                    t.k16[m] = __builtin_amdgcn_raw_buffer_load_b128(rk, k_boff + 64 * m, 0, kQLoadAux);
+                    t.k16[m] = __builtin_amdgcn_raw_buffer_load_b128(rk, k_boff + 64 * m, 0, k_code_aux<DT>());
             } else {
 #pragma unroll
                 for (int ks = 0; ks < KSTEPS; ++ks)
-                    t.k[ks] = __builtin_amdgcn_raw_buffer_load_b64(rk, k_boff + 32 * ks, 0, kQLoadAux);
+                    t.k[ks] = __builtin_amdgcn_raw_buffer_load_b64(rk, k_boff + 32 * ks, 0, k_code_aux<DT>());
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i)
-                t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, v_boff + 16 * i, 0, kQLoadAux);
+                t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, v_boff + 16 * i, 0, kVCodeAux);
             const int64_t srow = row0 * n_sc;
             const __amdgpu_buffer_rsrc_t rks = __builtin_amdgcn_make_buffer_rsrc(
                 (void *)(a.k_scales + srow), (short)0, 16 * n_sc * 4, kBufferWord3);
             const __amdgpu_buffer_rsrc_t rvs = __builtin_amdgcn_make_buffer_rsrc(
                 (void *)(a.v_scales + srow), (short)0, 16 * n_sc * 4, kBufferWord3);
-            t.ks = __builtin_amdgcn_raw_buffer_load_b32(rks, k_soff, 0, kQLoadAux);
-            t.vs = __builtin_amdgcn_raw_buffer_load_b32(rvs, v_soff, 0, kQLoadAux);
+            t.ks = __builtin_amdgcn_raw_buffer_load_b32(rks, k_soff, 0, kScaleAux);
+            t.vs = __builtin_amdgcn_raw_buffer_load_b32(rvs, v_soff, 0, kScaleAux);
         } else {
 #pragma unroll
             for (int ks = 0; ks < KSTEPS; ++ks)
