@@ -81,6 +81,30 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x16 mfma32_f16(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// f16 pair (round to nearest even, element 0 in the low half).
+__device__ __forceinline__ uint32_t f16_pair(float x, float y) {
+    const f32x2 v = {x, y};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+
+// Eight bf16 values as f16: exact for magnitudes in [2^-17, 65504] (bf16's 8
+// significant bits fit f16's 11, down into f16's subnormal range), rounded
+// below that, and infinite above.
+__device__ __forceinline__ u32x4 bf16x8_to_f16x8(u32x4 w) {
+    u32x4 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = f16_pair(__uint_as_float(w[j] << 16), __uint_as_float(w[j] & 0xFFFF0000u));
+    return r;
+}
+
 // bf16 bits (round to nearest even) of a finite f32.
 __device__ __forceinline__ uint32_t bf16_bits(float x) {
     const uint32_t u = __float_as_uint(x);
@@ -546,6 +570,7 @@ __device__ bool prefill_begin(const PrefillArgs &a, const PrefillSlot &sl, int32
 // ---------------------------------------------------------------------------
 constexpr int kStages = 3;
 template <int N> struct Int { static constexpr int value = N; };
+template <bool B> struct BoolC { static constexpr bool value = B; };
 // Padded row pitches: K rows 272 bytes (consecutive rows start 4 banks
 // apart, so the 16 rows of a K operand read hit 16 distinct 16-byte bank
 // groups), V rows 320 bytes (rows start 16 banks apart, so the 4 rows x 64
@@ -660,9 +685,17 @@ template <int BS, bool QF32, int DT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AIRKV_PREFILL_WAVES_PER_EU)))
 void prefill_pipe_kernel(PrefillArgs a) {
     constexpr int EB = DT == AIR_KV_BF16 ? 2 : 1;   // bytes per page element
-    // bf16 pages: P as hi + lo bf16 halves; 1-byte pages, whose V operand is
-    // already a bf16 rounding of code * scale, take the hi half only
-    constexpr bool kSplitP = DT == AIR_KV_BF16;
+    // PV products.  bf16 pages: first as f16 (V converted on its way to LDS,
+    // probabilities <= 2^8 rounded to f16: 11 significant bits each, one
+    // product per tile), and again with the exact operands -- V as bf16, P as
+    // hi + lo bf16 halves, two products -- for a work item whose f16 result
+    // is not finite (a value beyond f16's 65504) or whose every output of a
+    // query row is below 2^-14 in magnitude (values so small that f16's
+    // subnormal spacing, 2^-24, would show).  1-byte pages, whose V operand
+    // is already a bf16 rounding of code * scale, take P's hi half only.
+    constexpr bool kF16PV = DT == AIR_KV_BF16;
+    __shared__ int s_redo;
+    if (threadIdx.x == 0) s_redo = 0;              // read only after barriers below
     constexpr bool kSplitK = Lds<DT>::kSplitK;
     constexpr int KPITCH = Lds<DT>::KPITCH, KTILE_BYTES = Lds<DT>::KTILE_BYTES;
     constexpr int STAGE_BYTES = Lds<DT>::STAGE_BYTES;
@@ -743,7 +776,8 @@ void prefill_pipe_kernel(PrefillArgs a) {
     // Keys past the sequence and rows of out-of-pool blocks are staged as
     // zeros (stale page bytes may hold non-finite values); only the tiles
     // that hold such keys (a uniform test) pay for the selects.
-    auto stage_tile = [&](int slot, TileRegs &R, int kend) {
+    auto stage_tile = [&](auto f16v, int slot, TileRegs &R, int kend) {
+        constexpr bool F16V = decltype(f16v)::value;    // V staged as f16 (bf16 pages)
         uint8_t *ks = smem + slot * STAGE_BYTES;
         uint8_t *vs = ks + KTILE_BYTES;
         u32x4 kb[2], vb[2];                       // as bf16 (1-byte pages dequantized)
@@ -764,7 +798,8 @@ void prefill_pipe_kernel(PrefillArgs a) {
             for (int i = 0; i < 2; ++i) {
                 const int row = (tid >> 4) + 16 * i;
                 *reinterpret_cast<u32x4 *>(ks + row * KPITCH + (tid & 15) * 16) = R.k[i].w;
-                *reinterpret_cast<u32x4 *>(vs + row * VPITCH + (tid & 15) * 16) = R.v[i].w;
+                *reinterpret_cast<u32x4 *>(vs + row * VPITCH + (tid & 15) * 16) =
+                    F16V ? bf16x8_to_f16x8(R.v[i].w) : R.v[i].w;
             }
             return;
         }
@@ -845,10 +880,6 @@ void prefill_pipe_kernel(PrefillArgs a) {
         }
 
         f32x16 acc[D / 32];
-#pragma unroll
-        for (int n = 0; n < D / 32; ++n)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) acc[n][i] = 0.0f;
         float m_run = -INFINITY, l_run = 0.0f;
 
         auto qk = [&](int slot) {
@@ -891,8 +922,11 @@ void prefill_pipe_kernel(PrefillArgs a) {
                 m_run = m_new;
             }
         };
-        // second half: probabilities, their sum, and the PV products
-        auto softmax_pv = [&](int slot, const f32x16 &sc) {
+        // second half: probabilities, their sum, and the PV products (f16,
+        // bf16 hi + lo, or bf16 hi only)
+        auto softmax_pv = [&](auto f16pv, int slot, const f32x16 &sc) {
+            constexpr bool F16 = decltype(f16pv)::value;
+            constexpr bool kSplitP = DT == AIR_KV_BF16 && !F16;
             float p[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i)   // masked: exp2(-inf) = 0
@@ -909,7 +943,10 @@ void prefill_pipe_kernel(PrefillArgs a) {
                 uint32_t hv[4], lv[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    if constexpr (kSplitP) {
+                    if constexpr (F16) {
+                        hv[j] = f16_pair(p[8 * st + 2 * j], p[8 * st + 2 * j + 1]);
+                        lv[j] = 0;
+                    } else if constexpr (kSplitP) {
                         split_pair(p[8 * st + 2 * j], p[8 * st + 2 * j + 1], hv[j], lv[j]);
                     } else {
                         const f32x2 pv = {p[8 * st + 2 * j], p[8 * st + 2 * j + 1]};
@@ -921,85 +958,132 @@ void prefill_pipe_kernel(PrefillArgs a) {
                 const int vrow = 16 * st + 4 * hh + (sl >> 2);           // keys kb .. kb + 3, then + 8
 #pragma unroll
                 for (int n = 0; n < D / 32; ++n) {
-                    const int col = 32 * n + 16 * (grp & 1) + 4 * (sl & 3);   // bf16 column of the 8 bytes
+                    const int col = 32 * n + 16 * (grp & 1) + 4 * (sl & 3);   // 16-bit column of the 8 bytes
                     const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                         (__attribute__((address_space(3))) s16x4 *)(vs_ + vrow * VPITCH + col * 2));
                     const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                         (__attribute__((address_space(3))) s16x4 *)(vs_ + (vrow + 8) * VPITCH + col * 2));
                     const u32x2 a0 = __builtin_bit_cast(u32x2, t0), a1 = __builtin_bit_cast(u32x2, t1);
                     const u32x4 va = {a0[0], a0[1], a1[0], a1[1]};
-                    acc[n] = mfma32(va, phi, acc[n]);
-                    if constexpr (kSplitP) acc[n] = mfma32(va, plo, acc[n]);
+                    if constexpr (F16) {
+                        acc[n] = mfma32_f16(va, phi, acc[n]);
+                    } else {
+                        acc[n] = mfma32(va, phi, acc[n]);
+                        if constexpr (kSplitP) acc[n] = mfma32(va, plo, acc[n]);
+                    }
                 }
             }
         };
 
-        TileRegs R;
-        fetch_ids(0, kend);
-        load_tile(0, R);
-        fetch_ids(1, kend);
-        stage_tile(0, R, kend);
-        if (nt > 1) {
-            load_tile(1, R);
-            fetch_ids(2, kend);
-            stage_tile(1, R, kend);
-        }
-        if (nt > 2) {
-            load_tile(2, R);
-            fetch_ids(3, kend);
-        }
-        __syncthreads();
-        // One pipeline step for tile t, whose LDS slot S = t % 3 is a
-        // compile-time constant (the loop is unrolled six times: three slots
-        // times two score buffers), so every LDS address is a loop-invariant
-        // register plus an immediate offset.
-        auto step = [&](int t, auto slot, f32x16 &s_cur, f32x16 &s_next) {
-            constexpr int S = decltype(slot)::value;
-            // Unconditional: a wave past the last tile its own rows need sees
-            // only keys beyond its rows, which the mask turns into zero
-            // probabilities, and the S^T product of a slot past the last
-            // tile reads stale but in-bounds LDS that is never used.  One
-            // basic block then holds tile t + 1's S^T products and tile t's
-            // exponentials and PV products, interleaved below.
-            // The products and exponentials run at raised wave priority and
-            // staging, the barrier and the page loads at the base one: when
-            // both waves of a SIMD can issue, the one computing goes first
-            // (measured 0-7% faster across chunk mixes, none slower).
-            __builtin_amdgcn_s_setprio(1);
-            softmax_head(t, s_cur);
-            s_next = qk((S + 1) % kStages);
-            softmax_pv(S, s_cur);
-            constexpr int kQk = kSplitK ? 16 : 8;      // K operand reads per tile
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        // One pass over the item's key tiles: acc, m_run and l_run from
+        // scratch, with the PV products of `f16pv`.
+        auto run_pass = [&](auto f16pv) {
+            constexpr bool F16 = decltype(f16pv)::value;
+            constexpr bool kSplitP = DT == AIR_KV_BF16 && !F16;
 #pragma unroll
-            for (int i = 0; i < kQk; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 48 / kQk, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            }
-            constexpr int kPv = kSplitP ? 16 : 8;      // PV products per tile
+            for (int n = 0; n < D / 32; ++n)
 #pragma unroll
-            for (int i = 0; i < kPv; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 16 / kPv, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                for (int i = 0; i < 16; ++i) acc[n][i] = 0.0f;
+            m_run = -INFINITY;
+            l_run = 0.0f;
+            TileRegs R;
+            fetch_ids(0, kend);
+            load_tile(0, R);
+            fetch_ids(1, kend);
+            stage_tile(f16pv, 0, R, kend);
+            if (nt > 1) {
+                load_tile(1, R);
+                fetch_ids(2, kend);
+                stage_tile(f16pv, 1, R, kend);
             }
-            __builtin_amdgcn_s_setprio(0);
-            if (t + 2 < nt) stage_tile((S + 2) % kStages, R, kend);
+            if (nt > 2) {
+                load_tile(2, R);
+                fetch_ids(3, kend);
+            }
             __syncthreads();
-            if (t + 3 < nt) {
-                load_tile(t + 3, R);
-                fetch_ids(t + 4, kend);
+            // One pipeline step for tile t, whose LDS slot S = t % 3 is a
+            // compile-time constant (the loop is unrolled six times: three slots
+            // times two score buffers), so every LDS address is a loop-invariant
+            // register plus an immediate offset.
+            auto step = [&](int t, auto slot, f32x16 &s_cur, f32x16 &s_next) {
+                constexpr int S = decltype(slot)::value;
+                // Unconditional: a wave past the last tile its own rows need sees
+                // only keys beyond its rows, which the mask turns into zero
+                // probabilities, and the S^T product of a slot past the last
+                // tile reads stale but in-bounds LDS that is never used.  One
+                // basic block then holds tile t + 1's S^T products and tile t's
+                // exponentials and PV products, interleaved below.
+                // The products and exponentials run at raised wave priority and
+                // staging, the barrier and the page loads at the base one: when
+                // both waves of a SIMD can issue, the one computing goes first
+                // (measured 0-7% faster across chunk mixes, none slower).
+                __builtin_amdgcn_s_setprio(1);
+                softmax_head(t, s_cur);
+                s_next = qk((S + 1) % kStages);
+                softmax_pv(f16pv, S, s_cur);
+                constexpr int kQk = kSplitK ? 16 : 8;      // K operand reads per tile
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+                for (int i = 0; i < kQk; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 48 / kQk, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                constexpr int kPv = kSplitP ? 16 : 8;      // PV products per tile
+#pragma unroll
+                for (int i = 0; i < kPv; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x100, 16 / kPv, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                }
+                __builtin_amdgcn_s_setprio(0);
+                if (t + 2 < nt) stage_tile(f16pv, (S + 2) % kStages, R, kend);
+                __syncthreads();
+                if (t + 3 < nt) {
+                    load_tile(t + 3, R);
+                    fetch_ids(t + 4, kend);
+                }
+            };
+            f32x16 sa = qk(0), sb = sa;
+            for (int t = 0; t < nt; t += 6) {
+                step(t, Int<0>{}, sa, sb);
+                if (t + 1 < nt) step(t + 1, Int<1>{}, sb, sa);
+                if (t + 2 < nt) step(t + 2, Int<2>{}, sa, sb);
+                if (t + 3 < nt) step(t + 3, Int<0>{}, sb, sa);
+                if (t + 4 < nt) step(t + 4, Int<1>{}, sa, sb);
+                if (t + 5 < nt) step(t + 5, Int<2>{}, sb, sa);
             }
         };
-        f32x16 sa = qk(0), sb = sa;
-        for (int t = 0; t < nt; t += 6) {
-            step(t, Int<0>{}, sa, sb);
-            if (t + 1 < nt) step(t + 1, Int<1>{}, sb, sa);
-            if (t + 2 < nt) step(t + 2, Int<2>{}, sa, sb);
-            if (t + 3 < nt) step(t + 3, Int<0>{}, sb, sa);
-            if (t + 4 < nt) step(t + 4, Int<1>{}, sa, sb);
-            if (t + 5 < nt) step(t + 5, Int<2>{}, sb, sa);
+
+        // the sum of the query row's probabilities (its two lanes hold halves
+        // of its keys)
+        const bool row_live = wvalid && r0 + r32 < qlen;
+        if constexpr (kF16PV) {
+            run_pass(BoolC<true>{});
+            // Checked on the row's unnormalised outputs: a non-finite sum, or
+            // every |output| below 2^-14 (max |acc| < 2^-14 * l) on a row that
+            // saw keys, sends the whole work item through the exact pass.
+            float sum = 0.0f, mx = 0.0f;
+#pragma unroll
+            for (int n = 0; n < D / 32; ++n)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    sum += acc[n][i];
+                    mx = fmaxf(mx, fabsf(acc[n][i]));
+                }
+            const float l = l_run + __shfl_xor(l_run, 32);
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const bool bad = row_live && (!__builtin_isfinite(sum) || (l > 0.0f && mx < 0x1p-14f * l));
+            if (__ballot(bad) != 0ull && lane == 0) s_redo = 1;
+            __syncthreads();
+            const bool redo = s_redo != 0;
+            __syncthreads();                           // every wave has read the flag
+            if (redo) {
+                if (tid == 0) s_redo = 0;              // next read after this pass's barriers
+                run_pass(BoolC<false>{});
+            }
+        } else {
+            run_pass(BoolC<false>{});
         }
 
         if (sl.ns > 1) {
@@ -1015,7 +1099,7 @@ void prefill_pipe_kernel(PrefillArgs a) {
             float *pml = piece_ml(a, sl.ord, kh, sl.p);
             pml[wave * 64 + lane] = m_run;
             pml[kThreads + wave * 64 + lane] = l_run;
-        } else if (wvalid && r0 + r32 < qlen) {
+        } else if (row_live) {
             const float l = l_run + __shfl_xor(l_run, 32);
             store_out(a, acc, 1.0f / l, ((int64_t)(q0 + r0 + r32) * a.n_q_heads + h) * D + 4 * hh);
         }

@@ -377,3 +377,77 @@ def test_prefill_key_split_long_sequence_vs_torch_fp32(dtype, bs, nq, qf32):
     log(f"key split dtype={dtype} nq={nq} qf32={qf32}: {n_split} split slots, err split {es:.2e} plain {ep:.2e}")
     assert n_split > 0
     assert es <= tol and ep <= tol
+
+
+@pytest.mark.parametrize("case", ["unit", "tiny", "huge", "spikes", "split_tiny"])
+def test_prefill_bf16_value_ranges_vs_torch_fp32(case):
+    """bf16 pages run their PV products in f16 and take a work item through
+    the exact bf16 pass when the f16 result is not finite or every output of
+    a query row is below 2^-14.  V at unit scale (f16 pass only), scaled by
+    1e-6 (f16 subnormals: the exact pass), by 1e5 (beyond f16's 65504: the
+    exact pass), with a few 2e5 spikes in otherwise unit values (only the
+    work items that see a spike take the exact pass), and tiny values under
+    the key split (pieces take the exact pass on their own): all within 1e-3
+    of a float32 torch causal attention over the gathered cache."""
+    torch = torch_mod()
+    NKV, NQ, D, C = 8, 32, 128, 256
+    split = case == "split_tiny"
+    prefix = [6000] if split else [700, 1500, 90, 2600]
+    cfg = workloads.Config("vrange", NQ, NKV, D, 32, airkv.BF16, len(prefix))
+    ctx = [p + C for p in prefix]
+    w = workloads.build_prefill_decode(cfg, ctx, 141, decode_steps=0)
+    k, v = next(workloads.kv_rows(w.n_rows, NKV, D, seed=142, device="cuda", chunk_rows=1 << 24))
+    if case in ("tiny", "split_tiny"):
+        v = v * 1e-6
+    elif case == "huge":
+        v = v * 1e5
+    elif case == "spikes":
+        g0 = torch.Generator(device="cuda")
+        g0.manual_seed(143)
+        idx = torch.randint(0, v.numel(), (5,), generator=g0, device="cuda")
+        v.view(-1)[idx] = 2e5
+    pool = device_pool_for(w)
+    off = 0
+    for slots in w.batches:
+        n = len(slots)
+        pool.append(k[off:off + n].contiguous(), v[off:off + n].contiguous(), torch.from_numpy(slots).cuda())
+        off += n
+    tables, lens = w.tables()
+    B = len(prefix)
+    tt, lt = torch.from_numpy(tables).cuda(), torch.from_numpy(lens).cuda()
+    cu = torch.from_numpy(np.arange(B + 1, dtype=np.int32) * C).cuda()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(144)
+    q = torch.randn((B * C, NQ, D), generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.full((B * C, NQ, D), float("nan"), device="cuda")
+    if split:
+        ws = torch.zeros(pool.prefill_workspace_size(NQ, B, C), dtype=torch.uint8, device="cuda")
+        assert ws.numel() > 0
+        pool.paged_prefill(q, cu, tt, lt, out, max_q_len=C, workspace=ws)
+        assert int(ws[:4].view(torch.int32).item()) > 0
+    else:
+        pool.paged_prefill(q, cu, tt, lt, out, max_q_len=C)
+    offs = np.zeros(B + 1, np.int64)
+    offs[1:] = np.cumsum(np.array(lens, np.int64) * NKV * D)
+    gk = torch.empty(int(offs[-1]), device="cuda")
+    gv = torch.empty_like(gk)
+    pool.gather(tt, lt, torch.from_numpy(offs[:-1]).cuda(), gk, gv, out_dtype=airkv.F32,
+                layout=airkv.LAYOUT_TOKEN_MAJOR)
+    assert pool.error_count() == 0
+    torch.backends.cuda.matmul.allow_tf32 = False
+    worst = 0.0
+    for b in range(B):
+        L = int(lens[b])
+        kb = gk[offs[b]:offs[b + 1]].view(L, NKV, D).permute(1, 0, 2).contiguous().repeat_interleave(NQ // NKV, dim=0)
+        vb = gv[offs[b]:offs[b + 1]].view(L, NKV, D).permute(1, 0, 2).contiguous().repeat_interleave(NQ // NKV, dim=0)
+        qb = q[C * b:C * (b + 1)].float().permute(1, 0, 2).contiguous()
+        s = torch.bmm(qb, kb.transpose(1, 2).contiguous()) / np.sqrt(float(D))
+        qpos = torch.arange(L - C, L, device="cuda")[:, None]
+        kpos = torch.arange(L, device="cuda")[None, :]
+        s = s.masked_fill(kpos > qpos, float("-inf"))
+        ref = torch.bmm(torch.softmax(s, dim=-1), vb).permute(1, 0, 2)
+        got = out[C * b:C * (b + 1)]
+        assert bool(torch.isfinite(got).all())
+        worst = max(worst, float((got - ref).abs().max() / ref.abs().max()))
+    log(f"prefill bf16 value range {case}: worst rel err {worst:.2e}")
+    assert worst <= 1e-3
