@@ -635,50 +635,101 @@ __device__ __forceinline__ void store_out(const PrefillArgs &a, const f32x16 (&a
     }
 }
 
+// store_out for the column blocks n = 2 half, 2 half + 1 of acc only.
+__device__ __forceinline__ void store_out_half(const PrefillArgs &a, const f32x16 (&acc)[D / 32], int half,
+                                               float inv, int64_t orow) {
+#pragma unroll
+    for (int nn = 0; nn < 2; ++nn) {
+        const int n = 2 * half + nn;
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+            const f32x4 v = f32x4{acc[n][4 * i4], acc[n][4 * i4 + 1], acc[n][4 * i4 + 2], acc[n][4 * i4 + 3]} * inv;
+            if (a.out_dtype == AIR_KV_F32) {
+                *reinterpret_cast<f32x4 *>((float *)a.out + orow + 32 * n + 8 * i4) = v;
+            } else {
+                *reinterpret_cast<u32x2 *>((uint16_t *)a.out + orow + 32 * n + 8 * i4) =
+                    u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{v[0], v[1]}, bf16x2)),
+                          __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{v[2], v[3]}, bf16x2))};
+            }
+        }
+    }
+}
+
 // Log-sum-exp merge of the pieces of split slot blockIdx.x / n_kv_heads, kv
 // head blockIdx.x % n_kv_heads: lane for lane the partials the pieces wrote,
-// weighted by 2^(m_p - max m), then divided by the weighted sum of the sums
-// (the two lane halves of a query row hold halves of its keys).
-__global__ __launch_bounds__(kThreads) void prefill_merge_kernel(PrefillArgs a) {
+// folded in piece order with an online rescale by 2^(m_p - running max), then
+// divided by the folded sum (the two lane halves of a query row hold halves
+// of its keys).  Eight waves: wave w takes item wave w / 2 and half w % 2 of
+// its lanes' 64 accumulators, and loads kMergeBatch pieces per round trip;
+// the first batch is requested together with the slot's descriptor (piece
+// addresses depend only on the slot, head, piece and wave), so a slot of up
+// to kMergeBatch pieces costs one round trip before its output row.
+constexpr int kMergeThreads = 512;
+constexpr int kMergeBatch = 4;
+
+__global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(PrefillArgs a) {
     const int ord = (int)(blockIdx.x / (unsigned)a.n_kv_heads), kh = (int)(blockIdx.x % (unsigned)a.n_kv_heads);
+    if (ord >= a.ws_units) return;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int iw = wave >> 1, half = wave & 1;          // item wave, half of its accumulators
     const int32_t *hdr = (const int32_t *)a.ws;
-    if (ord >= hdr[0] || ord >= a.ws_units) return;
     const int32_t *d = hdr + 16 + 4 * ord;
+    const int n_split = hdr[0];
     const int b = d[0], z = d[1], ns = d[2];
-    if (b < 0 || b >= a.batch || z < 0 || z >= a.nz || ns < 2 || ns > a.ns_max) return;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float m = -INFINITY, l = 0.0f;
+    f32x4 o[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) o[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int p0 = 0; p0 < a.ns_max; p0 += kMergeBatch) {
+        // loads of pieces p0 .. p0 + kMergeBatch - 1 (within the slot's
+        // ns_max workspace entries; pieces past ns are read but not folded)
+        float pm[kMergeBatch], pl[kMergeBatch];
+        f32x4 pv[kMergeBatch][8];
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) {
+            const int pp = p0 + i < a.ns_max ? p0 + i : p0;
+            const float *ml = piece_ml(a, ord, kh, pp);
+            pm[i] = ml[iw * 64 + lane];
+            pl[i] = ml[kThreads + iw * 64 + lane];
+            const f32x4 *pa = piece_acc(a, ord, kh, pp, iw) + 8 * half * 64 + lane;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) pv[i][q] = pa[q * 64];
+        }
+        if (ord >= n_split || ns < 2 || ns > a.ns_max) return;   // uniform: an unused descriptor
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) {
+            // a piece past the slot's count, or with no visible key for this
+            // row (running max -inf), adds nothing
+            if (p0 + i >= ns || pm[i] == -INFINITY) continue;
+            const float m_new = fmaxf(m, pm[i]);
+            const float sa = __builtin_amdgcn_exp2f(m - m_new), sb = __builtin_amdgcn_exp2f(pm[i] - m_new);
+            l = l * sa + pl[i] * sb;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) o[q] = o[q] * sa + pv[i][q] * sb;
+            m = m_new;
+        }
+        if (p0 + kMergeBatch >= ns) break;
+    }
+    if (b < 0 || b >= a.batch || z < 0 || z >= a.nz) return;
     const int G = a.group;
     const int32_t q0 = a.cu_q[b];
     const int qlen = a.cu_q[b + 1] - q0;
     const int n_items = (qlen + kRows - 1) / kRows * G;
     const int n_wg = (n_items + kWaves - 1) / kWaves;
-    const int item = (n_wg - 1 - z) * kWaves + wave;
+    const int item = (n_wg - 1 - z) * kWaves + iw;
+    const float L = l + __shfl_xor(l, 32);
     if (item >= n_items) return;                        // uniform per wave
     const int tb = item / G, h = kh * G + item % G, r0 = tb * kRows;
     const int r32 = lane & 31, hh = lane >> 5;
-    float M = -INFINITY;
-    for (int p = 0; p < ns; ++p) M = fmaxf(M, piece_ml(a, ord, kh, p)[wave * 64 + lane]);
-    f32x16 o[D / 32];
+    if (r0 + r32 >= qlen) return;
+    // this half's accumulators are acc[n][4 * i4 ..] for n = 2 half, 2 half + 1
+    f32x16 acc[D / 32];
 #pragma unroll
-    for (int n = 0; n < D / 32; ++n)
+    for (int q = 0; q < 8; ++q)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[n][i] = 0.0f;
-    float L = 0.0f;
-    for (int p = 0; p < ns; ++p) {
-        const float *ml = piece_ml(a, ord, kh, p);
-        const float w = __builtin_amdgcn_exp2f(ml[wave * 64 + lane] - M);   // a piece with no visible key: 0
-        L += ml[kThreads + wave * 64 + lane] * w;
-        const f32x4 *pa = piece_acc(a, ord, kh, p, wave);
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const f32x4 v = pa[q * 64 + lane] * w;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[q / 4][4 * (q % 4) + e] += v[e];
-        }
-    }
-    L += __shfl_xor(L, 32);
-    if (r0 + r32 < qlen)
-        store_out(a, o, 1.0f / L, ((int64_t)(q0 + r0 + r32) * a.n_q_heads + h) * D + 4 * hh);
+        for (int e = 0; e < 4; ++e) acc[2 * half + q / 4][4 * (q % 4) + e] = o[q][e];
+    store_out_half(a, acc, half, 1.0f / L, ((int64_t)(q0 + r0 + r32) * a.n_q_heads + h) * D + 4 * hh);
 }
 
 template <int BS, bool QF32, int DT>
@@ -1146,11 +1197,15 @@ PrefillPlan prefill_plan(int32_t batch, int32_t n_kv_heads, int32_t group, int32
     // resident workgroup slots (one 32K-token sequence: 274 -> 495 TFLOP/s;
     // two of 16K: +18%).  With more, the longest groups start first and the
     // tail runs them on emptier CUs: at the c5 chunk mix (1024 groups on 512
-    // slots) splitting gained 3% in the main kernel and lost more to the plan
-    // and the merge.  Pieces per slot: enough for two per resident slot, 2..8.
+    // slots) splitting gained 6% in the main kernel and lost more to the plan
+    // and the merge.  Pieces per slot: enough for one per resident slot, 2..8
+    // (against two per resident slot: one 32K-token sequence 582 -> 736
+    // TFLOP/s, two of 16K 680 -> 785, one 8K int8 sequence at the 70B
+    // geometry 437 -> 521; half the partial outputs, and each piece's fixed
+    // costs spread over twice the keys).
     int64_t ns = 1;
     if (units_all < slots) {
-        ns = (2 * slots + units_all - 1) / (units_all > 0 ? units_all : 1);
+        ns = (slots + units_all - 1) / (units_all > 0 ? units_all : 1);
         ns = ns < 2 ? 2 : ns > 8 ? 8 : ns;
     }
     // a dispatch counts its work-items in 32 bits: at most 2^32 / 256 - 1
@@ -1195,8 +1250,8 @@ hipError_t launch_prefill(PrefillArgs a, int dtype, int block_size, int32_t max_
     const dim3 grid((unsigned)((int64_t)a.batch * a.n_kv_heads * a.nz * a.ns_max));
     hipError_t e = block_size == 16 ? launch_bs<16>(a, dtype, s, grid) : launch_bs<32>(a, dtype, s, grid);
     if (e != hipSuccess || a.ns_max == 1) return e;
-    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((int64_t)a.ws_units * a.n_kv_heads)), dim3(kThreads),
-                       0, s, a);
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((int64_t)a.ws_units * a.n_kv_heads)),
+                       dim3(kMergeThreads), 0, s, a);
     return hipGetLastError();
 }
 
