@@ -298,7 +298,11 @@ int air_paged_decode_noalloc(air_kv_pool *pool, void *stream, const void *q, int
  * q_len is still computed in full).  scale must be finite and > 0 (the
  * reference's is 1/sqrt(head_dim)).  Supports BF16, INT8 and FP8 pools with
  * head_dim 128 (quantized pages are dequantized q * scale in registers); other
- * pools return AIR_KV_E_INVALID_ARG.  A sequence whose rows do not lie in
+ * pools return AIR_KV_E_INVALID_ARG.  BF16 pools run the probability x value
+ * products with f16 operands (11 significant bits each); a work group whose
+ * result that way is not finite, or whose outputs of a query row are all
+ * below 2^-14 in magnitude, is recomputed with bf16 values and probabilities
+ * split into two bf16 halves.  A sequence whose rows do not lie in
  * [0, total_q], whose seq_len is outside [0, max_blocks * block_size] or
  * whose q_len exceeds its seq_len is counted (air_kv_pool_error_count) and its
  * rows (when they lie in [0, total_q]) are zero-filled; out-of-pool table
