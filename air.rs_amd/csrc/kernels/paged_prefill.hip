@@ -164,6 +164,23 @@ __device__ __forceinline__ void load_raw(__amdgpu_buffer_rsrc_t pg, __amdgpu_buf
     }
 }
 
+// Four 1-byte codes of word w times s as f32 pairs (elements 0, 1 and 2, 3):
+// the reference's dequantized value with one rounding.  int8: the code
+// biased to an unsigned byte (x ^ 0x80 = q + 128), and fma(q + 128, s, -128 s)
+// is q * s rounded once; fp8: the hardware OCP E4M3 conversion.
+template <int DT>
+__device__ __forceinline__ void dequant4(uint32_t w, float s, f32x2 &lo, f32x2 &hi) {
+    if constexpr (DT == AIR_KV_INT8) {
+        const uint32_t u = w ^ 0x80808080u;
+        const float off = -128.0f * s;
+        lo = f32x2{__builtin_fmaf((float)(u & 0xFFu), s, off), __builtin_fmaf((float)((u >> 8) & 0xFFu), s, off)};
+        hi = f32x2{__builtin_fmaf((float)((u >> 16) & 0xFFu), s, off), __builtin_fmaf((float)(u >> 24), s, off)};
+    } else {
+        lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false) * s;
+        hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true) * s;
+    }
+}
+
 template <int DT>
 __device__ __forceinline__ u32x4 to_bf16x8(const Raw8<DT> &r) {
     if constexpr (DT == AIR_KV_BF16) {
@@ -172,21 +189,31 @@ __device__ __forceinline__ u32x4 to_bf16x8(const Raw8<DT> &r) {
         u32x4 o;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const uint32_t w = r.w[h];
             f32x2 lo, hi;
-            if constexpr (DT == AIR_KV_INT8) {
-                const uint32_t u = w ^ 0x80808080u;   // q + 128 as an unsigned byte
-                const float off = -128.0f * r.s;     // exact: fma gives q * s with one rounding
-                lo = f32x2{__builtin_fmaf((float)(u & 0xFFu), r.s, off),
-                           __builtin_fmaf((float)((u >> 8) & 0xFFu), r.s, off)};
-                hi = f32x2{__builtin_fmaf((float)((u >> 16) & 0xFFu), r.s, off),
-                           __builtin_fmaf((float)(u >> 24), r.s, off)};
-            } else {
-                lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false) * r.s;
-                hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true) * r.s;
-            }
+            dequant4<DT>(r.w[h], r.s, lo, hi);
             o[2 * h] = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2));
             o[2 * h + 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2));
+        }
+        return o;
+    }
+}
+
+// Eight cache elements of one row as f16 (round to nearest even): bf16
+// pages as bf16x8_to_f16x8 converts them; 1-byte pages dequantized as
+// above and rounded once to f16's 11 significant bits (infinite beyond
+// 65504).
+template <int DT>
+__device__ __forceinline__ u32x4 to_f16x8(const Raw8<DT> &r) {
+    if constexpr (DT == AIR_KV_BF16) {
+        return bf16x8_to_f16x8(r.w);
+    } else {
+        u32x4 o;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            f32x2 lo, hi;
+            dequant4<DT>(r.w[h], r.s, lo, hi);
+            o[2 * h] = f16_pair(lo[0], lo[1]);
+            o[2 * h + 1] = f16_pair(hi[0], hi[1]);
         }
         return o;
     }
@@ -203,19 +230,8 @@ __device__ __forceinline__ void to_bf16x8_split(const Raw8<DT> &r, u32x4 &hi, u3
     } else {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const uint32_t w = r.w[h];
             f32x2 a, b;
-            if constexpr (DT == AIR_KV_INT8) {
-                const uint32_t u = w ^ 0x80808080u;
-                const float off = -128.0f * r.s;
-                a = f32x2{__builtin_fmaf((float)(u & 0xFFu), r.s, off),
-                          __builtin_fmaf((float)((u >> 8) & 0xFFu), r.s, off)};
-                b = f32x2{__builtin_fmaf((float)((u >> 16) & 0xFFu), r.s, off),
-                          __builtin_fmaf((float)(u >> 24), r.s, off)};
-            } else {
-                a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false) * r.s;
-                b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true) * r.s;
-            }
+            dequant4<DT>(r.w[h], r.s, a, b);
             uint32_t h0, l0, h1, l1;
             split_pair(a[0], a[1], h0, l0);
             split_pair(b[0], b[1], h1, l1);
@@ -736,15 +752,18 @@ template <int BS, bool QF32, int DT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(AIRKV_PREFILL_WAVES_PER_EU)))
 void prefill_pipe_kernel(PrefillArgs a) {
     constexpr int EB = DT == AIR_KV_BF16 ? 2 : 1;   // bytes per page element
-    // PV products.  bf16 pages: first as f16 (V converted on its way to LDS,
-    // probabilities <= 2^8 rounded to f16: 11 significant bits each, one
-    // product per tile), and again with the exact operands -- V as bf16, P as
-    // hi + lo bf16 halves, two products -- for a work item whose f16 result
-    // is not finite (a value beyond f16's 65504) or whose every output of a
-    // query row is below 2^-14 in magnitude (values so small that f16's
-    // subnormal spacing, 2^-24, would show).  1-byte pages, whose V operand
-    // is already a bf16 rounding of code * scale, take P's hi half only.
-    constexpr bool kF16PV = DT == AIR_KV_BF16;
+    // Two passes.  First every work item runs with f16 operands (11
+    // significant bits): V converted (bf16 pages) or dequantized (1-byte
+    // pages) to f16 on its way to LDS and probabilities <= 2^8 rounded to
+    // f16, one PV product per tile; 1-byte pages also take their keys
+    // dequantized to f16 and the queries as f16 (f32 queries as f16 hi + lo),
+    // one S^T product per step instead of the key's bf16 hi + lo pair.  A work
+    // item whose f16 result is not finite (a value beyond f16's 65504) or
+    // whose every output of a query row is below 2^-14 in magnitude (values
+    // so small that f16's subnormal spacing, 2^-24, would show) runs again
+    // with the exact operands: bf16 pages V as bf16 and P as hi + lo bf16
+    // halves (two products), 1-byte pages keys as hi + lo bf16 halves, V as
+    // the bf16 rounding of code * scale and P's hi half.
     __shared__ int s_redo;
     if (threadIdx.x == 0) s_redo = 0;              // read only after barriers below
     constexpr bool kSplitK = Lds<DT>::kSplitK;
@@ -854,11 +873,17 @@ void prefill_pipe_kernel(PrefillArgs a) {
             }
             return;
         }
-        u32x4 kl[2];                              // lo halves of the keys
+        u32x4 kl[2];                              // lo halves of the keys (exact pass)
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            to_bf16x8_split<DT>(R.k[i], kb[i], kl[i]);
-            vb[i] = to_bf16x8<DT>(R.v[i]);
+            if constexpr (F16V) {
+                kb[i] = to_f16x8<DT>(R.k[i]);
+                kl[i] = u32x4{0, 0, 0, 0};
+                vb[i] = to_f16x8<DT>(R.v[i]);
+            } else {
+                to_bf16x8_split<DT>(R.k[i], kb[i], kl[i]);
+                vb[i] = to_bf16x8<DT>(R.v[i]);
+            }
         }
         if (!(R.ok0 && R.ok1 && R.kt + kKeys <= kend)) {
             const u32x4 zero = {0, 0, 0, 0};
@@ -875,7 +900,7 @@ void prefill_pipe_kernel(PrefillArgs a) {
         for (int i = 0; i < 2; ++i) {
             const int row = (tid >> 4) + 16 * i;
             *reinterpret_cast<u32x4 *>(ks + row * KPITCH + (tid & 15) * 16) = kb[i];
-            *reinterpret_cast<u32x4 *>(ks + row * KPITCH + D * 2 + (tid & 15) * 16) = kl[i];
+            if constexpr (!F16V) *reinterpret_cast<u32x4 *>(ks + row * KPITCH + D * 2 + (tid & 15) * 16) = kl[i];
             *reinterpret_cast<u32x4 *>(vs + row * VPITCH + (tid & 15) * 16) = vb[i];
         }
     };
@@ -903,7 +928,11 @@ void prefill_pipe_kernel(PrefillArgs a) {
         const int qrow = r0 + r32 < qlen ? r0 + r32 : qlen - 1;
         const int qpos = q_offset + qrow;
         u32x4 qhi[D / 16], qlo[D / 16];
-        {
+        // The query operands of a pass: bf16 (f32 queries as hi + lo bf16
+        // halves), or for the f16 pass over 1-byte pages f16 (f32 queries as
+        // hi + lo f16 halves of the bf16 pair's sum, ~22 bits).
+        auto load_q = [&](auto f16q) {
+            constexpr bool F16Q = decltype(f16q)::value;
             const int64_t qbase = ((int64_t)(q0 + qrow) * a.n_q_heads + h) * D + 8 * hh;
 #pragma unroll
             for (int ks = 0; ks < D / 16; ++ks) {
@@ -922,18 +951,35 @@ void prefill_pipe_kernel(PrefillArgs a) {
                     qlo[ks] = u32x4{0, 0, 0, 0};
                 }
             }
+            if constexpr (F16Q) {
+#pragma unroll
+                for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float x0 = __uint_as_float(qhi[ks][j] << 16) + __uint_as_float(qlo[ks][j] << 16);
+                        const float x1 = __uint_as_float(qhi[ks][j] & 0xFFFF0000u) +
+                                         __uint_as_float(qlo[ks][j] & 0xFFFF0000u);
+                        const uint32_t hf = f16_pair(x0, x1);
+                        qhi[ks][j] = hf;
+                        if constexpr (QF32) {
+                            const f32x2 hv = __builtin_convertvector(__builtin_bit_cast(f16x2, hf), f32x2);
+                            qlo[ks][j] = f16_pair(x0 - hv[0], x1 - hv[1]);
+                        }
+                    }
+            }
             // consumed here so no vector-memory wait lands inside the tile loop
 #pragma unroll
             for (int ks = 0; ks < D / 16; ++ks) {
                 asm volatile("" ::"v"(qhi[ks]));
                 if constexpr (QF32) asm volatile("" ::"v"(qlo[ks]));
             }
-        }
+        };
 
         f32x16 acc[D / 32];
         float m_run = -INFINITY, l_run = 0.0f;
 
-        auto qk = [&](int slot) {
+        auto qk = [&](auto f16k, int slot) {
+            constexpr bool F16K = decltype(f16k)::value && DT != AIR_KV_BF16;   // f16 keys and queries
             const uint8_t *ks_ = smem + slot * STAGE_BYTES;
             f32x16 s;
 #pragma unroll
@@ -941,6 +987,11 @@ void prefill_pipe_kernel(PrefillArgs a) {
 #pragma unroll
             for (int ks = 0; ks < D / 16; ++ks) {
                 const u32x4 kA = *reinterpret_cast<const u32x4 *>(ks_ + r32 * KPITCH + (2 * ks + hh) * 16);
+                if constexpr (F16K) {
+                    s = mfma32_f16(kA, qhi[ks], s);
+                    if constexpr (QF32) s = mfma32_f16(kA, qlo[ks], s);
+                    continue;
+                }
                 s = mfma32(kA, qhi[ks], s);
                 if constexpr (QF32) s = mfma32(kA, qlo[ks], s);
                 if constexpr (kSplitK) {
@@ -1031,6 +1082,7 @@ void prefill_pipe_kernel(PrefillArgs a) {
         auto run_pass = [&](auto f16pv) {
             constexpr bool F16 = decltype(f16pv)::value;
             constexpr bool kSplitP = DT == AIR_KV_BF16 && !F16;
+            load_q(BoolC<F16 && DT != AIR_KV_BF16>{});
 #pragma unroll
             for (int n = 0; n < D / 32; ++n)
 #pragma unroll
@@ -1070,9 +1122,9 @@ void prefill_pipe_kernel(PrefillArgs a) {
                 // (measured 0-7% faster across chunk mixes, none slower).
                 __builtin_amdgcn_s_setprio(1);
                 softmax_head(t, s_cur);
-                s_next = qk((S + 1) % kStages);
+                s_next = qk(f16pv, (S + 1) % kStages);
                 softmax_pv(f16pv, S, s_cur);
-                constexpr int kQk = kSplitK ? 16 : 8;      // K operand reads per tile
+                constexpr int kQk = (kSplitK && !F16) ? 16 : 8;      // K operand reads per tile
                 __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
                 for (int i = 0; i < kQk; ++i) {
@@ -1095,7 +1147,7 @@ void prefill_pipe_kernel(PrefillArgs a) {
                     fetch_ids(t + 4, kend);
                 }
             };
-            f32x16 sa = qk(0), sb = sa;
+            f32x16 sa = qk(f16pv, 0), sb = sa;
             for (int t = 0; t < nt; t += 6) {
                 step(t, Int<0>{}, sa, sb);
                 if (t + 1 < nt) step(t + 1, Int<1>{}, sb, sa);
@@ -1109,7 +1161,7 @@ void prefill_pipe_kernel(PrefillArgs a) {
         // the sum of the query row's probabilities (its two lanes hold halves
         // of its keys)
         const bool row_live = wvalid && r0 + r32 < qlen;
-        if constexpr (kF16PV) {
+        {
             run_pass(BoolC<true>{});
             // Checked on the row's unnormalised outputs: a non-finite sum, or
             // every |output| below 2^-14 (max |acc| < 2^-14 * l) on a row that
@@ -1133,8 +1185,6 @@ void prefill_pipe_kernel(PrefillArgs a) {
                 if (tid == 0) s_redo = 0;              // next read after this pass's barriers
                 run_pass(BoolC<false>{});
             }
-        } else {
-            run_pass(BoolC<false>{});
         }
 
         if (sl.ns > 1) {

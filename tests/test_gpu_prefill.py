@@ -379,21 +379,25 @@ def test_prefill_key_split_long_sequence_vs_torch_fp32(dtype, bs, nq, qf32):
     assert es <= tol and ep <= tol
 
 
-@pytest.mark.parametrize("case", ["unit", "tiny", "huge", "spikes", "split_tiny"])
-def test_prefill_bf16_value_ranges_vs_torch_fp32(case):
-    """bf16 pages run their PV products in f16 and take a work item through
-    the exact bf16 pass when the f16 result is not finite or every output of
-    a query row is below 2^-14.  V at unit scale (f16 pass only), scaled by
-    1e-6 (f16 subnormals: the exact pass), by 1e5 (beyond f16's 65504: the
-    exact pass), with a few 2e5 spikes in otherwise unit values (only the
-    work items that see a spike take the exact pass), and tiny values under
-    the key split (pieces take the exact pass on their own): all within 1e-3
-    of a float32 torch causal attention over the gathered cache."""
+@pytest.mark.parametrize("dtype,bs", [(airkv.BF16, 32), (airkv.INT8, 16), (airkv.FP8, 32)])
+@pytest.mark.parametrize("case", ["unit", "tiny", "huge", "huge_k", "spikes", "split_tiny"])
+def test_prefill_value_ranges_vs_torch_fp32(dtype, bs, case):
+    """Every work item first runs with f16 operands (V as f16; 1-byte pages
+    also keys and queries as f16) and runs again with the exact operands
+    when that result is not finite or every output of a query row is below
+    2^-14.  V at unit scale (the f16 pass only), scaled by 1e-6 (f16
+    subnormals: the exact pass), by 1e5 (beyond f16's 65504: the exact pass),
+    K scaled by 1e5 and Q by 1e-5 (1-byte keys beyond 65504 after
+    dequantization, logits unchanged), a few
+    2e5 spikes in otherwise unit values (only the work items that see a
+    spike run again), and tiny values under the key split (pieces run again
+    on their own): all within 1e-3 (bf16 pages) or 2e-2 (int8 / fp8 pages) of
+    a float32 torch causal attention over the gathered cache."""
     torch = torch_mod()
     NKV, NQ, D, C = 8, 32, 128, 256
     split = case == "split_tiny"
     prefix = [6000] if split else [700, 1500, 90, 2600]
-    cfg = workloads.Config("vrange", NQ, NKV, D, 32, airkv.BF16, len(prefix))
+    cfg = workloads.Config("vrange", NQ, NKV, D, bs, dtype, len(prefix))
     ctx = [p + C for p in prefix]
     w = workloads.build_prefill_decode(cfg, ctx, 141, decode_steps=0)
     k, v = next(workloads.kv_rows(w.n_rows, NKV, D, seed=142, device="cuda", chunk_rows=1 << 24))
@@ -401,6 +405,8 @@ def test_prefill_bf16_value_ranges_vs_torch_fp32(case):
         v = v * 1e-6
     elif case == "huge":
         v = v * 1e5
+    elif case == "huge_k":
+        k = k * 1e5
     elif case == "spikes":
         g0 = torch.Generator(device="cuda")
         g0.manual_seed(143)
@@ -418,7 +424,10 @@ def test_prefill_bf16_value_ranges_vs_torch_fp32(case):
     cu = torch.from_numpy(np.arange(B + 1, dtype=np.int32) * C).cuda()
     g = torch.Generator(device="cuda")
     g.manual_seed(144)
-    q = torch.randn((B * C, NQ, D), generator=g, device="cuda").to(torch.bfloat16)
+    q = torch.randn((B * C, NQ, D), generator=g, device="cuda")
+    if case == "huge_k":      # logits stay O(1): keys x 1e5, queries x 1e-5
+        q = q * 1e-5
+    q = q.to(torch.bfloat16)
     out = torch.full((B * C, NQ, D), float("nan"), device="cuda")
     if split:
         ws = torch.zeros(pool.prefill_workspace_size(NQ, B, C), dtype=torch.uint8, device="cuda")
@@ -441,13 +450,13 @@ def test_prefill_bf16_value_ranges_vs_torch_fp32(case):
         kb = gk[offs[b]:offs[b + 1]].view(L, NKV, D).permute(1, 0, 2).contiguous().repeat_interleave(NQ // NKV, dim=0)
         vb = gv[offs[b]:offs[b + 1]].view(L, NKV, D).permute(1, 0, 2).contiguous().repeat_interleave(NQ // NKV, dim=0)
         qb = q[C * b:C * (b + 1)].float().permute(1, 0, 2).contiguous()
-        s = torch.bmm(qb, kb.transpose(1, 2).contiguous()) / np.sqrt(float(D))
+        s_ = torch.bmm(qb, kb.transpose(1, 2).contiguous()) / np.sqrt(float(D))
         qpos = torch.arange(L - C, L, device="cuda")[:, None]
         kpos = torch.arange(L, device="cuda")[None, :]
-        s = s.masked_fill(kpos > qpos, float("-inf"))
-        ref = torch.bmm(torch.softmax(s, dim=-1), vb).permute(1, 0, 2)
+        s_ = s_.masked_fill(kpos > qpos, float("-inf"))
+        ref = torch.bmm(torch.softmax(s_, dim=-1), vb).permute(1, 0, 2)
         got = out[C * b:C * (b + 1)]
         assert bool(torch.isfinite(got).all())
         worst = max(worst, float((got - ref).abs().max() / ref.abs().max()))
-    log(f"prefill bf16 value range {case}: worst rel err {worst:.2e}")
-    assert worst <= 1e-3
+    log(f"prefill value range dtype={dtype} {case}: worst rel err {worst:.2e}")
+    assert worst <= TOL[dtype]
