@@ -306,13 +306,15 @@ def config_decode(torch, name, iters=20):
     return res
 
 
-def prefill_leg(torch, iters=20, prefix=None):
+def prefill_leg(torch, iters=20, prefix=None, int8_70b=False):
     """Paged prefill at the configs[4] geometry: 512-token chunks (32 q / 8 kv
     heads, d 128, bs 32, bf16 pages and queries) over given prefixes (default:
-    eight drawn from the lognormal context mix).  Algorithmic flops count
-    QK^T and PV over the causal keys only: 4 * d per (query row, head, key).
-    The launch gets the key-split workspace the library asks for (none for
-    the c5 chunk mix; one for a single long sequence)."""
+    eight drawn from the lognormal context mix); with int8_70b, at the
+    configs[2] geometry instead (64 q / 8 kv heads, bs 16, int8 Q8_0 pages
+    with 1% outlier channels x20).  Algorithmic flops count QK^T and PV over
+    the causal keys only: 4 * d per (query row, head, key).  The launch gets
+    the key-split workspace the library asks for (none for the c5 chunk mix;
+    one for a single long sequence)."""
     import numpy as np
 
     import airkv
@@ -320,10 +322,15 @@ def prefill_leg(torch, iters=20, prefix=None):
     chunk = 512
     if prefix is None:
         prefix = workloads.c5_lengths(8, seed=5)
-    cfg = workloads.Config("c5-prefill", 32, 8, 128, 32, airkv.BF16, len(prefix))
+    if int8_70b:
+        cfg = workloads.Config("c3-prefill", 64, 8, 128, 16, airkv.INT8, len(prefix))
+    else:
+        cfg = workloads.Config("c5-prefill", 32, 8, 128, 32, airkv.BF16, len(prefix))
     w = workloads.build_prefill_decode(cfg, [p + chunk for p in prefix], seed=5, decode_steps=0)
     pool = airkv.KvPool(w.num_blocks, cfg.block_size, cfg.n_kv_heads, cfg.head_dim, cfg.dtype)
-    gen = workloads.kv_rows(10 ** 12, cfg.n_kv_heads, cfg.head_dim, seed=6, device="cuda", chunk_rows=32768)
+    gen = workloads.kv_rows(10 ** 12, cfg.n_kv_heads, cfg.head_dim, seed=6, device="cuda", chunk_rows=32768,
+                            outliers=workloads.outlier_channels(cfg.n_kv_heads, cfg.head_dim, seed=3) if int8_70b
+                            else None)
     for slots in w.batches:
         st = torch.from_numpy(slots).cuda()
         done = 0
@@ -346,6 +353,7 @@ def prefill_leg(torch, iters=20, prefix=None):
     assert pool.error_count() == 0
     pool.close()
     return {"tflops": round(tf, 1), "us": round(ms * 1e3, 1), "frac_of_bf16_mfma": round(tf / 2500.0, 4),
+            "kv_dtype": "int8" if int8_70b else "bf16", "n_q_heads": cfg.n_q_heads, "block_size": cfg.block_size,
             "prefix_tokens": [int(x) for x in prefix], "chunk": chunk, "q_rows": cfg.batch * chunk,
             "flops": int(flops), "key_split_workspace_bytes": 0 if ws is None else int(ws.numel())}
 
@@ -617,6 +625,8 @@ def main():
         log(f"prefill {extra['prefill_c5']['tflops']} TFLOP/s")
         extra["prefill_one_sequence_32k"] = prefill_leg(torch, iters=5, prefix=[32256])
         log(f"prefill one sequence {extra['prefill_one_sequence_32k']['tflops']} TFLOP/s")
+        extra["prefill_c5_chunks_int8_70b"] = prefill_leg(torch, int8_70b=True)
+        log(f"prefill int8 70B geometry {extra['prefill_c5_chunks_int8_70b']['tflops']} TFLOP/s")
         extra["kv_compress_blocks"] = compress_leg(torch)
         log(f"compress blocks {extra['kv_compress_blocks']['gbps']} GB/s")
         extra["kv_blocks"] = blocks_leg(torch)
