@@ -84,6 +84,18 @@ def test_prefill_f32_queries_bf16_out(bs):
     assert err <= 1e-3
 
 
+@pytest.mark.parametrize("dtype,bs", [(airkv.INT8, 16), (airkv.FP8, 32)])
+def test_prefill_f32_queries_1byte_pages(dtype, bs):
+    """f32 queries over int8 / fp8 pages: the f16 pass takes the queries as
+    f16 hi + lo halves against f16 keys; within 2e-2 of the oracle on the
+    same dequantized cache (f32 queries)."""
+    cfg = workloads.Config("q32b", 8, 2, 128, bs, dtype, 3)
+    got, want = _prefill_case(cfg, [70, 129, 250], [70, 64, 97], seed=72, q_bf16=False)
+    err = rel_err(got, want)
+    log(f"prefill f32 q dtype={dtype} bs={bs}: rel err {err:.2e}")
+    assert err <= TOL[dtype]
+
+
 def test_prefill_max_q_len_below_actual_still_complete():
     cfg = workloads.Config("mq", 8, 2, 128, 16, airkv.BF16, 2)
     got, want = _prefill_case(cfg, [300, 200], [300, 150], seed=73, max_q_len=40)
