@@ -930,7 +930,7 @@ void prefill_pipe_kernel(PrefillArgs a) {
         u32x4 qhi[D / 16], qlo[D / 16];
         // The query operands of a pass: bf16 (f32 queries as hi + lo bf16
         // halves), or for the f16 pass over 1-byte pages f16 (f32 queries as
-        // hi + lo f16 halves of the bf16 pair's sum, ~22 bits).
+        // hi + lo f16 halves, ~22 significant bits).
         auto load_q = [&](auto f16q) {
             constexpr bool F16Q = decltype(f16q)::value;
             const int64_t qbase = ((int64_t)(q0 + qrow) * a.n_q_heads + h) * D + 8 * hh;
@@ -939,33 +939,31 @@ void prefill_pipe_kernel(PrefillArgs a) {
                 if constexpr (QF32) {
                     const f32x4 *qp = reinterpret_cast<const f32x4 *>((const float *)a.q + qbase + 16 * ks);
                     const f32x4 x0 = qp[0], x1 = qp[1];
-                    uint32_t hv[4], lv[4];
-                    split_pair(x0[0], x0[1], hv[0], lv[0]);
-                    split_pair(x0[2], x0[3], hv[1], lv[1]);
-                    split_pair(x1[0], x1[1], hv[2], lv[2]);
-                    split_pair(x1[2], x1[3], hv[3], lv[3]);
-                    qhi[ks] = u32x4{hv[0], hv[1], hv[2], hv[3]};
-                    qlo[ks] = u32x4{lv[0], lv[1], lv[2], lv[3]};
+                    const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        if constexpr (F16Q) {          // f16 hi + lo: ~22 significant bits
+                            const uint32_t hf = f16_pair(x[2 * j], x[2 * j + 1]);
+                            const f32x2 hv = __builtin_convertvector(__builtin_bit_cast(f16x2, hf), f32x2);
+                            qhi[ks][j] = hf;
+                            qlo[ks][j] = f16_pair(x[2 * j] - hv[0], x[2 * j + 1] - hv[1]);
+                        } else {
+                            uint32_t hb, lb;
+                            split_pair(x[2 * j], x[2 * j + 1], hb, lb);
+                            qhi[ks][j] = hb;
+                            qlo[ks][j] = lb;
+                        }
+                    }
                 } else {
                     qhi[ks] = *reinterpret_cast<const u32x4 *>((const uint16_t *)a.q + qbase + 16 * ks);
                     qlo[ks] = u32x4{0, 0, 0, 0};
-                }
-            }
-            if constexpr (F16Q) {
+                    if constexpr (F16Q) {              // bf16 -> f16, exact within f16's range
 #pragma unroll
-                for (int ks = 0; ks < D / 16; ++ks)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const float x0 = __uint_as_float(qhi[ks][j] << 16) + __uint_as_float(qlo[ks][j] << 16);
-                        const float x1 = __uint_as_float(qhi[ks][j] & 0xFFFF0000u) +
-                                         __uint_as_float(qlo[ks][j] & 0xFFFF0000u);
-                        const uint32_t hf = f16_pair(x0, x1);
-                        qhi[ks][j] = hf;
-                        if constexpr (QF32) {
-                            const f32x2 hv = __builtin_convertvector(__builtin_bit_cast(f16x2, hf), f32x2);
-                            qlo[ks][j] = f16_pair(x0 - hv[0], x1 - hv[1]);
-                        }
+                        for (int j = 0; j < 4; ++j)
+                            qhi[ks][j] = f16_pair(__uint_as_float(qhi[ks][j] << 16),
+                                                  __uint_as_float(qhi[ks][j] & 0xFFFF0000u));
                     }
+                }
             }
             // consumed here so no vector-memory wait lands inside the tile loop
 #pragma unroll
