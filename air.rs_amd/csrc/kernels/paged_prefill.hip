@@ -26,18 +26,23 @@
 //                   l + 32 hold 16 keys each); the running max is raised only
 //                   when a tile exceeds it by 2^8, so probabilities stay below
 //                   256 and most tiles skip rescaling the accumulators.
-//   O^T += V^T . P^T  v_mfma_f32_32x32x16_bf16, M = 32 head_dim rows (four
+//   O^T += V^T . P^T  v_mfma_f32_32x32x16_f16, M = 32 head_dim rows (four
 //                   tiles), N = 32 queries, K = 16 keys per step.  P^T is used
 //                   where the S^T product left it: its B-operand keys are
 //                   those of the C layout, keys (8*(i/4) + 4*(lane/32) + i%4)
-//                   for registers i = 8*step .. +8.  P is split into hi + lo
-//                   bf16 halves (~16 mantissa bits): bf16 probabilities alone
-//                   leave ~1e-3 relative error at these lengths.
+//                   for registers i = 8*step .. +8.  V and P are f16 (11
+//                   significant bits; bf16 probabilities alone leave ~3e-3
+//                   relative error at these lengths).
+//
+// Two passes per work item.  The f16 pass above (1-byte pages: keys, values
+// and queries dequantized or converted to f16 as well, one S^T product per
+// step); a work item whose f16 result is not finite or whose every output of
+// a query row lies below 2^-14 runs again with exact operands: V as bf16 and
+// P as hi + lo bf16 halves (two PV products), 1-byte keys as hi + lo bf16
+// halves (two S^T products) and values as one bf16 rounding with P's hi half.
 //
 // K and V tiles are staged row-major in three LDS stages (1-byte codes
-// dequantized on the way: keys as hi + lo bf16 halves that take two S^T
-// products, values as one bf16 rounding, whose probabilities then take the
-// hi bf16 half only); the V^T operand comes
+// dequantized on the way); the V^T operand comes
 // from two transposing reads (ds_read_b64_tr_b16) per 16 keys.  The loop is
 // software-pipelined: the S^T product of tile t + 1 is issued before the
 // softmax and PV products of tile t, tile t + 2 is written to LDS after them,
