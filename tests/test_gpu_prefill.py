@@ -472,3 +472,54 @@ def test_prefill_value_ranges_vs_torch_fp32(dtype, bs, case):
         worst = max(worst, float((got - ref).abs().max() / ref.abs().max()))
     log(f"prefill value range dtype={dtype} {case}: worst rel err {worst:.2e}")
     assert worst <= TOL[dtype]
+
+
+def test_prefill_key_split_eight_pieces():
+    """A 128-row chunk of one 12288-token sequence: 32 work groups against
+    512 resident slots, so slots are cut into the maximum of eight pieces and
+    the merge folds them in two batches of four.  The workspace descriptors
+    must show eight pieces; the result matches a float32 torch causal
+    attention within 1e-3."""
+    torch = torch_mod()
+    NKV, NQ, D, L, C = 8, 32, 128, 12288, 128
+    cfg = workloads.Config("split8", NQ, NKV, D, 32, airkv.BF16, 1)
+    w = workloads.build_prefill_decode(cfg, [L], 151, decode_steps=0)
+    k, v = next(workloads.kv_rows(w.n_rows, NKV, D, seed=152, device="cuda", chunk_rows=1 << 24))
+    pool = device_pool_for(w)
+    off = 0
+    for slots in w.batches:
+        n = len(slots)
+        pool.append(k[off:off + n].contiguous(), v[off:off + n].contiguous(), torch.from_numpy(slots).cuda())
+        off += n
+    tables, lens = w.tables()
+    tt, lt = torch.from_numpy(tables).cuda(), torch.from_numpy(lens).cuda()
+    cu = torch.tensor([0, C], dtype=torch.int32, device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(153)
+    q = torch.randn((C, NQ, D), generator=g, device="cuda").to(torch.bfloat16)
+    ws = torch.zeros(pool.prefill_workspace_size(NQ, 1, C), dtype=torch.uint8, device="cuda")
+    assert ws.numel() > 0
+    out = torch.empty((C, NQ, D), device="cuda")
+    pool.paged_prefill(q, cu, tt, lt, out, max_q_len=C, workspace=ws)
+    hdr = ws[:64 + 16 * 64].view(torch.int32).cpu().numpy()
+    n_split = int(hdr[0])
+    pieces = [int(hdr[16 + 4 * i + 2]) for i in range(n_split)]
+    offs = np.array([0, L * NKV * D], np.int64)
+    gk = torch.empty(int(offs[-1]), device="cuda")
+    gv = torch.empty_like(gk)
+    pool.gather(tt, lt, torch.from_numpy(offs[:-1]).cuda(), gk, gv, out_dtype=airkv.F32,
+                layout=airkv.LAYOUT_TOKEN_MAJOR)
+    assert pool.error_count() == 0
+    torch.backends.cuda.matmul.allow_tf32 = False
+    kb = gk.view(L, NKV, D).permute(1, 0, 2).contiguous().repeat_interleave(NQ // NKV, dim=0)
+    vb = gv.view(L, NKV, D).permute(1, 0, 2).contiguous().repeat_interleave(NQ // NKV, dim=0)
+    qb = q.float().permute(1, 0, 2).contiguous()
+    s_ = torch.bmm(qb, kb.transpose(1, 2).contiguous()) / np.sqrt(float(D))
+    qpos = torch.arange(L - C, L, device="cuda")[:, None]
+    kpos = torch.arange(L, device="cuda")[None, :]
+    s_ = s_.masked_fill(kpos > qpos, float("-inf"))
+    ref = torch.bmm(torch.softmax(s_, dim=-1), vb).permute(1, 0, 2)
+    err = float((out - ref).abs().max() / ref.abs().max())
+    log(f"key split eight pieces: {n_split} split slots, pieces {sorted(set(pieces))}, err {err:.2e}")
+    assert n_split > 0 and max(pieces) == 8
+    assert err <= 1e-3
