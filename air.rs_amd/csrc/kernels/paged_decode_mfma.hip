@@ -742,9 +742,9 @@ void decode_mfma_kernel(DecodeArgs a) {
 // Log-sum-exp merge of the pieces of one (sequence, kv head), lane l holding
 // head_dim columns 2l and 2l + 1.  A wave loads the (max, sum) and partial
 // outputs of kBatch pieces together and folds them with an online rescale,
-// so it spends one memory round trip per kBatch pieces (16, or 4 when
-// sequences average about two pieces: fewer registers, more resident
-// waves).  The kernel is bound by those round trips and by how many waves it
+// so it spends one memory round trip per kBatch pieces (16 when sequences
+// average more than eight pieces, 8 when they average three to eight, 4 when
+// about two: fewer registers, more resident waves).  The kernel is bound by those round trips and by how many waves it
 // launches, not by bytes, so the host picks WH, the waves per query head:
 // one wave per head when the
 // batch's sequences have few pieces each (WH = 1, grid z covers groups above
@@ -846,8 +846,12 @@ hipError_t launch_cfg(const DecodeArgs &a, hipStream_t s) {
         hipLaunchKernelGGL((decode_merge_kernel<128, kWaves, 16>),
                            dim3((unsigned)a.batch, (unsigned)a.n_kv_heads, (unsigned)a.group), dim3(kThreads), 0,
                            s, a);
-    } else if (a.slices > 2 * a.batch) {
+    } else if (a.slices > 8 * a.batch) {
         hipLaunchKernelGGL((decode_merge_kernel<128, 1, 16>),
+                           dim3((unsigned)a.batch, (unsigned)a.n_kv_heads, (unsigned)((a.group + kWaves - 1) / kWaves)),
+                           dim3(kThreads), 0, s, a);
+    } else if (a.slices > 2 * a.batch) {        // about 3..8 pieces: eight per round trip (c2 105.1 -> 103.0 us)
+        hipLaunchKernelGGL((decode_merge_kernel<128, 1, 8>),
                            dim3((unsigned)a.batch, (unsigned)a.n_kv_heads, (unsigned)((a.group + kWaves - 1) / kWaves)),
                            dim3(kThreads), 0, s, a);
     } else {                    // about two pieces per sequence: fewer registers, more waves resident
