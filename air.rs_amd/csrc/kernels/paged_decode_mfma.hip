@@ -850,7 +850,7 @@ hipError_t launch_cfg(const DecodeArgs &a, hipStream_t s) {
         hipLaunchKernelGGL((decode_merge_kernel<128, 1, 16>),
                            dim3((unsigned)a.batch, (unsigned)a.n_kv_heads, (unsigned)((a.group + kWaves - 1) / kWaves)),
                            dim3(kThreads), 0, s, a);
-    } else if (a.slices > 2 * a.batch) {        // about 3..8 pieces: eight per round trip (c2 105.1 -> 103.0 us)
+    } else if (a.slices > 2 * a.batch) {        // about 3..8 pieces: eight per round trip
         hipLaunchKernelGGL((decode_merge_kernel<128, 1, 8>),
                            dim3((unsigned)a.batch, (unsigned)a.n_kv_heads, (unsigned)((a.group + kWaves - 1) / kWaves)),
                            dim3(kThreads), 0, s, a);
