@@ -105,6 +105,8 @@ SIGNATURES = {
     "air_paged_decode_workspace_size": (_int, [_P, _i32, _i32, _i32, _i32, ctypes.POINTER(_SZ)]),
     "air_paged_decode": (_int, [_P, _P, _P, _i32, _i32, _P, _P, _i32, _i32, ctypes.c_float, _i32, _P,
                                 _SZ, _P, _i32]),
+    "air_paged_decode_append": (_int, [_P, _P, _P, _i32, _i32, _P, _P, _P, _P, _i32, _i32, ctypes.c_float,
+                                       _i32, _P, _SZ, _P, _i32]),
     "air_paged_decode_noalloc": (_int, [_P, _P, _P, _i32, _i32, _P, _P, _i32, _i32, ctypes.c_float, _i32,
                                         _P, _i32]),
     "air_paged_prefill": (_int, [_P, _P, _P, _i32, _i32, _P, _i32, _i32, _P, _P, _i32, _i32,

@@ -134,8 +134,7 @@ class KvPool:
         n = self.decode_workspace_size(n_q_heads, batch, max_blocks, max_splits)
         return torch.empty(max(n, 16), dtype=torch.uint8, device="cuda")
 
-    def paged_decode(self, q, block_tables, seq_lens, out, scale=None, max_splits=64,
-                     workspace=None, stream=None):
+    def _decode_args(self, q, block_tables, seq_lens, out, scale, max_splits, workspace, stream):
         torch = _torch()
         batch, n_q, d = q.shape
         if d != self.head_dim:
@@ -158,35 +157,62 @@ class KvPool:
             scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
         qdt = F32 if q.dtype == torch.float32 else BF16
         odt = F32 if out.dtype == torch.float32 else BF16
-        _lib.check(_lib.load().air_paged_decode(
-            self.handle, _stream_ptr(stream), ctypes.c_void_p(q.data_ptr()), qdt, n_q,
-            ctypes.c_void_p(block_tables.data_ptr()), ctypes.c_void_p(seq_lens.data_ptr()), batch,
-            max_blocks, scale, max_splits, ctypes.c_void_p(workspace.data_ptr()), ws_bytes,
-            ctypes.c_void_p(out.data_ptr()), odt), "air_paged_decode")
+        head = (self.handle, _stream_ptr(stream), ctypes.c_void_p(q.data_ptr()), qdt, n_q)
+        tail = (ctypes.c_void_p(block_tables.data_ptr()), ctypes.c_void_p(seq_lens.data_ptr()), batch,
+                max_blocks, scale, max_splits, ctypes.c_void_p(workspace.data_ptr()), ws_bytes,
+                ctypes.c_void_p(out.data_ptr()), odt)
+        return head, tail
+
+    def _new_rows(self, q, k_new, v_new):
+        torch = _torch()
+        shape = (q.shape[0], self.n_kv_heads, self.head_dim)
+        _dev(k_new, torch.float32, "k_new", shape)
+        _dev(v_new, torch.float32, "v_new", shape)
+        return (ctypes.c_void_p(k_new.data_ptr()), ctypes.c_void_p(v_new.data_ptr()))
+
+    def paged_decode(self, q, block_tables, seq_lens, out, scale=None, max_splits=64,
+                     workspace=None, stream=None):
+        head, tail = self._decode_args(q, block_tables, seq_lens, out, scale, max_splits, workspace, stream)
+        _lib.check(_lib.load().air_paged_decode(*head, *tail), "air_paged_decode")
+        return out
+
+    def paged_decode_append(self, q, k_new, v_new, block_tables, seq_lens, out, scale=None,
+                            max_splits=64, workspace=None, stream=None):
+        """One decode step in one launch: append k_new / v_new (float32
+        [batch, n_kv_heads, head_dim]) as each sequence's token seq_lens[b] - 1,
+        then attend as paged_decode (BF16 pools, head_dim 128)."""
+        head, tail = self._decode_args(q, block_tables, seq_lens, out, scale, max_splits, workspace, stream)
+        rows = self._new_rows(q, k_new, v_new)
+        _lib.check(_lib.load().air_paged_decode_append(*head, *rows, *tail), "air_paged_decode_append")
         return out
 
     def bind_decode(self, q, block_tables, seq_lens, out, workspace, scale=None, max_splits=64,
                     stream=None):
         """Validate once, return a zero-argument launcher (for timing loops:
         no per-call Python checks between launches)."""
-        torch = _torch()
         self.paged_decode(q, block_tables, seq_lens, out, scale, max_splits, workspace, stream)
-        fn = _lib.load().air_paged_decode
-        batch, n_q, d = q.shape
-        qdt = F32 if q.dtype == torch.float32 else BF16
-        odt = F32 if out.dtype == torch.float32 else BF16
-        if scale is None:
-            scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
-        args = (self.handle, _stream_ptr(stream), ctypes.c_void_p(q.data_ptr()), qdt, n_q,
-                ctypes.c_void_p(block_tables.data_ptr()), ctypes.c_void_p(seq_lens.data_ptr()),
-                batch, block_tables.shape[1], scale, max_splits,
-                ctypes.c_void_p(workspace.data_ptr()), workspace.numel() * workspace.element_size(),
-                ctypes.c_void_p(out.data_ptr()), odt)
+        head, tail = self._decode_args(q, block_tables, seq_lens, out, scale, max_splits, workspace, stream)
+        fn, args = _lib.load().air_paged_decode, head + tail
 
         def launch():
             rc = fn(*args)
             if rc:
                 _lib.check(rc, "air_paged_decode")
+        return launch
+
+    def bind_decode_append(self, q, k_new, v_new, block_tables, seq_lens, out, workspace, scale=None,
+                           max_splits=64, stream=None):
+        """bind_decode for paged_decode_append.  The launcher appends on every
+        call: a timing loop rewrites the same rows with the same values."""
+        self.paged_decode_append(q, k_new, v_new, block_tables, seq_lens, out, scale, max_splits,
+                                 workspace, stream)
+        head, tail = self._decode_args(q, block_tables, seq_lens, out, scale, max_splits, workspace, stream)
+        fn, args = _lib.load().air_paged_decode_append, head + self._new_rows(q, k_new, v_new) + tail
+
+        def launch():
+            rc = fn(*args)
+            if rc:
+                _lib.check(rc, "air_paged_decode_append")
         return launch
 
     def prefill_workspace_size(self, n_q_heads, batch, max_q_len):

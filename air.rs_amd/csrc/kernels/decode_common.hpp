@@ -31,6 +31,10 @@ struct DecodeArgs {
     void *out;
     int32_t out_dtype;
     unsigned long long *errors;
+    // Matrix-core kernel, bf16 pools: the decode step's new K / V rows,
+    // [batch][n_kv_heads][head_dim] f32, written as each sequence's token
+    // seq_lens[b] - 1 by the wave that computes that token's tile (NULL: none)
+    const float *k_new, *v_new;
 };
 
 bool decode_mfma_supported(int dtype, int head_dim, int block_size, int group, int scale_group);

@@ -374,8 +374,11 @@ int plan_decode(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int32_t 
 hipError_t launch_decode(const air_kv_pool &p, hipStream_t s, const DecodePlan &plan, const void *q,
                          int32_t q_dtype, int32_t n_q_heads, const int32_t *tables,
                          const int32_t *lens, int32_t batch, int32_t max_blocks, float scale,
-                         void *workspace, void *out, int32_t out_dtype) {
+                         void *workspace, void *out, int32_t out_dtype, const float *k_new,
+                         const float *v_new) {
     DecodeArgs a;
+    a.k_new = plan.mfma ? k_new : nullptr;   // the vector kernels take no new rows
+    a.v_new = plan.mfma ? v_new : nullptr;
     a.q = q; a.q_dtype = q_dtype; a.n_q_heads = n_q_heads;
     a.tables = tables; a.lens = lens;
     a.batch = batch; a.max_blocks = max_blocks;

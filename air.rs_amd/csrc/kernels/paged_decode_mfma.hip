@@ -194,12 +194,17 @@ __device__ __forceinline__ int slice_chunk(int total, int slices) {
 // pre[b] = tiles (ceil(len / 16), len clamped to [0, max_blocks * BS]) of the
 // sequences before b, for b = 0..batch, in LDS.  All threads take part.
 template <int BS>
-__device__ void tile_prefix(const DecodeArgs &a, int32_t *pre, int32_t *wsum) {
+// long_seq (optional, B bits, zero on entry): bit b set when sequence b is
+// longer than its table.
+__device__ void tile_prefix(const DecodeArgs &a, int32_t *pre, int32_t *wsum, uint32_t *long_seq = nullptr) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int B = a.batch;
     const int64_t max_len = (int64_t)a.max_blocks * BS;
-    for (int b = tid; b < B; b += kThreads)
-        pre[b + 1] = (int32_t)((clamp_len(a.lens[b], max_len) + 15) / 16);
+    for (int b = tid; b < B; b += kThreads) {
+        const int32_t len = a.lens[b];
+        pre[b + 1] = (int32_t)((clamp_len(len, max_len) + 15) / 16);
+        if (long_seq && len > max_len) atomicOr(&long_seq[b >> 5], 1u << (b & 31));
+    }
     if (tid == 0) pre[0] = 0;
     __syncthreads();
     // each thread scans a run of `per` entries; runs are chained by a
@@ -253,6 +258,10 @@ template <int DT> struct Tile {
 };
 template <> struct Tile<AIR_KV_BF16> {
     u32x4 k[4], v[4];
+    // fused-append kernels, a sequence's last tile: the new token's f32 K
+    // (this lane's head_dim 32*ks + 8*g4 .. +8 as kn[2ks], kn[2ks + 1]) and
+    // V (head_dim vcol .. +8) rows
+    f32x4 kn[8], vn[2];
 };
 
 // Four 1-byte codes of one word times `s`, as two bf16 pairs.  The f32 value
@@ -320,11 +329,14 @@ constexpr int kernel_waves_per_simd(int dt, bool qf32) {
     return (qf32 && dt != AIR_KV_BF16) ? 2 : waves_per_simd(dt);
 }
 
-template <int D, int BS, bool QF32, int DT>
+// APPEND (bf16 pages): the launch also writes each sequence's new token,
+// a.k_new / a.v_new, as described at the fused append below.
+template <int D, int BS, bool QF32, int DT, bool APPEND>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kernel_waves_per_simd(DT, QF32))))
 void decode_mfma_kernel(DecodeArgs a) {
     static_assert(D == 128, "lane mappings assume head_dim 128");
     constexpr bool QUANT = DT != AIR_KV_BF16;
+    static_assert(!(APPEND && QUANT), "the fused append writes bf16 pages");
     constexpr int EB = QUANT ? 1 : 2;         // bytes per cache element
     constexpr int KSTEPS = D / 32;            // QK k-steps
     constexpr int DTILES = D / 16;            // PV output tiles along head_dim
@@ -343,7 +355,15 @@ void decode_mfma_kernel(DecodeArgs a) {
     // g4) holds row r16's scale of step g4; the S rows it needs are 4*g4..+3)
     __shared__ __align__(16) float s_ksc[kWaves][QUANT ? 64 : 4];
 
-    tile_prefix<BS>(a, s_pre, s_wsum);
+    // fused append: sequences longer than their table (they append nothing)
+    __shared__ uint32_t s_long[APPEND ? kMaxBatch / 32 : 1];
+    if constexpr (APPEND) {
+        for (int i = threadIdx.x; i < (a.batch + 31) / 32; i += kThreads) s_long[i] = 0;
+        __syncthreads();
+        tile_prefix<BS>(a, s_pre, s_wsum, s_long);
+    } else {
+        tile_prefix<BS>(a, s_pre, s_wsum);
+    }
     const int B = a.batch;
     const int total = s_pre[B];
     const int chunk = slice_chunk(total, a.slices);
@@ -367,6 +387,7 @@ void decode_mfma_kernel(DecodeArgs a) {
     // its sequence, tile index within the sequence, block id and valid tokens.
     int32_t tbl = 0, seq_l = 0, j_l = 0, nv_l = 0;
     uint64_t first_m = 0, last_m = 0;      // tile starts / ends a piece
+    uint64_t seqend_m = 0;                 // tile holds its sequence's last token
     auto load_window = [&](int c0) {
         const int t = c0 + lane < hi ? c0 + lane : hi - 1;
         const int bq = seq_of_tile(s_pre, B, t);
@@ -380,6 +401,8 @@ void decode_mfma_kernel(DecodeArgs a) {
         const bool valid = c0 + lane < hi;
         first_m = __ballot(valid && (t == lo || j == 0));
         last_m = __ballot(valid && (t + 1 == hi || t + 1 == s_pre[bq + 1]));
+        if constexpr (APPEND)
+            seqend_m = __ballot(valid && t + 1 == s_pre[bq + 1] && !((s_long[bq >> 5] >> (bq & 31)) & 1));
     };
 
     // ---- Q^T in the B-operand layout.  The QK contraction runs over head_dim
@@ -507,6 +530,26 @@ void decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
             for (int v = 0; v < 4; ++v)
                 t.v[v] = __builtin_amdgcn_raw_buffer_load_b128(rv, v_boff + v * 4 * D * 2, 0, kLoadAux);
+            if constexpr (APPEND) {
+                // a sequence's last tile: its new K / V rows load with the
+                // tile, so their latency hides behind the page loads
+                if (ok && ((seqend_m >> idx) & 1)) {
+                    const int bq = __builtin_amdgcn_readlane(seq_l, idx);
+                    const int64_t src = ((int64_t)bq * a.n_kv_heads + kh) * D;
+                    const __amdgpu_buffer_rsrc_t rkn = __builtin_amdgcn_make_buffer_rsrc(
+                        (void *)(a.k_new + src), (short)0, D * 4, kBufferWord3);
+                    const __amdgpu_buffer_rsrc_t rvn = __builtin_amdgcn_make_buffer_rsrc(
+                        (void *)(a.v_new + src), (short)0, D * 4, kBufferWord3);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        t.kn[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                rkn, (32 * (i >> 1) + 8 * g4 + 4 * (i & 1)) * 4, 0, 0));
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+                        t.vn[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                rvn, (vcol + 4 * i) * 4, 0, 0));
+                }
+            }
         }
         return ok;
     };
@@ -534,7 +577,7 @@ void decode_mfma_kernel(DecodeArgs a) {
         }
     };
 
-    auto compute_tile = [&](int k, int idx, const Tile<DT> &t, bool ok) {
+    auto compute_tile = [&](int k, int idx, Tile<DT> &t, bool ok) {
         const int bq = __builtin_amdgcn_readlane(seq_l, idx);
         if ((first_m >> idx) & 1) {          // a new sequence starts in this slice
             if (k != lo) load_q(bq);
@@ -548,6 +591,41 @@ void decode_mfma_kernel(DecodeArgs a) {
         // consumed on all paths and the loads in flight never need draining.
         if (!ok && lane == 0) atomicAdd(a.errors, 1ull);
         const int nv = ok ? __builtin_amdgcn_readlane(nv_l, idx) : 0;   // valid tokens
+        if constexpr (APPEND) {
+            // Fused append: the decode step's new token is row nv - 1 of its
+            // sequence's last tile, which this wave alone reads (a sequence
+            // longer than its table has no such tile: it appends nothing).
+            // Its K / V rows, loaded with the tile and rounded to bf16 as
+            // air_kv_append rounds them, replace that row in the tile's
+            // registers and are written to the page.
+            if (ok && ((seqend_m >> idx) & 1)) {
+                const int rn = nv - 1;
+                const int32_t blk = __builtin_amdgcn_readlane(tbl, idx);
+                const int jt = __builtin_amdgcn_readlane(j_l, idx);
+                const int64_t prow = ((int64_t)blk * a.n_kv_heads + kh) * BS + (16 * jt) % BS + rn;
+                auto pack8 = [](f32x4 x0, f32x4 x1) {
+                    return u32x4{(uint32_t)bf16_rne(x0[0]) | ((uint32_t)bf16_rne(x0[1]) << 16),
+                                 (uint32_t)bf16_rne(x0[2]) | ((uint32_t)bf16_rne(x0[3]) << 16),
+                                 (uint32_t)bf16_rne(x1[0]) | ((uint32_t)bf16_rne(x1[1]) << 16),
+                                 (uint32_t)bf16_rne(x1[2]) | ((uint32_t)bf16_rne(x1[3]) << 16)};
+                };
+                const bool krow = r16 == rn;     // K row rn: lanes (rn, g4), head_dim 32 ks + 8 g4 .. +8
+#pragma unroll
+                for (int ks = 0; ks < KSTEPS; ++ks) {
+                    const u32x4 w = pack8(t.kn[2 * ks], t.kn[2 * ks + 1]);
+                    t.k[ks] = krow ? w : t.k[ks];
+                    if (krow) *reinterpret_cast<u32x4 *>((uint16_t *)a.k_pages + prow * D + 32 * ks + 8 * g4) = w;
+                }
+                // V row rn: lanes with vrow = rn % 4, register set rn / 4
+                // (a select per set: a store to t.v[rn / 4] would index the
+                // tile dynamically, in private memory)
+                const bool vhit = vrow == (rn & 3);
+                const u32x4 w = pack8(t.vn[0], t.vn[1]);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) t.v[v] = (vhit && v == (rn >> 2)) ? w : t.v[v];
+                if (vhit) *reinterpret_cast<u32x4 *>((uint16_t *)a.v_pages + prow * D + vcol) = w;
+            }
+        }
         // lane holds S[token 4*g4 + i][head r16]
         float sc[4];
         if constexpr (QUANT) {
@@ -837,7 +915,14 @@ template <int BS, bool QF32, int DT>
 hipError_t launch_cfg(const DecodeArgs &a, hipStream_t s) {
     const int64_t waves = (int64_t)a.n_kv_heads * a.slices;
     const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves));
-    hipLaunchKernelGGL((decode_mfma_kernel<128, BS, QF32, DT>), grid, dim3(kThreads), 0, s, a);
+    if constexpr (DT == AIR_KV_BF16) {
+        if (a.k_new)
+            hipLaunchKernelGGL((decode_mfma_kernel<128, BS, QF32, DT, true>), grid, dim3(kThreads), 0, s, a);
+        else
+            hipLaunchKernelGGL((decode_mfma_kernel<128, BS, QF32, DT, false>), grid, dim3(kThreads), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((decode_mfma_kernel<128, BS, QF32, DT, false>), grid, dim3(kThreads), 0, s, a);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // Sequences average slices / batch pieces: past one round trip's worth,
@@ -925,6 +1010,11 @@ hipError_t launch_decode_mfma(const DecodeArgs &base, const DecodePlan &plan, vo
         a.out = (char *)base.out + q_row * (base.out_dtype == AIR_KV_F32 ? 4 : 2);
         a.tables = base.tables + (int64_t)b0 * a.max_blocks;
         a.lens = base.lens + b0;
+        if (base.k_new) {
+            const int64_t kv_row = (int64_t)b0 * a.n_kv_heads * 128;
+            a.k_new = base.k_new + kv_row;
+            a.v_new = base.v_new + kv_row;
+        }
         char *ws = (char *)workspace;
         a.prefix = (int32_t *)ws;
         ws += align256((size_t)(plan.batch_per_launch + 1) * 4);

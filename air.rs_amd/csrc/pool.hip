@@ -174,6 +174,36 @@ int air_paged_decode(air_kv_pool *p, void *stream, const void *q, int32_t q_dtyp
     return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "air_paged_decode launch");
 }
 
+int air_paged_decode_append(air_kv_pool *p, void *stream, const void *q, int32_t q_dtype, int32_t n_q_heads,
+                            const float *k_new, const float *v_new, const int32_t *block_tables,
+                            const int32_t *seq_lens, int32_t batch, int32_t max_blocks, float scale,
+                            int32_t max_splits, void *workspace, size_t ws_bytes, void *out,
+                            int32_t out_dtype) {
+    if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
+    airkv::DecodePlan plan;
+    if (int rc = airkv::plan_decode(*p, n_q_heads, batch, max_blocks, max_splits, &plan)) return rc;
+    if (!plan.mfma || p->desc.dtype != AIR_KV_BF16)
+        return fail(AIR_KV_E_INVALID_ARG,
+                    "fused append + decode needs a BF16 pool on the matrix-core decode (head_dim 128, "
+                    "group 1..16); use air_kv_append, then air_paged_decode");
+    if (batch == 0) return AIR_KV_OK;
+    if (!q || !k_new || !v_new || !block_tables || !seq_lens || !out || !workspace)
+        return fail(AIR_KV_E_INVALID_ARG, "NULL decode buffer");
+    if ((uintptr_t)k_new % 16 || (uintptr_t)v_new % 16)   // read as 16-byte vectors
+        return fail(AIR_KV_E_INVALID_ARG, "k_new and v_new must be 16-byte aligned");
+    if (ws_bytes < plan.ws_bytes)
+        return fail(AIR_KV_E_INVALID_ARG, "workspace %zu bytes < %zu needed", ws_bytes, plan.ws_bytes);
+    if (q_dtype != AIR_KV_F32 && q_dtype != AIR_KV_BF16)
+        return fail(AIR_KV_E_INVALID_ARG, "q_dtype must be F32 or BF16");
+    if (out_dtype != AIR_KV_F32 && out_dtype != AIR_KV_BF16)
+        return fail(AIR_KV_E_INVALID_ARG, "out_dtype must be F32 or BF16");
+    if (!(scale == scale)) return fail(AIR_KV_E_INVALID_ARG, "scale is NaN");
+    hipError_t e = airkv::launch_decode(*p, (hipStream_t)stream, plan, q, q_dtype, n_q_heads,
+                                        block_tables, seq_lens, batch, max_blocks, scale, workspace,
+                                        out, out_dtype, k_new, v_new);
+    return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "air_paged_decode_append launch");
+}
+
 int air_paged_prefill_workspace_size(const air_kv_pool *p, int32_t n_q_heads, int32_t batch,
                                      int32_t max_q_len, size_t *bytes) {
     if (!p || !bytes) return fail(AIR_KV_E_INVALID_ARG, "pool or bytes is NULL");

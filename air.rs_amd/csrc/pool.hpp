@@ -58,7 +58,8 @@ hipError_t launch_gather(const air_kv_pool &pool, hipStream_t s, const int32_t *
 hipError_t launch_decode(const air_kv_pool &pool, hipStream_t s, const DecodePlan &plan,
                          const void *q, int32_t q_dtype, int32_t n_q_heads, const int32_t *tables,
                          const int32_t *lens, int32_t batch, int32_t max_blocks, float scale,
-                         void *workspace, void *out, int32_t out_dtype);
+                         void *workspace, void *out, int32_t out_dtype,
+                         const float *k_new = nullptr, const float *v_new = nullptr);
 hipError_t launch_copy_blocks(const air_kv_pool &pool, hipStream_t s, const int32_t *src,
                               const int32_t *dst, int32_t n);
 hipError_t launch_stage_blocks(const air_kv_pool &pool, hipStream_t s, const int32_t *ids, int32_t n,

@@ -506,23 +506,31 @@ def main():
     appends = [pool.bind_append(step_k[i], step_v[i], step_slots[i]) for i in range(n_steps)]
     decodes = [pool.bind_decode(step_q[i], tables, step_lens[i], out, ws, max_splits=args.max_splits)
                for i in range(n_steps)]
+    # the step as one launch: step i's K/V rows land at token step_lens[i] - 1,
+    # the slot step_slots[i] names, written by the decode that reads them
+    fused = [pool.bind_decode_append(step_q[i], step_k[i], step_v[i], tables, step_lens[i], out, ws,
+                                     max_splits=args.max_splits) for i in range(n_steps)]
     torch.cuda.synchronize()
     log(f"setup {time.perf_counter() - t_setup:.1f} s")
 
-    # ---- timed steps: append + decode ------------------------------------
-    for i in range(args.warmup):
-        appends[i]()
-        decodes[i]()
-    torch.cuda.synchronize()
-    torch.cuda._sleep(20_000_000)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(args.warmup, n_steps):
-        appends[i]()
-        decodes[i]()
-    e1.record()
-    torch.cuda.synchronize()
-    ms_step = e0.elapsed_time(e1) / args.steps
+    def timed_steps(step_fns):
+        for i in range(args.warmup):
+            for f in step_fns[i]:
+                f()
+        torch.cuda.synchronize()
+        torch.cuda._sleep(20_000_000)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(args.warmup, n_steps):
+            for f in step_fns[i]:
+                f()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps
+
+    # ---- timed steps: append + decode in one launch, then as two calls ----
+    ms_step = timed_steps([(f,) for f in fused])
+    ms_two = timed_steps(list(zip(appends, decodes)))
     assert pool.error_count() == 0
 
     kv_b = cfg.n_kv_heads * cfg.head_dim * 2 * 2           # K+V bytes per cached token (bf16)
@@ -535,10 +543,14 @@ def main():
         qo = cfg.batch * cfg.n_q_heads * cfg.head_dim * (2 + 2)
         return tok * kv_b + 4 * pages + qo
 
-    append_bytes_step = cfg.batch * cfg.n_kv_heads * cfg.head_dim * 2 * (4 + 2) + 8 * cfg.batch
+    # new rows: f32 K and V read, bf16 written; the two-call step also reads
+    # the int64 slot mapping
+    append_bytes_step = cfg.batch * cfg.n_kv_heads * cfg.head_dim * 2 * (4 + 2)
     step_bytes = sum(decode_bytes(l) for l in lens_t) / args.steps + append_bytes_step
     value = step_bytes / (ms_step * 1e-3) / 1e9
-    log(f"step {ms_step * 1e3:.1f} us, {value:.0f} GB/s")
+    two_gbps = (step_bytes + 8 * cfg.batch) / (ms_two * 1e-3) / 1e9
+    extra_step = {"step_two_call_us": round(ms_two * 1e3, 2), "step_two_call_gbps": round(two_gbps, 1)}
+    log(f"step {ms_step * 1e3:.1f} us, {value:.0f} GB/s (two calls: {ms_two * 1e3:.1f} us, {two_gbps:.0f} GB/s)")
 
     # ---- decode kernel alone, final state ---------------------------------
     # calls alternate between the pool and a copy of it (same bytes, same
@@ -551,7 +563,7 @@ def main():
     dec_gbps = dec_bytes / (ms_dec * 1e-3) / 1e9
     log(f"decode {ms_dec * 1e3:.1f} us, {dec_gbps:.0f} GB/s ({dec_gbps / PEAK_HBM_GBPS:.1%} of peak)")
 
-    extra = {}
+    extra = dict(extra_step)
     if not args.only_decode:
         # gather of every sequence to contiguous bf16 [head][len][dim]
         lens_f = np.array(lens0) + n_steps
@@ -659,7 +671,8 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) K/V/Q, seeded U[512,4096] contexts, shuffled pool)",
         "config": {
-            "workload": "c2: append 1 token/seq + split-K paged decode, Llama-3-8B shape",
+            "workload": "c2: append 1 token/seq + split-K paged decode (one fused launch), "
+                        "Llama-3-8B shape",
             "batch": cfg.batch, "n_q_heads": cfg.n_q_heads, "n_kv_heads": cfg.n_kv_heads,
             "head_dim": cfg.head_dim, "block_size": cfg.block_size, "kv_dtype": "bf16",
             "q_dtype": "bf16", "out_dtype": "bf16", "ctx": "U[512,4096] seed 2",

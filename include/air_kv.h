@@ -264,6 +264,26 @@ int air_paged_decode(air_kv_pool *pool, void *stream, const void *q, int32_t q_d
                      int32_t batch, int32_t max_blocks, float scale, int32_t max_splits,
                      void *workspace, size_t ws_bytes, void *out, int32_t out_dtype);
 
+/* One decode step's append and attention in one launch: the same pages and
+ * outputs as air_kv_append of k_new / v_new (f32, [batch][n_kv_heads]
+ * [head_dim]) at each sequence's token seq_lens[b] - 1 -- the slot its block
+ * table gives that token, the slot SequenceManager::append_token hands out
+ * (src/paged_attention.rs:225-248) -- followed by air_paged_decode with the
+ * same arguments (the reference's decode step appends the token's K/V, then
+ * attends, src/model.rs:577, src/ops.rs:333-357).  Each new row is written by
+ * the wave that attends over it, so no launch orders the two.  Sequences of
+ * length 0 append nothing; a sequence longer than its table, or whose last
+ * block is outside the pool, appends nothing and is counted as by
+ * air_paged_decode.  BF16 pools on the matrix-core decode only (head_dim 128,
+ * group 1..16); other pools return AIR_KV_E_INVALID_ARG (use air_kv_append,
+ * then air_paged_decode).  k_new and v_new are 16-byte aligned device
+ * pointers.  The workspace is air_paged_decode's. */
+int air_paged_decode_append(air_kv_pool *pool, void *stream, const void *q, int32_t q_dtype,
+                            int32_t n_q_heads, const float *k_new, const float *v_new,
+                            const int32_t *block_tables, const int32_t *seq_lens, int32_t batch,
+                            int32_t max_blocks, float scale, int32_t max_splits, void *workspace,
+                            size_t ws_bytes, void *out, int32_t out_dtype);
+
 /* Bytes of the file-scope device array air_paged_decode_noalloc uses as its
  * workspace (one copy per GPU, held until the process ends). */
 #define AIR_KV_NOALLOC_SCRATCH_BYTES (32u << 20)

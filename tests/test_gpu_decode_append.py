@@ -1,0 +1,198 @@
+"""GPU tests of air_paged_decode_append, the decode step that appends each
+sequence's new K/V row and attends in one launch.  Through the C ABI, its
+pages and outputs equal those of air_kv_append followed by air_paged_decode
+(src/model.rs:577 appends, then src/ops.rs:333-357 attends) bit for bit, and
+its outputs stay within the oracle tolerance of the restated append + decode.
+Covered: sequences of 1 token and with full and partial last tiles,
+sequences whose last tile sits in a later slice than their first, a batch
+that takes two launches, GQA groups 4 and 8, bf16 and f32 queries, page sizes
+16 and 32, a sequence of length 0, a last block outside the pool, a sequence
+longer than its table, repeated calls, and the pools the fused path
+rejects."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import airkv
+from airkv import _lib, workloads
+from gpu_helpers import (assert_bits_equal, assert_floats_bit_equal, device_pool_for, host_pool_for, log,
+                         rel_err, torch_mod)
+
+pytestmark = pytest.mark.gpu
+
+TOL_BF16 = 1e-3
+
+
+def _to_dev(x):
+    torch = torch_mod()
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def _setup(cfg, ctx_lens, seed):
+    """Two device pools and the oracle pool holding every sequence's context;
+    the decode step's slots and new rows are returned unappended."""
+    w = workloads.build_prefill_decode(cfg, ctx_lens, seed=seed, decode_steps=1)
+    k, v = next(workloads.kv_rows(w.n_rows, cfg.n_kv_heads, cfg.head_dim, seed=seed + 1, chunk_rows=1 << 24))
+    pa, pb, host = device_pool_for(w), device_pool_for(w), host_pool_for(w)
+    off = 0
+    for slots in w.batches[:-1]:
+        n = len(slots)
+        for p in (pa, pb):
+            p.append(_to_dev(k[off:off + n]), _to_dev(v[off:off + n]), _to_dev(slots))
+        assert host.append(k[off:off + n], v[off:off + n], slots) == 0
+        off += n
+    k_new, v_new = k[off:], v[off:]
+    assert len(k_new) == cfg.batch
+    tables, lens = w.tables()
+    return w, pa, pb, host, tables, lens, k_new, v_new
+
+
+def _run_pair(cfg, pa, pb, host, tables, lens, k_new, v_new, q, q_f32, out_f32=True, append_mask=None):
+    """Pool a: air_kv_append + air_paged_decode; pool b: air_paged_decode_append.
+    append_mask[b] False: the reference path appends nothing for sequence b
+    (length 0, last block outside the pool, longer than its table)."""
+    torch = torch_mod()
+    bs = cfg.block_size
+    batch = len(lens)
+    if append_mask is None:
+        append_mask = np.ones(batch, bool)
+    idx = np.nonzero(append_mask)[0]
+    last = lens[idx] - 1
+    slots = (tables[idx, last // bs].astype(np.int64) * bs + last % bs).astype(np.int64)
+    qt = _to_dev(q)
+    if not q_f32:
+        qt = qt.to(torch.bfloat16)
+        q = qt.float().cpu().numpy()
+    odt = torch.float32 if out_f32 else torch.bfloat16
+    t, sl = _to_dev(tables), _to_dev(lens)
+    kn, vn = _to_dev(k_new), _to_dev(v_new)
+    ws = pa.new_workspace(cfg.n_q_heads, batch, tables.shape[1], cfg.max_splits)
+    out_a = torch.full((batch, cfg.n_q_heads, cfg.head_dim), float("nan"), dtype=odt, device="cuda")
+    out_b = torch.full_like(out_a, float("nan"))
+    if len(idx):
+        pa.append(_to_dev(k_new[idx]), _to_dev(v_new[idx]), _to_dev(slots))
+    pa.paged_decode(qt, t, sl, out_a, max_splits=cfg.max_splits, workspace=ws)
+    pb.paged_decode_append(qt, kn, vn, t, sl, out_b, max_splits=cfg.max_splits, workspace=ws)
+    torch.cuda.synchronize()
+    ka, va, _, _ = pa.snapshot()
+    kb, vb, _, _ = pb.snapshot()
+    assert_bits_equal(kb, ka, "k pages")
+    assert_bits_equal(vb, va, "v pages")
+    got_a, got_b = out_a.float().cpu().numpy(), out_b.float().cpu().numpy()
+    assert_floats_bit_equal(got_b, got_a, "decode output")
+    if len(idx):
+        assert host.append(k_new[idx], v_new[idx], slots) == 0
+    return q, got_b
+
+
+@pytest.mark.parametrize("n_q,bs,q_f32", [(32, 16, False), (64, 32, True), (32, 32, True), (64, 16, False)])
+def test_decode_append_matches_append_then_decode(n_q, bs, q_f32):
+    log(f"decode_append n_q={n_q} bs={bs} q_f32={q_f32}")
+    # context lengths before the step: 0 (a one-token sequence), tiles that
+    # the new token fills, starts or lands inside, and long sequences
+    ctx = [0, 15, 16, 30, 31, 32, 47, 100, 700, 1500, 2200, 40, 4095]
+    cfg = workloads.Config("decode_append", n_q, 8, 128, bs, airkv.BF16, len(ctx))
+    w, pa, pb, host, tables, lens, k_new, v_new = _setup(cfg, ctx, seed=71 + bs + n_q)
+    q = np.random.default_rng(73).standard_normal((cfg.batch, n_q, 128)).astype(np.float32)
+    q, got = _run_pair(cfg, pa, pb, host, tables, lens, k_new, v_new, q, q_f32)
+    want = host.paged_decode(q, tables, lens, chunk=64)
+    err = rel_err(got, want)
+    log(f"  identical to append + decode; rel err vs oracle {err:.2e}")
+    assert err <= TOL_BF16
+    assert pa.error_count() == 0 and pb.error_count() == 0
+
+
+def test_decode_append_multi_slice_sequences():
+    """Two long sequences over every slice: each sequence's last tile is
+    computed by a later slice than its first, and partial outputs merge."""
+    log("decode_append multi-slice")
+    ctx = [20000, 9000]
+    cfg = workloads.Config("decode_append_long", 32, 8, 128, 16, airkv.BF16, len(ctx))
+    w, pa, pb, host, tables, lens, k_new, v_new = _setup(cfg, ctx, seed=81)
+    q = np.random.default_rng(82).standard_normal((cfg.batch, 32, 128)).astype(np.float32)
+    q, got = _run_pair(cfg, pa, pb, host, tables, lens, k_new, v_new, q, q_f32=False, out_f32=False)
+    want = host.paged_decode(q, tables, lens, chunk=256)
+    err = rel_err(got, want)
+    log(f"  identical; rel err vs oracle {err:.2e}")
+    assert err <= TOL_BF16 + 2 ** -8       # bf16 output rounding
+
+
+def test_decode_append_batch_above_one_launch():
+    """4100 sequences: the host splits the batch over two launches, and the
+    second launch's new rows start at sequence 4096."""
+    log("decode_append batch 4100")
+    ctx = np.random.default_rng(111).integers(0, 40, 4100).tolist()
+    cfg = workloads.Config("decode_append_wide", 32, 8, 128, 16, airkv.BF16, len(ctx))
+    w, pa, pb, host, tables, lens, k_new, v_new = _setup(cfg, ctx, seed=112)
+    q = np.random.default_rng(113).standard_normal((cfg.batch, 32, 128)).astype(np.float32)
+    _run_pair(cfg, pa, pb, host, tables, lens, k_new, v_new, q, q_f32=False)
+    log("  identical to append + decode")
+
+
+def test_decode_append_skips_invalid_sequences():
+    """Length 0, a last block outside the pool and a sequence longer than its
+    table append nothing, as the reference path appends nothing for them."""
+    log("decode_append invalid sequences")
+    ctx = [50, 63, 200, 17, 90]
+    cfg = workloads.Config("decode_append_bad", 32, 8, 128, 16, airkv.BF16, len(ctx))
+    w, pa, pb, host, tables, lens, k_new, v_new = _setup(cfg, ctx, seed=91)
+    lens = lens.copy()
+    tables = tables.copy()
+    lens[1] = 0                                        # empty sequence
+    tables[2, (lens[2] - 1) // 16] = w.num_blocks + 7  # last block outside the pool
+    lens[3] = tables.shape[1] * 16 + 5                 # longer than its table
+    mask = np.array([True, False, False, False, True])
+    q = np.random.default_rng(92).standard_normal((cfg.batch, 32, 128)).astype(np.float32)
+    _run_pair(cfg, pa, pb, host, tables, lens, k_new, v_new, q, q_f32=True, append_mask=mask)
+    assert pb.error_count() > 0                        # the bad entries were counted
+    log("  identical to append + decode, errors counted")
+
+
+def test_decode_append_repeat_is_stable():
+    """A second identical call rewrites the same rows with the same values:
+    pages and outputs do not change (the bench loop relies on it)."""
+    torch = torch_mod()
+    log("decode_append repeat")
+    ctx = [33, 300, 1000]
+    cfg = workloads.Config("decode_append_rep", 64, 8, 128, 16, airkv.BF16, len(ctx))
+    w, pa, pb, host, tables, lens, k_new, v_new = _setup(cfg, ctx, seed=101)
+    q = _to_dev(np.random.default_rng(102).standard_normal((cfg.batch, 64, 128)).astype(np.float32))
+    t, sl, kn, vn = _to_dev(tables), _to_dev(lens), _to_dev(k_new), _to_dev(v_new)
+    ws = pb.new_workspace(64, cfg.batch, tables.shape[1])
+    out = torch.empty((cfg.batch, 64, 128), device="cuda")
+    launch = pb.bind_decode_append(q, kn, vn, t, sl, out, ws)
+    torch.cuda.synchronize()
+    first = out.cpu().numpy().copy()
+    k1, v1, _, _ = pb.snapshot()
+    for _ in range(3):
+        launch()
+    torch.cuda.synchronize()
+    assert_floats_bit_equal(out.cpu().numpy(), first, "repeated output")
+    k2, v2, _, _ = pb.snapshot()
+    assert_bits_equal(k2, k1, "k pages")
+    assert_bits_equal(v2, v1, "v pages")
+
+
+@pytest.mark.parametrize("dtype,n_q,head_dim,bs", [(airkv.INT8, 32, 128, 16), (airkv.FP8, 32, 128, 16),
+                                                    (airkv.BF16, 32, 64, 16), (airkv.F32, 32, 128, 16)])
+def test_decode_append_rejects_other_pools(dtype, n_q, head_dim, bs):
+    """1-byte and f32 pools and head_dim 64 decode on the two-call path: the
+    fused entry returns AIR_KV_E_INVALID_ARG before any device work."""
+    torch = torch_mod()
+    pool = airkv.KvPool(64, bs, 8, head_dim, dtype)
+    q = torch.zeros((2, n_q, head_dim), device="cuda")
+    kn = torch.zeros((2, 8, head_dim), device="cuda")
+    t = torch.zeros((2, 4), dtype=torch.int32, device="cuda")
+    sl = torch.full((2,), 3, dtype=torch.int32, device="cuda")
+    out = torch.empty_like(q)
+    with pytest.raises(_lib.AirKvError, match="fused append"):
+        pool.paged_decode_append(q, kn, kn, t, sl, out)
+    L = _lib.load()
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    rc = L.air_paged_decode_append(pool.handle, None, ctypes.c_void_p(q.data_ptr()), airkv.F32, n_q,
+                                   ctypes.c_void_p(kn.data_ptr()), ctypes.c_void_p(kn.data_ptr()),
+                                   ctypes.c_void_p(t.data_ptr()), ctypes.c_void_p(sl.data_ptr()), 2, 4,
+                                   ctypes.c_float(0.1), 64, ctypes.c_void_p(ws.data_ptr()), 1 << 20,
+                                   ctypes.c_void_p(out.data_ptr()), airkv.F32)
+    assert rc == _lib.AIR_KV_E_INVALID_ARG
