@@ -1016,10 +1016,15 @@ void prefill_pipe_kernel(PrefillArgs a) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) sc[i] = 8 * (i >> 2) + (i & 3) <= kq ? sc[i] : -INFINITY;
             }
-            float mt = fmaxf(sc[0], sc[1]);
-#pragma unroll
-            for (int i = 2; i < 16; ++i) mt = fmaxf(mt, sc[i]);
-            mt = fmaxf(mt, __shfl_xor(mt, 32)) * a.scale_log2;
+            // a tree of three-input maxima, then the lane 32 apart through
+            // the gfx950 lane swap (a VALU op; a shuffle is an LDS round trip
+            // on the path to the exponentials)
+            const float m0 = fmaxf(fmaxf(sc[0], sc[1]), sc[2]), m1 = fmaxf(fmaxf(sc[3], sc[4]), sc[5]);
+            const float m2 = fmaxf(fmaxf(sc[6], sc[7]), sc[8]), m3 = fmaxf(fmaxf(sc[9], sc[10]), sc[11]);
+            const float m4 = fmaxf(fmaxf(sc[12], sc[13]), sc[14]);
+            float mt = fmaxf(fmaxf(fmaxf(m0, m1), m2), fmaxf(fmaxf(m3, m4), sc[15]));
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+            mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * a.scale_log2;
             if (__ballot(mt > m_run + 8.0f) != 0ull) {
                 const float m_new = fmaxf(m_run, mt);
                 const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);   // 0 on the first tile
