@@ -503,13 +503,20 @@ def main():
                  for i in range(n_steps)]
     out = torch.empty(cfg.batch, cfg.n_q_heads, cfg.head_dim, device=dev, dtype=torch.bfloat16)
     ws = pool.new_workspace(cfg.n_q_heads, cfg.batch, max_blocks, args.max_splits)
-    appends = [pool.bind_append(step_k[i], step_v[i], step_slots[i]) for i in range(n_steps)]
-    decodes = [pool.bind_decode(step_q[i], tables, step_lens[i], out, ws, max_splits=args.max_splits)
+    # Steps alternate between the pool and a copy of it (same bytes, same
+    # tables), so no step finds pages the previous one left in the 256 MB
+    # MALL: in a model, the other layers' pages pass through it between two
+    # steps of one layer.  Each copy takes the appends of its own steps; the
+    # bytes every step moves are the same.
+    twin = twin_pool(torch, pool)
+    pools = (pool, twin)
+    appends = [pools[i % 2].bind_append(step_k[i], step_v[i], step_slots[i]) for i in range(n_steps)]
+    decodes = [pools[i % 2].bind_decode(step_q[i], tables, step_lens[i], out, ws, max_splits=args.max_splits)
                for i in range(n_steps)]
     # the step as one launch: step i's K/V rows land at token step_lens[i] - 1,
     # the slot step_slots[i] names, written by the decode that reads them
-    fused = [pool.bind_decode_append(step_q[i], step_k[i], step_v[i], tables, step_lens[i], out, ws,
-                                     max_splits=args.max_splits) for i in range(n_steps)]
+    fused = [pools[i % 2].bind_decode_append(step_q[i], step_k[i], step_v[i], tables, step_lens[i], out, ws,
+                                             max_splits=args.max_splits) for i in range(n_steps)]
     torch.cuda.synchronize()
     log(f"setup {time.perf_counter() - t_setup:.1f} s")
 
@@ -531,7 +538,7 @@ def main():
     # ---- timed steps: append + decode in one launch, then as two calls ----
     ms_step = timed_steps([(f,) for f in fused])
     ms_two = timed_steps(list(zip(appends, decodes)))
-    assert pool.error_count() == 0
+    assert pool.error_count() == 0 and twin.error_count() == 0
 
     kv_b = cfg.n_kv_heads * cfg.head_dim * 2 * 2           # K+V bytes per cached token (bf16)
     bs = cfg.block_size
@@ -555,7 +562,6 @@ def main():
     # ---- decode kernel alone, final state ---------------------------------
     # calls alternate between the pool and a copy of it (same bytes, same
     # tables), so no call finds pages the previous one left in the MALL
-    twin = twin_pool(torch, pool)
     last = alternating([p.bind_decode(step_q[-1], tables, step_lens[-1], out, ws, max_splits=args.max_splits)
                         for p in (pool, twin)])
     ms_dec = timed_loop(torch, last, args.kernel_iters)
