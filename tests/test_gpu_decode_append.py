@@ -5,7 +5,7 @@ pages and outputs equal those of air_kv_append followed by air_paged_decode
 its outputs stay within the oracle tolerance of the restated append + decode.
 Covered: sequences of 1 token and with full and partial last tiles,
 sequences whose last tile sits in a later slice than their first, a batch
-that takes two launches, GQA groups 4 and 8, bf16 and f32 queries, page sizes
+that takes two launches, GQA groups 1, 2, 4, 8 and 16, bf16 and f32 queries, page sizes
 16 and 32, a sequence of length 0, a last block outside the pool, a sequence
 longer than its table, repeated calls, and the pools the fused path
 rejects."""
@@ -86,7 +86,8 @@ def _run_pair(cfg, pa, pb, host, tables, lens, k_new, v_new, q, q_f32, out_f32=T
     return q, got_b
 
 
-@pytest.mark.parametrize("n_q,bs,q_f32", [(32, 16, False), (64, 32, True), (32, 32, True), (64, 16, False)])
+@pytest.mark.parametrize("n_q,bs,q_f32", [(32, 16, False), (64, 32, True), (32, 32, True), (64, 16, False),
+                                          (8, 16, False), (128, 32, True), (16, 32, False)])
 def test_decode_append_matches_append_then_decode(n_q, bs, q_f32):
     log(f"decode_append n_q={n_q} bs={bs} q_f32={q_f32}")
     # context lengths before the step: 0 (a one-token sequence), tiles that
