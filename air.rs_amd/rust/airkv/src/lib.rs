@@ -552,6 +552,26 @@ impl KvPool {
             .map(|_| ())
     }
 
+    /// One decode step in one launch (bf16 pools, head_dim 128, group
+    /// 1..16): appends `k_new` / `v_new` (f32 `[batch][n_kv_heads][head_dim]`,
+    /// 16-byte aligned) as each sequence's token `lens[b] - 1`, then attends
+    /// as [`KvPool::paged_decode`] (src/model.rs:569-577).
+    ///
+    /// # Safety
+    /// As [`KvPool::paged_decode`]; `k_new` / `v_new` are device arrays of
+    /// `batch * n_kv_heads * head_dim` floats.
+    #[allow(clippy::too_many_arguments)]
+    pub unsafe fn paged_decode_append(&self, stream: Stream, q: *const c_void, q_dtype: KvDtype,
+                                      n_q_heads: usize, k_new: *const f32, v_new: *const f32,
+                                      tables: *const i32, lens: *const i32, batch: usize, max_blocks: usize,
+                                      scale: f32, max_splits: usize, workspace: *mut c_void, ws_bytes: usize,
+                                      out: *mut c_void, out_dtype: KvDtype) -> Result<(), AirKvError> {
+        check(sys::air_paged_decode_append(self.raw, stream, q, q_dtype as i32, n_q_heads as i32, k_new, v_new,
+                                           tables, lens, batch as i32, max_blocks as i32, scale,
+                                           max_splits as i32, workspace, ws_bytes, out, out_dtype as i32))
+            .map(|_| ())
+    }
+
     /// The same decode with the library's own workspace array (for callers
     /// that cannot allocate device memory).
     ///
