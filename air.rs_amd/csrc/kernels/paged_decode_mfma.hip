@@ -323,11 +323,9 @@ constexpr int waves_per_simd(int dt) {
                               : AIRKV_DECODE_QWAVES_PER_EU;
 }
 
-// f32 queries on 1-byte pages carry the hi + lo query halves as well and do
-// not fit the 3-wave register budget: they are built for 2 waves per SIMD.
-constexpr int kernel_waves_per_simd(int dt, bool qf32) {
-    return (qf32 && dt != AIR_KV_BF16) ? 2 : waves_per_simd(dt);
-}
+// Every build of a page dtype has the same register budget (f32 queries on
+// 1-byte pages are rounded to bf16 once, below, so they carry no lo halves).
+constexpr int kernel_waves_per_simd(int dt, bool) { return waves_per_simd(dt); }
 
 // APPEND (bf16 pages): the launch also writes each sequence's new token,
 // a.k_new / a.v_new, as described at the fused append below.
@@ -429,7 +427,20 @@ void decode_mfma_kernel(DecodeArgs a) {
             // 16*(g4 & 1) + 8*(g4 >> 1) .. +8
             const int qoff = (QUANT && AIRKV_DECODE_K16) ? (r16 * D + 16 * (g4 & 1) + 8 * (g4 >> 1)) * QB
                                                          : (r16 * D + 8 * g4) * QB;
-            if constexpr (QF32) {
+            if constexpr (QF32 && QUANT) {
+                // 1-byte pages: the query rounded to bf16 once.  Its error
+                // (2^-9 relative per element) is an order below the codes' own
+                // quantization and the 2e-2 tolerance of these pools; the hi
+                // + lo products of bf16 pages would cost a second product per
+                // k-step and a third of the waves.
+                const u32x4 x0 = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + step * ks, 0, 0);
+                const u32x4 x1 = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + step * ks + 16, 0, 0);
+                qhi[ks] = u32x4{bf16_bits(__uint_as_float(x0[0])) | (bf16_bits(__uint_as_float(x0[1])) << 16),
+                                bf16_bits(__uint_as_float(x0[2])) | (bf16_bits(__uint_as_float(x0[3])) << 16),
+                                bf16_bits(__uint_as_float(x1[0])) | (bf16_bits(__uint_as_float(x1[1])) << 16),
+                                bf16_bits(__uint_as_float(x1[2])) | (bf16_bits(__uint_as_float(x1[3])) << 16)};
+                qlo[ks] = u32x4{0, 0, 0, 0};
+            } else if constexpr (QF32) {
                 const u32x4 x0 = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + step * ks, 0, 0);
                 const u32x4 x1 = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff + step * ks + 16, 0, 0);
                 const uint32_t x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
@@ -453,8 +464,7 @@ void decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     sum += __uint_as_float(qhi[ks][j] << 16) + __uint_as_float(qhi[ks][j] & 0xFFFF0000u);
-                    if constexpr (QF32)
-                        sum += __uint_as_float(qlo[ks][j] << 16) + __uint_as_float(qlo[ks][j] & 0xFFFF0000u);
+
                 }
                 sum += __shfl_xor(sum, 16);
                 sum += __shfl_xor(sum, 32);
@@ -662,7 +672,7 @@ void decode_mfma_kernel(DecodeArgs a) {
             for (int ks = 0; ks < KSTEPS; ++ks) {
                 const float b0 = DT == AIR_KV_INT8 ? qbias[ks] : 0.0f;
                 f32x4 p = mfma_qk(codes_bf16<DT>(kc[ks]), qhi[ks], f32x4{b0, b0, b0, b0});
-                if constexpr (QF32) p = mfma_qk(codes_bf16<DT>(kc[ks]), qlo[ks], p);
+
                 // the step's scales of this lane's tokens 4*g4 .. +3
                 const f32x4 ksc = *reinterpret_cast<const f32x4 *>(&s_ksc[wave][ks * 16 + 4 * g4]);
 #pragma unroll
@@ -986,9 +996,8 @@ int plan_decode_mfma(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int
     plan->dtype = p.desc.dtype;
     plan->part_tokens = plan->num_parts = 0;
     plan->slices = (int32_t)slices;
-    // f32 queries on 1-byte pages run a kernel built for fewer waves per
-    // SIMD: their slices match what is resident at once, and the workspace
-    // (sized for plan->slices) holds them.
+    // the f32-query build's slices (what is resident at once; the workspace,
+    // sized for plan->slices, holds them whenever that build runs fewer waves)
     plan->slices_qf32 = (int32_t)slices_for(kernel_waves_per_simd(p.desc.dtype, true));
     plan->batch_per_launch = nb;
     plan->slots = (int32_t)(slices + nb);

@@ -763,7 +763,7 @@ void prefill_pipe_kernel(PrefillArgs a) {
     // significant bits): V converted (bf16 pages) or dequantized (1-byte
     // pages) to f16 on its way to LDS and probabilities <= 2^8 rounded to
     // f16, one PV product per tile; 1-byte pages also take their keys
-    // dequantized to f16 and the queries as f16 (f32 queries as f16 hi + lo),
+    // dequantized to f16 and the queries as f16 (f32 queries rounded once),
     // one S^T product per step instead of the key's bf16 hi + lo pair.  A work
     // item whose f16 result is not finite (a value beyond f16's 65504) or
     // whose every output of a query row is below 2^-14 in magnitude (values
@@ -949,11 +949,14 @@ void prefill_pipe_kernel(PrefillArgs a) {
                     const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        if constexpr (F16Q) {          // f16 hi + lo: ~22 significant bits
-                            const uint32_t hf = f16_pair(x[2 * j], x[2 * j + 1]);
-                            const f32x2 hv = __builtin_convertvector(__builtin_bit_cast(f16x2, hf), f32x2);
-                            qhi[ks][j] = hf;
-                            qlo[ks][j] = f16_pair(x[2 * j] - hv[0], x[2 * j + 1] - hv[1]);
+                        if constexpr (F16Q) {
+                            // f16 pass, 1-byte pages: the query rounded to f16
+                            // once (11 significant bits, finer than a bf16
+                            // query, which the same pass takes exactly); a
+                            // value beyond f16's range sends the work item to
+                            // the exact pass, which splits it into hi + lo
+                            qhi[ks][j] = f16_pair(x[2 * j], x[2 * j + 1]);
+                            qlo[ks][j] = 0u;
                         } else {
                             uint32_t hb, lb;
                             split_pair(x[2 * j], x[2 * j + 1], hb, lb);
@@ -976,7 +979,7 @@ void prefill_pipe_kernel(PrefillArgs a) {
 #pragma unroll
             for (int ks = 0; ks < D / 16; ++ks) {
                 asm volatile("" ::"v"(qhi[ks]));
-                if constexpr (QF32) asm volatile("" ::"v"(qlo[ks]));
+                if constexpr (QF32 && !F16Q) asm volatile("" ::"v"(qlo[ks]));
             }
         };
 
@@ -994,7 +997,6 @@ void prefill_pipe_kernel(PrefillArgs a) {
                 const u32x4 kA = *reinterpret_cast<const u32x4 *>(ks_ + r32 * KPITCH + (2 * ks + hh) * 16);
                 if constexpr (F16K) {
                     s = mfma32_f16(kA, qhi[ks], s);
-                    if constexpr (QF32) s = mfma32_f16(kA, qlo[ks], s);
                     continue;
                 }
                 s = mfma32(kA, qhi[ks], s);

@@ -10,7 +10,8 @@ import pytest
 import airkv
 import oracle
 from airkv import workloads
-from gpu_helpers import (device_pool_for, host_pool_for, log, rel_err, run_appends, torch_mod)
+from gpu_helpers import (assert_floats_bit_equal, device_pool_for, host_pool_for, log, rel_err, run_appends,
+                         torch_mod)
 
 pytestmark = pytest.mark.gpu
 
@@ -180,6 +181,27 @@ def test_bf16_group16_query_and_output_dtypes(q_bf16, out_bf16):
     err = rel_err(got, want)
     log(f"g16 q_bf16={q_bf16} out_bf16={out_bf16} rel err {err:.2e}")
     assert err <= (4e-3 if out_bf16 else 1e-3)
+
+
+@pytest.mark.parametrize("dtype,bs", [(airkv.INT8, 16), (airkv.FP8, 32)])
+def test_one_byte_pages_f32_queries(dtype, bs):
+    """1-byte pools round f32 queries to bf16 once: the output equals, bit for
+    bit, that of the same queries given as bf16, and stays within the 2e-2
+    tolerance of the oracle's f32-query attention (c3 / c4 head geometry,
+    outlier channels)."""
+    torch = torch_mod()
+    cfg = workloads.Config("q32", 64, 8, 128, bs, dtype, 4)
+    outl = workloads.outlier_channels(8, 128, seed=9)
+    got, want, (pool, host, tables, lens, q) = _decode_case(cfg, [300, 1700, 4100, 9000], seed=48,
+                                                           q_bf16=False, outliers=outl)
+    err = rel_err(got, want)
+    qb = torch.from_numpy(q).cuda().to(torch.bfloat16)
+    out_b = torch.zeros(q.shape, dtype=torch.float32, device="cuda")
+    pool.paged_decode(qb, torch.from_numpy(tables).cuda(), torch.from_numpy(lens).cuda(), out_b)
+    torch.cuda.synchronize()
+    assert_floats_bit_equal(got, out_b.cpu().numpy(), "f32 queries against the same queries in bf16")
+    log(f"1-byte dtype={dtype} f32 queries rel err {err:.2e}")
+    assert err <= TOL[dtype]
 
 
 def test_workspace_reuse_across_calls():
