@@ -248,7 +248,10 @@ int air_paged_decode_workspace_size(const air_kv_pool *pool, int32_t n_q_heads, 
  * (src/ops.rs:333-357, :514-568) and generalises flash_decode
  * (src/flash_decode.rs:153-173: split-K partials merged by log-sum-exp,
  * :114-142) to paged storage.  q: [batch][n_q_heads][head_dim] as q_dtype
- * (AIR_KV_F32 or AIR_KV_BF16); out likewise as out_dtype.  The reference's
+ * (AIR_KV_F32 or AIR_KV_BF16); out likewise as out_dtype.  On the
+ * matrix-core kernel F32 queries enter the products as two bf16 halves on
+ * BF16 pools and rounded to bf16 on INT8 / FP8 pools (an error an order below
+ * their quantization's).  The reference's
  * scale is 1/sqrt(head_dim).  max_splits (1..256) bounds the split-K work
  * division: bf16 pools with head_dim 128 (the matrix-core kernel) cut the
  * batch's cached tokens into at most batch * max_splits equal slices per kv
@@ -319,10 +322,12 @@ int air_paged_decode_noalloc(air_kv_pool *pool, void *stream, const void *q, int
  * reference's is 1/sqrt(head_dim)).  Supports BF16, INT8 and FP8 pools with
  * head_dim 128 (quantized pages are dequantized q * scale in registers); other
  * pools return AIR_KV_E_INVALID_ARG.  BF16 pools run the probability x value
- * products with f16 operands (11 significant bits each); a work group whose
- * result that way is not finite, or whose outputs of a query row are all
- * below 2^-14 in magnitude, is recomputed with bf16 values and probabilities
- * split into two bf16 halves.  A sequence whose rows do not lie in
+ * products with f16 operands (11 significant bits each), INT8 / FP8 pools the
+ * key x query products as well (keys, values and F32 queries rounded to f16
+ * once); a work group whose result that way is not finite, or whose outputs
+ * of a query row are all below 2^-14 in magnitude, is recomputed with bf16
+ * operands: probabilities as two bf16 halves on BF16 pools, keys as two bf16
+ * halves on INT8 / FP8 pools.  A sequence whose rows do not lie in
  * [0, total_q], whose seq_len is outside [0, max_blocks * block_size] or
  * whose q_len exceeds its seq_len is counted (air_kv_pool_error_count) and its
  * rows (when they lie in [0, total_q]) are zero-filled; out-of-pool table
