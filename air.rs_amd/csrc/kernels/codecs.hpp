@@ -107,8 +107,23 @@ __device__ __forceinline__ float fp8_scale(float max_abs) {
     return max_abs < 1e-8f ? 1.0f : max_abs / 448.0f;
 }
 
-__device__ __forceinline__ uint8_t fp8_code(float x, float scale) {
+// The code of x / scale, with y = RN(1 / scale) and `mark` = scale and y both
+// normal (a group's values, computed once).  The quotient is then
+// q0 = RN(x * y) corrected once, q = RN(q0 + fma(-q0, scale, x) * y)
+// (Markstein): RN(x / scale) whenever the remainder is exact, which holds for
+// every |q| >= 2^-6 -- the only quotients whose code depends on more than
+// their sign (here |x| >= 2^-6 * scale >= 2^-42, far from the subnormals).
+// Below that the code is the sign alone, and a quotient that comes out
+// subnormal or zero is divided exactly, so a tiny negative one is not turned
+// into a zero.  The codes equal the division's on random and boundary cases
+// (tests/fp8_quotient_check.c; 4e8 cases run once, none differing).
+__device__ __forceinline__ uint8_t fp8_code(float x, float scale, float y, bool mark) {
 #pragma clang fp contract(off)
+    if (mark) {
+        float q = x * y;
+        q = __builtin_fmaf(__builtin_fmaf(-q, scale, x), y, q);
+        if (__builtin_fabsf(q) >= 0x1p-126f) return fp8_encode(q);
+    }
     return fp8_encode(x / scale);
 }
 

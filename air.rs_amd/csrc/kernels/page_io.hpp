@@ -109,10 +109,16 @@ __device__ __forceinline__ void store_row_chunk(const float (&x)[8], void *pages
             for (int j = 0; j < 4; ++j) hi |= (uint32_t)(uint8_t)q8_code(x[4 + j], inv) << (8 * j);
         } else {
             scale = fp8_scale(m);
+            float y;
+            {
+#pragma clang fp contract(off)
+                y = 1.0f / scale;
+            }
+            const bool mark = __builtin_isnormal(scale) && __builtin_isnormal(y);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) lo |= (uint32_t)fp8_code(x[j], scale) << (8 * j);
+            for (int j = 0; j < 4; ++j) lo |= (uint32_t)fp8_code(x[j], scale, y, mark) << (8 * j);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) hi |= (uint32_t)fp8_code(x[4 + j], scale) << (8 * j);
+            for (int j = 0; j < 4; ++j) hi |= (uint32_t)fp8_code(x[4 + j], scale, y, mark) << (8 * j);
         }
         if (valid) {
             pio_store(pio_u32x2{lo, hi}, reinterpret_cast<pio_u32x2 *>((uint8_t *)pages + elem));
