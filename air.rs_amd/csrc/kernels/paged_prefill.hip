@@ -330,6 +330,21 @@ __device__ __forceinline__ int slot_pieces(int64_t tiles, int64_t T, int ns_max)
     return (int)(n < ns_max ? n : ns_max);
 }
 
+// Whether sequence b's rows and length are consistent: 0 <= cu_q[b] <=
+// cu_q[b + 1] <= total_q, 0 <= seq_len <= max_blocks * block_size and
+// q_len <= seq_len.  The one test every prefill kernel applies: an
+// inconsistent sequence is counted and zero-filled by its first workgroup,
+// never split into pieces and never written by the merge.
+__device__ __forceinline__ bool prefill_rows_ok(const PrefillArgs &a, int b) {
+    const int32_t q0 = a.cu_q[b], q1 = a.cu_q[b + 1];
+    return q0 >= 0 && q1 >= q0 && q1 <= a.total_q;
+}
+__device__ __forceinline__ bool prefill_seq_ok(const PrefillArgs &a, int b) {
+    const int64_t len = a.lens[b];
+    const int64_t qlen = (int64_t)a.cu_q[b + 1] - a.cu_q[b];
+    return prefill_rows_ok(a, b) && len >= 0 && len <= a.max_len && qlen <= len;
+}
+
 // The plan of a split launch: one int2 per grid row {item, slot info}.
 __device__ __forceinline__ int2 *prefill_plan_table(const PrefillArgs &a) {
     return reinterpret_cast<int2 *>((uint8_t *)a.ws + 64 + 16 * (int64_t)a.ws_units);
@@ -449,8 +464,10 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillArgs 
     const int nz = a.nz, nsm = a.ns_max;
     for (int i = tid; i < a.batch; i += kPlanThreads) {
         slen[i] = a.lens[i];
-        const int64_t ql = (int64_t)a.cu_q[i + 1] - a.cu_q[i];
-        sq[i] = ql < 0 ? 0 : ql > 0x7fffffff ? 0x7fffffff : (int)ql;
+        // an inconsistent sequence plans as one with no rows: no keys, one
+        // piece, never split (its first workgroup counts and zero-fills it)
+        const int64_t ql = prefill_seq_ok(a, i) ? (int64_t)a.cu_q[i + 1] - a.cu_q[i] : 0;
+        sq[i] = ql > 0x7fffffff ? 0x7fffffff : (int)ql;
     }
     if (tid < 256) hist[tid] = cnt[tid] = 0;
     __syncthreads();
@@ -537,13 +554,11 @@ template <int BS>
 __device__ bool prefill_begin(const PrefillArgs &a, const PrefillSlot &sl, int32_t &q0, int &qlen, int64_t &len) {
     const int b = sl.b, kh = sl.kh, tid = threadIdx.x;
     const int G = a.group;
-    const int64_t max_len = (int64_t)a.max_blocks * BS;
     q0 = a.cu_q[b];
-    const int32_t q1 = a.cu_q[b + 1];
     len = a.lens[b];
-    qlen = q1 - q0;
-    const bool rows_ok = q0 >= 0 && q1 >= q0 && q1 <= a.total_q;
-    const bool seq_ok = rows_ok && len >= 0 && len <= max_len && qlen <= len;
+    qlen = a.cu_q[b + 1] - q0;
+    const bool rows_ok = prefill_rows_ok(a, b);
+    const bool seq_ok = prefill_seq_ok(a, b);
     const int32_t *tbl = a.tables + (int64_t)b * a.max_blocks;
     if (sl.z == 0 && sl.p == 0 && kh == 0) {
         if (!seq_ok) {
@@ -735,6 +750,7 @@ __global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(PrefillArg
         if (p0 + kMergeBatch >= ns) break;
     }
     if (b < 0 || b >= a.batch || z < 0 || z >= a.nz) return;
+    if (!prefill_seq_ok(a, b)) return;                  // the plan never splits one: defence only
     const int G = a.group;
     const int32_t q0 = a.cu_q[b];
     const int qlen = a.cu_q[b + 1] - q0;
@@ -1297,6 +1313,7 @@ hipError_t launch_prefill(PrefillArgs a, int dtype, int block_size, int32_t max_
     if (pl.nz < 1) return hipErrorInvalidConfiguration;
     a.nz = pl.nz;
     a.slots = 2 * cus;
+    a.max_len = (int64_t)a.max_blocks * block_size;
     if (!a.ws || a.ws_units < 1 || pl.ns_max == 1) {
         a.ns_max = 1;
         a.ws = nullptr;

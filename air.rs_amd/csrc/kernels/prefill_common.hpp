@@ -12,6 +12,7 @@ struct PrefillArgs {
     const int32_t *cu_q;           // [batch + 1] query row offsets
     const int32_t *tables, *lens;  // [batch][max_blocks], [batch]
     int32_t batch, max_blocks, total_q;
+    int64_t max_len;               // max_blocks * block_size (set by launch_prefill)
     float scale_log2;              // softmax scale * log2(e)
     int32_t n_kv_heads, group, scale_group;
     int64_t num_blocks;

@@ -306,6 +306,75 @@ def test_prefill_invalid_sequences_counted_and_zeroed():
     assert torch.isfinite(out1).all()
 
 
+def _long_split_pool(bs=16, L=12288, seed=161):
+    torch = torch_mod()
+    cfg = workloads.Config("split_bad", 32, 8, 128, bs, airkv.BF16, 1)
+    w = workloads.build_prefill_decode(cfg, [L], seed, decode_steps=0)
+    k, v = next(workloads.kv_rows(w.n_rows, 8, 128, seed=seed + 1, device="cuda", chunk_rows=1 << 24))
+    pool = device_pool_for(w)
+    off = 0
+    for slots in w.batches:
+        n = len(slots)
+        pool.append(k[off:off + n].contiguous(), v[off:off + n].contiguous(), torch.from_numpy(slots).cuda())
+        off += n
+    tables, lens = w.tables()
+    return pool, tables, lens
+
+
+def test_prefill_key_split_skips_sequence_longer_than_its_table():
+    """A 512-row chunk of one 12288-token sequence is a launch the key split
+    cuts (fewer work groups than resident slots), but with seq_len one past
+    its table the sequence is inconsistent: it must be counted once and its
+    rows zero-filled, with no piece planned for it, so a workspace full of
+    NaN bytes is never folded into its rows."""
+    torch = torch_mod()
+    C = 512
+    pool, tables, lens = _long_split_pool()
+    bad = lens.copy()
+    bad[0] = tables.shape[1] * 16 + 1
+    cu = torch.tensor([0, C], dtype=torch.int32, device="cuda")
+    q = torch.randn((C, 32, 128), device="cuda").to(torch.bfloat16)
+    ws = torch.full((pool.prefill_workspace_size(32, 1, C),), 0xFF, dtype=torch.uint8, device="cuda")
+    assert ws.numel() > 0
+    out = torch.full((C, 32, 128), 7.0, device="cuda")
+    pool.error_count(reset=True)
+    pool.paged_prefill(q, cu, torch.from_numpy(tables).cuda(), torch.from_numpy(bad).cuda(), out,
+                       max_q_len=C, workspace=ws)
+    torch.cuda.synchronize()
+    assert pool.error_count(reset=True) == 1
+    assert int(ws[:4].view(torch.int32).item()) == 0       # no split slot planned
+    assert bool((out == 0.0).all())
+    # the same launch with the true length is split and finite
+    ws2 = torch.full_like(ws, 0xFF)
+    pool.paged_prefill(q, cu, torch.from_numpy(tables).cuda(), torch.from_numpy(lens).cuda(), out,
+                       max_q_len=C, workspace=ws2)
+    torch.cuda.synchronize()
+    assert pool.error_count(reset=True) == 0
+    assert int(ws2[:4].view(torch.int32).item()) > 0
+    assert bool(torch.isfinite(out).all())
+
+
+def test_prefill_key_split_rows_past_total_q_write_nothing():
+    """cu_q = [0, 512] with only 448 query rows: the rows are inconsistent, so
+    the sequence is counted, nothing is split, and nothing is written -- the
+    guard rows that follow `out` in the same allocation keep their bytes."""
+    torch = torch_mod()
+    C, T = 512, 448
+    pool, tables, lens = _long_split_pool(seed=171)
+    cu = torch.tensor([0, C], dtype=torch.int32, device="cuda")
+    q = torch.randn((T, 32, 128), device="cuda").to(torch.bfloat16)
+    big = torch.full((C, 32, 128), 7.0, device="cuda")
+    out = big[:T]
+    ws = torch.full((pool.prefill_workspace_size(32, 1, C),), 0xFF, dtype=torch.uint8, device="cuda")
+    pool.error_count(reset=True)
+    pool.paged_prefill(q, cu, torch.from_numpy(tables).cuda(), torch.from_numpy(lens).cuda(), out,
+                       max_q_len=C, workspace=ws)
+    torch.cuda.synchronize()
+    assert pool.error_count(reset=True) == 1
+    assert int(ws[:4].view(torch.int32).item()) == 0
+    assert bool((big == 7.0).all())                      # rows inside and past `out` untouched
+
+
 def test_prefill_rejects_unsupported_pools_and_args():
     torch = torch_mod()
     L = airkv.load()
