@@ -43,6 +43,20 @@ def _dev(t, dtype, what, shape=None):
     return ctypes.c_void_p(t.data_ptr())
 
 
+def _launcher(fn, args, name, keep):
+    """A zero-argument launcher of fn(*args).  args holds raw device
+    addresses, so the launcher also holds `keep`, every tensor (and stream)
+    those addresses point into: they live as long as the launcher does.
+    Without that, a tensor the caller dropped would return to torch's caching
+    allocator while the launcher still wrote through its address."""
+    def launch():
+        rc = fn(*args)
+        if rc:
+            _lib.check(rc, name)
+    launch.keep = tuple(keep)
+    return launch
+
+
 _TORCH_OF = {F32: "float32", BF16: "bfloat16"}
 
 
@@ -190,30 +204,25 @@ class KvPool:
                     stream=None):
         """Validate once, return a zero-argument launcher (for timing loops:
         no per-call Python checks between launches)."""
+        if workspace is None:
+            workspace = self.new_workspace(q.shape[1], q.shape[0], block_tables.shape[1], max_splits)
         self.paged_decode(q, block_tables, seq_lens, out, scale, max_splits, workspace, stream)
         head, tail = self._decode_args(q, block_tables, seq_lens, out, scale, max_splits, workspace, stream)
-        fn, args = _lib.load().air_paged_decode, head + tail
-
-        def launch():
-            rc = fn(*args)
-            if rc:
-                _lib.check(rc, "air_paged_decode")
-        return launch
+        return _launcher(_lib.load().air_paged_decode, head + tail, "air_paged_decode",
+                         (q, block_tables, seq_lens, out, workspace, stream))
 
     def bind_decode_append(self, q, k_new, v_new, block_tables, seq_lens, out, workspace, scale=None,
                            max_splits=64, stream=None):
         """bind_decode for paged_decode_append.  The launcher appends on every
         call: a timing loop rewrites the same rows with the same values."""
+        if workspace is None:
+            workspace = self.new_workspace(q.shape[1], q.shape[0], block_tables.shape[1], max_splits)
         self.paged_decode_append(q, k_new, v_new, block_tables, seq_lens, out, scale, max_splits,
                                  workspace, stream)
         head, tail = self._decode_args(q, block_tables, seq_lens, out, scale, max_splits, workspace, stream)
-        fn, args = _lib.load().air_paged_decode_append, head + self._new_rows(q, k_new, v_new) + tail
-
-        def launch():
-            rc = fn(*args)
-            if rc:
-                _lib.check(rc, "air_paged_decode_append")
-        return launch
+        return _launcher(_lib.load().air_paged_decode_append, head + self._new_rows(q, k_new, v_new) + tail,
+                         "air_paged_decode_append",
+                         (q, k_new, v_new, block_tables, seq_lens, out, workspace, stream))
 
     def prefill_workspace_size(self, n_q_heads, batch, max_q_len):
         """Bytes of the key-split workspace air_paged_prefill takes for this shape."""
@@ -280,11 +289,7 @@ class KvPool:
                                       workspace, split)
         fn = _lib.load().air_paged_prefill
         _lib.check(fn(*args), "air_paged_prefill")
-
-        def launch():
-            rc = fn(*args)
-            if rc:
-                _lib.check(rc, "air_paged_prefill")
+        launch = _launcher(fn, args, "air_paged_prefill", (q, cu_q, block_tables, seq_lens, out, ws, stream))
         launch.workspace = ws
         return launch
 
@@ -295,12 +300,7 @@ class KvPool:
         args = (self.handle, _stream_ptr(stream), ctypes.c_void_p(k.data_ptr()),
                 ctypes.c_void_p(v.data_ptr()), ctypes.c_void_p(slot_mapping.data_ptr()),
                 slot_mapping.shape[0])
-
-        def launch():
-            rc = fn(*args)
-            if rc:
-                _lib.check(rc, "air_kv_append")
-        return launch
+        return _launcher(fn, args, "air_kv_append", (k, v, slot_mapping, stream))
 
     def bind_gather(self, block_tables, seq_lens, out_offsets, out_k, out_v, out_dtype=None,
                     layout=LAYOUT_HEAD_MAJOR, stream=None):
@@ -313,12 +313,7 @@ class KvPool:
                 ctypes.c_void_p(seq_lens.data_ptr()), ctypes.c_void_p(out_offsets.data_ptr()),
                 block_tables.shape[0], block_tables.shape[1], ctypes.c_void_p(out_k.data_ptr()),
                 ctypes.c_void_p(out_v.data_ptr()), out_dtype, layout)
-
-        def launch():
-            rc = fn(*args)
-            if rc:
-                _lib.check(rc, "air_kv_gather")
-        return launch
+        return _launcher(fn, args, "air_kv_gather", (block_tables, seq_lens, out_offsets, out_k, out_v, stream))
 
     def copy_blocks(self, src, dst, stream=None):
         torch = _torch()

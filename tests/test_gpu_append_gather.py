@@ -327,3 +327,73 @@ def test_copy_blocks_and_swap_roundtrip():
     new_blocks = swap.restore(s, cb[1:2] + cb[2:3])
     assert len(new_blocks) == 3
     assert np.array_equal(pool.read_blocks(new_blocks), before)
+
+
+def test_bound_launchers_keep_their_tensors_alive():
+    """bind_append / bind_gather / bind_decode / bind_prefill return launchers
+    that call the C ABI with raw device addresses; each launcher must hold the
+    tensors those addresses point into.  With the caller's references dropped
+    and same-sized tensors allocated in between (which would take over freed
+    memory), every tensor is still alive -- checked before any launch -- and
+    each launch gives the direct call's pages and outputs bit for bit."""
+    import gc
+    import weakref
+    torch = torch_mod()
+    cfg = workloads.Config("bind", 32, 8, 128, 16, airkv.BF16, 2)
+    w = workloads.build_prefill_decode(cfg, [40, 70], seed=191, decode_steps=0)
+    slots_np = np.concatenate(w.batches)
+    pa = airkv.KvPool(w.num_blocks, 16, 8, 128, airkv.BF16)
+    pb = airkv.KvPool(w.num_blocks, 16, 8, 128, airkv.BF16)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(192)
+    k = torch.randn(len(slots_np), 8, 128, generator=g, device="cuda")
+    v = torch.randn_like(k)
+    st = torch.from_numpy(slots_np).cuda()
+    pa.append(k, v, st)
+    launch_append = pb.bind_append(k.clone(), v.clone(), st.clone())   # only the launcher holds these
+    refs = [weakref.ref(t) for t in launch_append.keep if isinstance(t, torch.Tensor)]
+    tables, lens = w.tables()
+    per = lens.astype(np.int64) * 8 * 128
+    offs = np.concatenate([[0], np.cumsum(per)[:-1]]).astype(np.int64)
+    want_k = torch.zeros(int(per.sum()), dtype=torch.bfloat16, device="cuda")
+    want_v = torch.zeros_like(want_k)
+    tt, lt, ot = (torch.from_numpy(x).cuda() for x in (tables, lens, offs))
+    pa.gather(tt, lt, ot, want_k, want_v)
+    gk, gv = torch.zeros_like(want_k), torch.zeros_like(want_v)
+    launch_gather = pb.bind_gather(tt.clone(), lt.clone(), ot.clone(), gk, gv)
+    refs += [weakref.ref(t) for t in launch_gather.keep if isinstance(t, torch.Tensor)]
+    q = torch.randn(2, 32, 128, generator=g, device="cuda").to(torch.bfloat16)
+    want_o = torch.empty(2, 32, 128, device="cuda")
+    pa.paged_decode(q, tt, lt, want_o)
+    out = torch.empty_like(want_o)
+    launch_decode = pb.bind_decode(q.clone(), tt.clone(), lt.clone(), out, None)
+    refs += [weakref.ref(t) for t in launch_decode.keep if isinstance(t, torch.Tensor)]
+    cu = torch.tensor([0, 8, 24], dtype=torch.int32, device="cuda")
+    qp = torch.randn(24, 32, 128, generator=g, device="cuda").to(torch.bfloat16)
+    want_p = torch.empty(24, 32, 128, device="cuda")
+    pa.paged_prefill(qp, cu, tt, lt, want_p)
+    outp = torch.empty_like(want_p)
+    launch_prefill = pb.bind_prefill(qp.clone(), cu.clone(), tt.clone(), lt.clone(), outp)
+    refs += [weakref.ref(t) for t in launch_prefill.keep if isinstance(t, torch.Tensor)]
+    torch.cuda.synchronize()
+    gc.collect()
+    # same-sized allocations that would reuse any memory the launchers lost
+    filler = [torch.full_like(t, 7) for t in (k, v, q, qp)] + [torch.full_like(x, -1) for x in (st, tt, lt, ot, cu)]
+    assert len(refs) >= 17 and all(r() is not None for r in refs), "a launcher lost a tensor it writes through"
+    del filler
+    gk.zero_()
+    gv.zero_()
+    out.zero_()
+    outp.zero_()
+    launch_append()
+    launch_gather()
+    launch_decode()
+    launch_prefill()
+    torch.cuda.synchronize()
+    pka, pva, _, _ = pa.snapshot()
+    pkb, pvb, _, _ = pb.snapshot()
+    assert np.array_equal(pka, pkb) and np.array_equal(pva, pvb)
+    assert torch.equal(gk.view(torch.int16), want_k.view(torch.int16))
+    assert torch.equal(gv.view(torch.int16), want_v.view(torch.int16))
+    assert torch.equal(out, want_o) and torch.equal(outp, want_p)
+    assert pa.error_count() == 0 and pb.error_count() == 0
