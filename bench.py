@@ -47,6 +47,10 @@ def parse():
                     help="skip the gather / append bandwidth legs (for profiling runs)")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the c3 / c4 / c5 decode legs")
+    ap.add_argument("--legs", default="all",
+                    help="comma list of the legs after the c2 step and decode to run (for profiling runs): "
+                         "gather_append, ceilings, configs, quant_append, c5_step, prefill, compress, blocks; "
+                         "default all")
     return ap.parse_args()
 
 
@@ -199,16 +203,23 @@ def cpu_info():
         aff = ncpu
     omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
     threads = max(1, min(aff, omp) if omp > 0 else aff)
-    model = "unknown"
+    # the first processor's fields: a bare "AMD EPYC" model name still names
+    # its generation by family / model / stepping (family 25: Zen 3 / Zen 4,
+    # family 26: Zen 5), and the flags say whether AVX-512 is there
+    fields = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
+            if not line.strip():
                 break
+            key, _, val = line.partition(":")
+            fields.setdefault(key.strip(), val.strip())
     except OSError:
         pass
-    return threads, {"cpu_model": model, "host_cpus": ncpu, "affinity_cpus": aff,
-                     "omp_num_threads": omp or None}
+    flags = fields.get("flags", "").split()
+    return threads, {"cpu_model": fields.get("model name", "unknown"), "cpu_family": fields.get("cpu family"),
+                     "cpu_model_id": fields.get("model"), "cpu_stepping": fields.get("stepping"),
+                     "cpu_mhz": fields.get("cpu MHz"), "avx512": "avx512f" in flags,
+                     "host_cpus": ncpu, "affinity_cpus": aff, "omp_num_threads": omp or None}
 
 
 def cpu_baseline(pool, w, tables, lens, q_f32, budget_s, decode_bytes_of):
@@ -296,12 +307,28 @@ def config_decode(torch, name, iters=20):
     tok = int(lens.astype(np.int64).sum())
     pages = int(((lens + cfg.block_size - 1) // cfg.block_size).sum())
     nbytes = tok * per_tok + 4 * pages + cfg.batch * cfg.n_q_heads * cfg.head_dim * 4
-    assert pool.error_count() == 0 and twin.error_count() == 0
-    twin.close()
     res = {"decode_gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "decode_us": round(ms * 1e3, 1),
            "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4), "cached_tokens": tok,
            "batch": cfg.batch, "kv_dtype": {airkv.BF16: "bf16", airkv.INT8: "int8", airkv.FP8: "fp8"}[cfg.dtype],
            "block_size": cfg.block_size, "n_q_heads": cfg.n_q_heads}
+    if cfg.dtype in (airkv.INT8, airkv.FP8):
+        # the dequantizing gather of every sequence to contiguous f32
+        # [head][len][dim] (code * scale, src/kv_cache.rs:78-92,
+        # src/fp8.rs:263-264): codes and scales read, f32 written
+        per = lens.astype(np.int64) * cfg.n_kv_heads * cfg.head_dim
+        offs = torch.from_numpy(np.concatenate([[0], np.cumsum(per)[:-1]]).astype(np.int64)).cuda()
+        gk = torch.empty(int(per.sum()), dtype=torch.float32, device="cuda")
+        gv = torch.empty_like(gk)
+        gather = alternating([p.bind_gather(tt, lt, offs, gk, gv, out_dtype=airkv.F32) for p in (pool, twin)])
+        gather()
+        ms_g = timed_loop(torch, gather, 10)
+        g_bytes = tok * (per_tok + cfg.n_kv_heads * cfg.head_dim * 2 * 4) + 4 * pages
+        res["gather_f32"] = {"gbps": round(g_bytes / (ms_g * 1e-3) / 1e9, 1), "us": round(ms_g * 1e3, 1),
+                             "frac": round(g_bytes / (ms_g * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+                             "algorithmic_bytes": int(g_bytes)}
+        del gk, gv
+    assert pool.error_count() == 0 and twin.error_count() == 0
+    twin.close()
     pool.close()
     return res
 
@@ -453,6 +480,292 @@ def blocks_leg(torch, iters=20):
     return res
 
 
+QUANT_APPEND_ROWS = 32768
+
+
+def quant_append_workload(name):
+    """The slots of two 32768-row append launches at a 1-byte config's
+    geometry (c3: int8 Q8_0, bs 16; c4: fp8, bs 32): eight sequences of
+    8192 tokens over a pool of 1.25x the tokens with a shuffled free list, so
+    each launch writes four whole sequences' pages scattered over the pool."""
+    import numpy as np
+
+    from airkv import workloads
+    cfg = workloads.CONFIGS[name]
+    w = workloads.build_prefill_decode(cfg, [8192] * 8, seed=61 if name == "c3" else 71, decode_steps=0)
+    allslots = np.concatenate(w.batches)
+    n = QUANT_APPEND_ROWS
+    return cfg, w, [allslots[j * n:(j + 1) * n] for j in range(2)]
+
+
+def quant_append_bytes(cfg, n_rows):
+    """f32 K and V rows read, 1-byte codes and f32 group scales written, int64 slots read."""
+    row = cfg.n_kv_heads * cfg.head_dim
+    return n_rows * (row * 2 * (4 + 1) + cfg.n_kv_heads * (cfg.head_dim // cfg.scale_group) * 4 * 2 + 8)
+
+
+def quant_append_leg(torch, name, iters=20):
+    """Quantize-on-append at full size for c3 (int8 Q8_0, 1% outlier channels
+    x20) and c4 (fp8, reference E4M3 with the absmax/448 scale): 32768 f32
+    K/V rows per launch (the c2 leg's size), two source / slot sets used
+    alternately (2 x 268 MB of rows exceed the 256 MB MALL)."""
+    import airkv
+    from airkv import workloads
+    cfg, w, sets = quant_append_workload(name)
+    pool = airkv.KvPool(w.num_blocks, cfg.block_size, cfg.n_kv_heads, cfg.head_dim, cfg.dtype, cfg.scale_group)
+    outl = workloads.outlier_channels(cfg.n_kv_heads, cfg.head_dim, seed=3) if name == "c3" else None
+    gen = workloads.kv_rows(10 ** 12, cfg.n_kv_heads, cfg.head_dim, seed=62, device="cuda",
+                            chunk_rows=QUANT_APPEND_ROWS, outliers=outl)
+    fns = []
+    for s in sets:
+        k, v = next(gen)
+        fns.append(pool.bind_append(k, v, torch.from_numpy(s).cuda()))
+    call = alternating(fns)
+    call()
+    ms = timed_loop(torch, call, iters)
+    nbytes = quant_append_bytes(cfg, QUANT_APPEND_ROWS)
+    assert pool.error_count() == 0
+    pool.close()
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    return {"gbps": round(gbps, 1), "us": round(ms * 1e3, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4),
+            "rows": QUANT_APPEND_ROWS, "kv_dtype": {airkv.INT8: "int8", airkv.FP8: "fp8"}[cfg.dtype],
+            "block_size": cfg.block_size, "algorithmic_bytes": int(nbytes)}
+
+
+def c5_step_leg(torch, warmup=2, steps=6):
+    """configs[4] as timed steps at full size: 256 sequences (32 q / 8 kv
+    heads, head_dim 128, bf16 pages, block 32, lognormal target contexts
+    median 1024 clipped to [16, 32768]); per step one append launch of the
+    512-token prefill chunks of up to 8 sequences still prefilling plus one
+    token for every other sequence, then the gather of every live sequence to
+    contiguous bf16 [head][len][dim], then the split-K paged decode of every
+    live sequence; after the step 13 sequences (5%) are freed and 13 new ones
+    created, whose blocks later come from the FIFO free list the frees have
+    fragmented (src/paged_attention.rs:115-135).  The same workflow is
+    checked bit for bit in tests/test_gpu_full_configs.py.
+
+    The host work of each step (slot allocation through the SequenceManager,
+    table export, the frees and creations) is planned first and timed on
+    the CPU; every step's slots, tables, rows and queries are then resident
+    in HBM, and the device part is timed with HIP events: the whole step
+    (three launches), then each launch kind alone over the same steps."""
+    import numpy as np
+
+    import airkv
+    from airkv import workloads
+    NQ, NKV, D, BS, CHUNK, N_SEQ, CHURN = 32, 8, 128, 32, 512, 256, 13
+    n_steps = warmup + steps
+    rng = np.random.default_rng(180)
+    targets0 = workloads.c5_lengths(N_SEQ, seed=181)
+    cap = int(1.3 * (sum(targets0) + CHURN * n_steps * 4096 + N_SEQ * n_steps) / BS) + N_SEQ
+    mgr = airkv.SequenceManager(cap, BS, free_order=workloads.lcg_permutation(cap, 182))
+    pool = airkv.KvPool(cap, BS, NKV, D, airkv.BF16)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(183)
+    seqs = [mgr.create_sequence() for _ in range(N_SEQ)]
+    target = dict(zip(seqs, targets0))
+    have = {s: 0 for s in seqs}
+    # contexts before the measured steps (untimed): all but eight sequences
+    # prefilled; those eight take the first step's prefill chunks
+    for s in seqs[: N_SEQ - 8]:
+        slots = torch.from_numpy(mgr.append_slots(s, target[s])).cuda()
+        have[s] = target[s]
+        for c0 in range(0, len(slots), 32768):
+            sl = slots[c0:c0 + 32768]
+            k = torch.randn(len(sl), NKV, D, generator=g, device="cuda")
+            pool.append(k, torch.randn_like(k), sl)
+    new_targets = iter(workloads.c5_lengths(CHURN * n_steps, seed=184))
+    plans, host_us = [], []
+    for step in range(n_steps):
+        t0 = time.perf_counter()
+        slots, n_pref = [], 0
+        for s in seqs:
+            if have[s] < target[s]:
+                if n_pref == 8:
+                    continue                        # waits for a prefill slot
+                n = min(CHUNK, target[s] - have[s])
+                n_pref += 1
+            else:
+                n = 1
+            slots.append(mgr.append_slots(s, n))
+            have[s] += n
+        slots = np.concatenate(slots)
+        live = [s for s in seqs if have[s] > 0]
+        mb = max(-(-have[s] // BS) for s in live)
+        tables, lens = mgr.export_tables(live, mb)
+        t1 = time.perf_counter()
+        for s in rng.choice(seqs, size=CHURN, replace=False).tolist():
+            mgr.free_sequence(s)
+            seqs.remove(s)
+            del have[s], target[s]
+            t = mgr.create_sequence()
+            seqs.append(t)
+            have[t] = 0
+            target[t] = int(next(new_targets))
+        t2 = time.perf_counter()
+        host_us.append(((t1 - t0) * 1e6, (t2 - t1) * 1e6))
+        plans.append((slots, tables, lens, n_pref))
+    # device inputs of every step, resident before timing
+    dev = []
+    max_tok = max(int(p[2].astype(np.int64).sum()) for p in plans)
+    gk = torch.empty(max_tok * NKV * D, dtype=torch.bfloat16, device="cuda")
+    gv = torch.empty_like(gk)
+    ws = pool.new_workspace(NQ, max(len(p[2]) for p in plans), max(p[1].shape[1] for p in plans))
+    for slots, tables, lens, _ in plans:
+        st = torch.from_numpy(slots).cuda()
+        k = torch.randn(len(slots), NKV, D, generator=g, device="cuda")
+        v = torch.randn_like(k)
+        tt, lt = torch.from_numpy(tables).cuda(), torch.from_numpy(lens).cuda()
+        per = lens.astype(np.int64) * NKV * D
+        offs = torch.from_numpy(np.concatenate([[0], np.cumsum(per)[:-1]]).astype(np.int64)).cuda()
+        q = torch.randn(len(lens), NQ, D, generator=g, device="cuda").to(torch.bfloat16)
+        out = torch.empty_like(q)
+        dev.append((pool.bind_append(k, v, st), pool.bind_gather(tt, lt, offs, gk, gv),
+                    pool.bind_decode(q, tt, lt, out, ws)))
+    torch.cuda.synchronize()
+
+    def run(parts):
+        for i in range(warmup):
+            for j in parts:
+                dev[i][j]()
+        torch.cuda.synchronize()
+        torch.cuda._sleep(20_000_000)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(warmup, n_steps):
+            for j in parts:
+                dev[i][j]()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps * 1e3    # us per step
+
+    us_step = run((0, 1, 2))
+    us_parts = [run((j,)) for j in range(3)]
+    assert pool.error_count() == 0
+    timed = plans[warmup:]
+    tok_app = sum(len(p[0]) for p in timed) / steps
+    ctx = [p[2].astype(np.int64) for p in timed]
+    tok = sum(int(c.sum()) for c in ctx) / steps
+    pages = sum(int(((c + BS - 1) // BS).sum()) for c in ctx) / steps
+    live = sum(len(c) for c in ctx) / steps
+    row = NKV * D * 2                                  # K+V elements per token
+    b_app = tok_app * (row * (4 + 2) + 8)
+    b_gat = tok * row * (2 + 2) + 4 * pages
+    b_dec = tok * row * 2 + 4 * pages + live * NQ * D * (2 + 2)
+
+    def part(us, nbytes):
+        gbps = nbytes / (us * 1e-6) / 1e9
+        return {"us": round(us, 1), "gbps": round(gbps, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4),
+                "algorithmic_bytes": int(nbytes)}
+    res = {"step": part(us_step, b_app + b_gat + b_dec), "append": part(us_parts[0], b_app),
+           "gather": part(us_parts[1], b_gat), "decode": part(us_parts[2], b_dec),
+           "steps_timed": steps, "appended_tokens_per_step": tok_app,
+           "prefill_chunks_per_step": sum(p[3] for p in timed) / steps,
+           "live_sequences_per_step": live, "cached_tokens_per_step": tok,
+           "tokens_per_step_list": [int(len(p[0])) for p in timed],
+           "host_alloc_us_per_step": round(sum(h[0] for h in host_us[warmup:]) / steps, 1),
+           "host_free_realloc_us_per_step": round(sum(h[1] for h in host_us[warmup:]) / steps, 1),
+           "host_note": "SequenceManager work through the C ABI from Python (ctypes), timed on the CPU; "
+                        "not inside the device figures"}
+    pool.close()
+    return res
+
+
+def cpu_rate(fn, items, bytes_of, budget_s, threads):
+    """One thread: items in order until budget_s (at least one); then every
+    item over `threads` threads (ctypes releases the GIL around the C oracle).
+    Returns (GB/s on 1 thread, GB/s on all, items done on 1 thread, s)."""
+    import concurrent.futures
+    done, t0 = 0, time.perf_counter()
+    for it in items:
+        fn(it)
+        done += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    t1 = time.perf_counter() - t0
+    with concurrent.futures.ThreadPoolExecutor(threads) as ex:
+        t0 = time.perf_counter()
+        list(ex.map(fn, items))
+        tn = time.perf_counter() - t0
+    return bytes_of(items[:done]) / t1 / 1e9, bytes_of(items) / tn / 1e9, done, tn
+
+
+def cpu_append_gather(budget_s, threads):
+    """The oracle's append (f32 rows -> bf16 / Q8_0 int8 / reference fp8
+    pages, src/kv_cache.rs:54-75, src/fp8.rs:54-91 + :228-238), its gather
+    of the pages back to contiguous [head][len][dim] (bf16 -> bf16, int8 /
+    fp8 -> f32 dequantized, src/kv_cache.rs:78-92, src/fp8.rs:263-264), and
+    Q8Tensor::quantize over the flattened rows as save_layer calls it
+    (src/kv_cache.rs:307-315), on the same geometries, slot sets and byte
+    counts as the GPU legs: 32768 rows per config in 512-row items, gathers
+    of those rows' four sequences in 1024-token pieces."""
+    import numpy as np
+
+    import oracle
+    from airkv import workloads
+    res = {}
+    rows = QUANT_APPEND_ROWS
+    for name, dt in (("c2", oracle.BF16), ("c3", oracle.INT8), ("c4", oracle.FP8)):
+        if name == "c2":
+            cfg = workloads.CONFIGS["c2"]
+            w = workloads.build_prefill_decode(cfg, [8192] * 4, seed=51, decode_steps=0)
+            slots = np.concatenate(w.batches)[:rows]
+        else:
+            cfg, w, sets = quant_append_workload(name)
+            slots = sets[0]
+        host = oracle.HostPool(w.num_blocks, cfg.block_size, cfg.n_kv_heads, cfg.head_dim, dt, cfg.scale_group)
+        outl = workloads.outlier_channels(cfg.n_kv_heads, cfg.head_dim, seed=3) if name == "c3" else None
+        k, v = next(workloads.kv_rows(rows, cfg.n_kv_heads, cfg.head_dim, seed=63, outliers=outl,
+                                      chunk_rows=rows))
+        items = [(i, min(i + 512, rows)) for i in range(0, rows, 512)]
+        eb = oracle.ELEM_BYTES[dt]
+        rb = cfg.n_kv_heads * cfg.head_dim * 2 * (4 + eb) + 8
+        if dt != oracle.BF16:
+            rb += cfg.n_kv_heads * (cfg.head_dim // cfg.scale_group) * 4 * 2
+
+        def app(it):
+            host.append(k[it[0]:it[1]], v[it[0]:it[1]], slots[it[0]:it[1]])
+        a1, an, d1, tn = cpu_rate(app, items, lambda its: rb * sum(b - a for a, b in its), budget_s, threads)
+        kd = {oracle.BF16: "bf16", oracle.INT8: "int8", oracle.FP8: "fp8"}[dt]
+        res[f"append_{kd}"] = {"gbps_1thread": round(a1, 3), "gbps_all": round(an, 3),
+                               "sample": f"{name} geometry, {rows} f32 K/V rows in 512-row appends over a shuffled "
+                                         f"pool; one thread {d1} appends, {threads} threads all in {tn:.2f} s"}
+        # gather of the appended rows' four sequences, 1024-token pieces
+        tables, lens = w.tables()
+        per_blk = 1024 // cfg.block_size
+        pieces = [(b, j) for b in range(4) for j in range(int(lens[b]) // 1024)]
+        odt = oracle.BF16 if dt == oracle.BF16 else oracle.F32
+        ob = 2 if odt == oracle.BF16 else 4
+        gb = 1024 * (cfg.n_kv_heads * cfg.head_dim * 2 * (eb + ob)) + 4 * per_blk
+        if dt != oracle.BF16:
+            gb += 1024 * cfg.n_kv_heads * (cfg.head_dim // cfg.scale_group) * 4 * 2
+
+        def gat(p):
+            b, j = p
+            t = np.ascontiguousarray(tables[b:b + 1, j * per_blk:(j + 1) * per_blk])
+            _, _, _, bad = host.gather(t, np.array([1024], np.int32), odt)
+            assert bad == 0
+        g1, gn, d1, tn = cpu_rate(gat, pieces, lambda ps: gb * len(ps), budget_s, threads)
+        res[f"gather_{kd}_to_{'bf16' if ob == 2 else 'f32'}"] = {
+            "gbps_1thread": round(g1, 3), "gbps_all": round(gn, 3),
+            "sample": f"{name} geometry, four 8192-token sequences in {len(pieces)} pieces of 1024 tokens; one "
+                      f"thread {d1} pieces, {threads} threads all in {tn:.2f} s"}
+        if dt == oracle.INT8:
+            flat = k.reshape(-1)
+
+            def q8(it):
+                a, b = it[0] * cfg.n_kv_heads * cfg.head_dim, it[1] * cfg.n_kv_heads * cfg.head_dim
+                oracle.q8_quantize(flat[a:b])
+            qb = cfg.n_kv_heads * cfg.head_dim * (4 + 1) + cfg.n_kv_heads * (cfg.head_dim // 32) * 4
+            q1, qn, d1, tn = cpu_rate(q8, items, lambda its: qb * sum(b - a for a, b in its), budget_s, threads)
+            res["quantize_q8"] = {"gbps_1thread": round(q1, 3), "gbps_all": round(qn, 3),
+                                  "sample": f"Q8Tensor::quantize of {rows} K rows (x {cfg.n_kv_heads * cfg.head_dim} "
+                                            f"f32) in 512-row pieces; one thread {d1} pieces, {threads} threads "
+                                            f"all in {tn:.2f} s"}
+        del host
+    return res
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -570,7 +883,13 @@ def main():
     log(f"decode {ms_dec * 1e3:.1f} us, {dec_gbps:.0f} GB/s ({dec_gbps / PEAK_HBM_GBPS:.1%} of peak)")
 
     extra = dict(extra_step)
-    if not args.only_decode:
+    legs = set(args.legs.split(",")) if args.legs != "all" else {
+        "gather_append", "ceilings", "configs", "quant_append", "c5_step", "prefill", "compress", "blocks"}
+    if args.only_decode:
+        legs = set()
+    if args.no_configs:
+        legs -= {"configs", "quant_append", "c5_step", "prefill", "compress", "blocks"}
+    if "gather_append" in legs:
         # gather of every sequence to contiguous bf16 [head][len][dim]
         lens_f = np.array(lens0) + n_steps
         per = lens_f.astype(np.int64) * cfg.n_kv_heads * cfg.head_dim
@@ -619,10 +938,11 @@ def main():
     del src, dst
     log(f"torch copy {extra['copy_gbps']} GB/s")
 
-    if not args.only_decode:
+    if "ceilings" in legs:
         extra["ceilings"] = ceilings_leg(torch)
         log(f"ceilings {extra['ceilings']}")
         c = extra["ceilings"]
+    if "ceilings" in legs and "gather_append" in legs:
         extra["frac_of_ceiling"] = {
             "decode_vs_page_read": round(dec_gbps / c["page_read"]["gbps"], 4),
             "gather_vs_copy": round(extra["gather_gbps"] / c["copy"]["gbps"], 4),
@@ -631,7 +951,7 @@ def main():
             "append_vs_page_mix21": round(extra["append_gbps"] / c["page_mix21"]["gbps"], 4),
         }
 
-    if not args.no_configs and not args.only_decode:
+    if "configs" in legs:
         extra["other_configs"] = {}
         for name in ("c3", "c4", "c5"):
             extra["other_configs"][name] = config_decode(torch, name)
@@ -639,14 +959,23 @@ def main():
                 extra["other_configs"][name]["frac_of_page_read_ceiling"] = round(
                     extra["other_configs"][name]["decode_gbps"] / extra["ceilings"]["page_read"]["gbps"], 4)
             log(f"{name} decode {extra['other_configs'][name]}")
+    if "quant_append" in legs:
+        extra["append_quantized"] = {name: quant_append_leg(torch, name) for name in ("c3", "c4")}
+        log(f"quantize-on-append {extra['append_quantized']}")
+    if "c5_step" in legs:
+        extra["c5_step"] = c5_step_leg(torch)
+        log(f"c5 step {extra['c5_step']}")
+    if "prefill" in legs:
         extra["prefill_c5"] = prefill_leg(torch)
         log(f"prefill {extra['prefill_c5']['tflops']} TFLOP/s")
         extra["prefill_one_sequence_32k"] = prefill_leg(torch, iters=5, prefix=[32256])
         log(f"prefill one sequence {extra['prefill_one_sequence_32k']['tflops']} TFLOP/s")
         extra["prefill_c5_chunks_int8_70b"] = prefill_leg(torch, int8_70b=True)
         log(f"prefill int8 70B geometry {extra['prefill_c5_chunks_int8_70b']['tflops']} TFLOP/s")
+    if "compress" in legs:
         extra["kv_compress_blocks"] = compress_leg(torch)
         log(f"compress blocks {extra['kv_compress_blocks']['gbps']} GB/s")
+    if "blocks" in legs:
         extra["kv_blocks"] = blocks_leg(torch)
         log(f"block copy / wire {extra['kv_blocks']}")
 
@@ -662,6 +991,8 @@ def main():
         cpu = cpu_baseline(pool, w, tables_np, lens_final, q_last, args.cpu_seconds, bytes_of)
         log(f"cpu oracle {cpu['value']:.3f} GB/s ({cpu['cores']} threads), "
             f"{cpu['value_1core']:.3f} GB/s (1 thread)")
+        cpu["pieces"] = cpu_append_gather(min(2.0, args.cpu_seconds), cpu["cores"])
+        log(f"cpu oracle append / gather / quantize {cpu['pieces']}")
 
     result = {
         "metric": "paged decode attn HBM GB/s (% of peak); KV append+gather GB/s, 1 MI355X",
