@@ -352,3 +352,48 @@ def test_lcg_matches_reference_definition():
 def test_box_muller_is_standard_normal():
     x = oracle.box_muller_fill(42, 200_000)
     assert abs(float(x.mean())) < 0.01 and abs(float(x.std()) - 1.0) < 0.01
+
+
+def _box_muller_uniforms(seed: int, pairs: int):
+    """The two uniforms of each pair of src/kv_compress.rs:1001-1005, drawn
+    with Python integers: the 64-bit LCG step, the top 53 bits converted to
+    f32 (exact to f64, then one rounding), divided by 2^53 (exact), u1 floored
+    at 1e-10."""
+    s = seed + 1
+    u1s, u2s = [], []
+    for _ in range(pairs):
+        s = (s * 6364136223846793005 + 1442695040888963407) % 2 ** 64
+        u1 = np.float32(float(s >> 11)) / np.float32(2.0 ** 53)
+        s = (s * 6364136223846793005 + 1442695040888963407) % 2 ** 64
+        u2 = np.float32(float(s >> 11)) / np.float32(2.0 ** 53)
+        u1s.append(max(u1, np.float32(1e-10)))
+        u2s.append(u2)
+    return np.array(u1s, np.float64), np.array(u2s, np.float64)
+
+
+@pytest.mark.parametrize("fill", ["box_muller", "qjl_orig_dim_4"])
+def test_box_muller_pairs_are_radius_and_angle(fill):
+    """Each output pair (x0, x1) of the Box-Muller stream is the point at
+    radius sqrt(-2 ln u1) and angle 2 pi u2 (src/kv_compress.rs:1007-1015):
+    x0^2 + x1^2 = -2 ln u1 and atan2(x1, x0) = 2 pi u2 (mod 2 pi), to f32
+    accuracy.  Swapping cos and sin, or u1 and u2, or dropping a sign moves
+    one of the two far outside the tolerance."""
+    pairs = 4096
+    if fill == "box_muller":
+        x = oracle.box_muller_fill(11, 2 * pairs).astype(np.float64)
+    else:   # qjl_projection_matrix scales every value by 1 / sqrt(orig_dim) = 1/2
+        x = oracle.qjl_projection_matrix(2 * pairs // 4, 4, 11).astype(np.float64) * 2.0
+    u1, u2 = _box_muller_uniforms(11, pairs)
+    x0, x1 = x[0::2], x[1::2]
+    r2 = -2.0 * np.log(u1)
+    assert np.allclose(x0 * x0 + x1 * x1, r2, rtol=2e-6, atol=1e-12)
+    ang = np.mod(np.arctan2(x1, x0), 2 * np.pi)
+    want = np.mod(2 * np.pi * u2, 2 * np.pi)
+    d = np.abs(ang - want)
+    d = np.minimum(d, 2 * np.pi - d)             # distance on the circle
+    far = r2 > 1e-4                               # angles of tiny radii carry no information
+    assert far.sum() > pairs * 0.99
+    assert float(d[far].max()) < 2e-5
+    # the mistakes this pins: each one moves the angle or the radius by far more
+    assert np.abs(np.mod(np.arctan2(x0, x1), 2 * np.pi) - want)[far].max() > 1.0     # cos <-> sin
+    assert not np.allclose(x0 * x0 + x1 * x1, -2.0 * np.log(np.maximum(u2, 1e-10)), rtol=1e-2)  # u1 <-> u2
