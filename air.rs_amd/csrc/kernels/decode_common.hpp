@@ -18,6 +18,7 @@ struct DecodeArgs {
     int32_t batch, max_blocks;
     int32_t part_tokens, num_parts;  // fixed partitions (vector kernel)
     int32_t slices, slots;           // balanced slices (matrix-core kernel)
+    int32_t max_splits;              // pieces per sequence at most (matrix-core kernel)
     float scale_log2;              // softmax scale * log2(e): exp(x*s) == exp2(x*scale_log2)
     int32_t n_kv_heads, block_size, scale_group, group;
     int64_t num_blocks;
@@ -27,7 +28,7 @@ struct DecodeArgs {
     // Matrix-core kernel: [n_kv][slots][group][head_dim] and [..][2].
     float *part_o;                 // unnormalised partial outputs
     float *part_ml;                // running max (log2 units), sum
-    int32_t *prefix;               // matrix-core kernel: tiles before each sequence, [batch + 1]
+    int32_t *prefix;               // matrix-core kernel: tiles before each sequence, [batch + 1], then the chunk
     void *out;
     int32_t out_dtype;
     unsigned long long *errors;

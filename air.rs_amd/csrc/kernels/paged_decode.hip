@@ -353,6 +353,7 @@ int plan_decode(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int32_t 
     if (max_splits < 1 || max_splits > 256)
         return fail(AIR_KV_E_INVALID_ARG, "max_splits %d outside 1..256", max_splits);
     plan->group = g;
+    plan->max_splits = max_splits;
     if (decode_mfma_supported(p.desc.dtype, d, bs, g, p.desc.scale_group))
         return plan_decode_mfma(p, n_q_heads, batch, max_blocks, max_splits, plan);
     plan->mfma = false;
@@ -383,7 +384,7 @@ hipError_t launch_decode(const air_kv_pool &p, hipStream_t s, const DecodePlan &
     a.tables = tables; a.lens = lens;
     a.batch = batch; a.max_blocks = max_blocks;
     a.part_tokens = plan.part_tokens; a.num_parts = plan.num_parts;
-    a.slices = plan.slices; a.slots = plan.slots;
+    a.slices = plan.slices; a.slots = plan.slots; a.max_splits = plan.max_splits;
     a.scale_log2 = scale * 1.4426950408889634f;
     a.n_kv_heads = p.desc.n_kv_heads; a.block_size = p.desc.block_size;
     a.scale_group = p.desc.scale_group; a.group = plan.group; a.num_blocks = p.desc.num_blocks;

@@ -11,7 +11,9 @@
 // at every sequence boundary the wave emits the (max, sum, O) of the piece it
 // holds.  The pieces of sequence b come from slices w0(b) = prefix[b] / chunk
 // .. w1(b) = (prefix[b + 1] - 1) / chunk and are stored at slots b + w, which
-// never collide across sequences because w0(b + 1) >= w1(b).  A sequence that
+// never collide across sequences because w0(b + 1) >= w1(b).  The chunk is
+// widened when needed so that no sequence has more than max_splits pieces
+// (configs[3]'s bound: split-K over up to 64 partitions).  A sequence that
 // lies in one slice is normalised and written by that wave; the others are
 // combined by decode_merge_kernel by log-sum-exp (src/flash_decode.rs:114-142).
 //
@@ -185,14 +187,23 @@ __device__ __forceinline__ int64_t clamp_len(int64_t len, int64_t max_len) {
     return len < 0 ? 0 : (len > max_len ? max_len : len);
 }
 
-// Tiles per slice: an equal share of `total`, at least kMinChunk.
-__device__ __forceinline__ int slice_chunk(int total, int slices) {
-    const int c = (total + slices - 1) / slices;
-    return c < kMinChunk ? kMinChunk : c;
+// Tiles per slice: an equal share of `total`, at least kMinChunk, and large
+// enough that no sequence is cut into more than max_splits pieces.  A
+// sequence of T tiles starting anywhere meets at most ceil((T - 1) / chunk) +
+// 1 slices, so chunk >= ceil((T - 1) / (max_splits - 1)) for the longest
+// sequence (tmax tiles) bounds every one; max_splits 1 leaves one slice per
+// kv head.
+__device__ __forceinline__ int slice_chunk(int total, int slices, int tmax, int max_splits) {
+    int c = (total + slices - 1) / slices;
+    c = c < kMinChunk ? kMinChunk : c;
+    if (max_splits <= 1) return c > total ? c : total;
+    const int cs = (tmax - 1 + max_splits - 2) / (max_splits - 1);
+    return c > cs ? c : cs;
 }
 
 // pre[b] = tiles (ceil(len / 16), len clamped to [0, max_blocks * BS]) of the
-// sequences before b, for b = 0..batch, in LDS.  All threads take part.
+// sequences before b, for b = 0..batch, in LDS, and pre[B + 1] = the most
+// tiles of one sequence.  All threads take part.
 template <int BS>
 // long_seq (optional, B bits, zero on entry): bit b set when sequence b is
 // longer than its table.
@@ -200,12 +211,27 @@ __device__ void tile_prefix(const DecodeArgs &a, int32_t *pre, int32_t *wsum, ui
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int B = a.batch;
     const int64_t max_len = (int64_t)a.max_blocks * BS;
+    int tmax = 0;
     for (int b = tid; b < B; b += kThreads) {
         const int32_t len = a.lens[b];
-        pre[b + 1] = (int32_t)((clamp_len(len, max_len) + 15) / 16);
+        const int32_t t = (int32_t)((clamp_len(len, max_len) + 15) / 16);
+        pre[b + 1] = t;
+        tmax = t > tmax ? t : tmax;
         if (long_seq && len > max_len) atomicOr(&long_seq[b >> 5], 1u << (b & 31));
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const int y = __shfl_xor(tmax, o);
+        tmax = y > tmax ? y : tmax;
+    }
+    if (lane == 0) wsum[wave] = tmax;
     if (tid == 0) pre[0] = 0;
+    __syncthreads();
+    if (tid == 0) {
+        int m = wsum[0];
+        for (int w = 1; w < kWaves; ++w) m = wsum[w] > m ? wsum[w] : m;
+        pre[B + 1] = m;
+    }
     __syncthreads();
     // each thread scans a run of `per` entries; runs are chained by a
     // wave-level then a workgroup-level exclusive scan of the run sums
@@ -346,7 +372,7 @@ void decode_mfma_kernel(DecodeArgs a) {
     constexpr int PITCH = D + 32;
     constexpr int VTILE = 16 * PITCH;         // bf16 elements per wave's V tile
     static_assert(BS % 16 == 0, "a 16-token tile must not straddle pages");
-    __shared__ int32_t s_pre[kMaxBatch + 1];
+    __shared__ int32_t s_pre[kMaxBatch + 2];
     __shared__ int32_t s_wsum[kWaves];
     __shared__ __align__(16) uint16_t s_v[kWaves * VTILE];
     // 1-byte pages: the tile's K scales [k-step][token] per wave (lane (r16,
@@ -364,9 +390,11 @@ void decode_mfma_kernel(DecodeArgs a) {
     }
     const int B = a.batch;
     const int total = s_pre[B];
-    const int chunk = slice_chunk(total, a.slices);
-    if (blockIdx.x == 0)                       // for the merge kernel
+    const int chunk = slice_chunk(total, a.slices, s_pre[B + 1], a.max_splits);
+    if (blockIdx.x == 0) {                     // for the merge kernel: prefix, then the chunk
         for (int i = threadIdx.x; i <= B; i += kThreads) a.prefix[i] = s_pre[i];
+        if (threadIdx.x == 0) a.prefix[B + 1] = chunk;
+    }
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: scalar loop control
@@ -866,7 +894,7 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
     const int G = a.group;
     const int64_t max_len = (int64_t)a.max_blocks * a.block_size;
     // every index the workgroup needs, loaded together (one round trip)
-    const int p0 = a.prefix[b], p1 = a.prefix[b + 1], ptot = a.prefix[a.batch];
+    const int p0 = a.prefix[b], p1 = a.prefix[b + 1], chunk = a.prefix[a.batch + 1];
     const int len = a.lens[b];
     if (tid == 0 && kh == 0 && blockIdx.z == 0 && (len < 0 || len > max_len)) atomicAdd(a.errors, 1ull);
     const int64_t obase = ((int64_t)b * a.n_q_heads + kh * G) * D;
@@ -875,7 +903,6 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
             for (int idx = tid; idx < G * D; idx += kThreads) store_out(a, obase + idx, 0.0f);
         return;
     }
-    const int chunk = slice_chunk(ptot, a.slices);
     const int w0 = p0 / chunk, w1 = (p1 - 1) / chunk;
     if (w0 == w1) return;                                // written by its slice
     const int n = w1 - w0 + 1;
@@ -976,8 +1003,11 @@ bool decode_mfma_supported(int dtype, int head_dim, int block_size, int group, i
 }
 
 // Slices per kv head: one wave for every wave slot of the GPU (4 SIMDs per
-// compute unit x waves_per_simd), at most batch * max_splits.  The workspace
-// holds the tile prefix and (slices + batch) partial rows per query head.
+// compute unit x waves_per_simd), at most batch * max_splits.  The kernel
+// widens the slices when the longest sequence would otherwise be cut into
+// more than max_splits pieces (slice_chunk), leaving the rest of the waves
+// idle.  The workspace holds the tile prefix and the chunk, then (slices +
+// batch) partial rows per query head.
 int plan_decode_mfma(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int32_t max_blocks,
                      int32_t max_splits, DecodePlan *plan) {
     const int nkv = p.desc.n_kv_heads, d = p.desc.head_dim, bs = p.desc.block_size;
@@ -1001,7 +1031,7 @@ int plan_decode_mfma(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int
     plan->slices_qf32 = (int32_t)slices_for(kernel_waves_per_simd(p.desc.dtype, true));
     plan->batch_per_launch = nb;
     plan->slots = (int32_t)(slices + nb);
-    plan->ws_bytes = align256((size_t)(nb + 1) * 4) + align256((size_t)n_q_heads * plan->slots * 2 * 4) +
+    plan->ws_bytes = align256((size_t)(nb + 2) * 4) + align256((size_t)n_q_heads * plan->slots * 2 * 4) +
                      (size_t)n_q_heads * plan->slots * d * 4;
     return AIR_KV_OK;
 }
@@ -1026,7 +1056,7 @@ hipError_t launch_decode_mfma(const DecodeArgs &base, const DecodePlan &plan, vo
         }
         char *ws = (char *)workspace;
         a.prefix = (int32_t *)ws;
-        ws += align256((size_t)(plan.batch_per_launch + 1) * 4);
+        ws += align256((size_t)(plan.batch_per_launch + 2) * 4);
         a.part_ml = (float *)ws;
         ws += align256((size_t)a.n_q_heads * plan.slots * 2 * 4);
         a.part_o = (float *)ws;

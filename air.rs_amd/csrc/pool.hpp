@@ -43,6 +43,7 @@ struct DecodePlan {
     int32_t slices;       // slices per kv head (one wave each)
     int32_t slices_qf32;  // the same for f32 queries (their kernel may hold fewer waves per SIMD)
     int32_t batch_per_launch;
+    int32_t max_splits;   // pieces per sequence at most
     int32_t slots;        // partial rows per (kv head, q head of the group): slices + batch
     size_t ws_bytes;
 };

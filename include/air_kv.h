@@ -253,10 +253,14 @@ int air_paged_decode_workspace_size(const air_kv_pool *pool, int32_t n_q_heads, 
  * BF16 pools and rounded to bf16 on INT8 / FP8 pools (an error an order below
  * their quantization's).  The reference's
  * scale is 1/sqrt(head_dim).  max_splits (1..256) bounds the split-K work
- * division: bf16 pools with head_dim 128 (the matrix-core kernel) cut the
- * batch's cached tokens into at most batch * max_splits equal slices per kv
- * head, where a slice may end inside a sequence and hold several; other pools
- * cut each sequence into at most max_splits partitions.  Out-of-pool table
+ * division: no sequence is cut into more than max_splits partitions.  Pools
+ * with head_dim 128, block_size 16 or 32 and group 1..16 -- bf16, and int8 /
+ * fp8 with scale_group >= 32 -- take the matrix-core kernel, which cuts the
+ * batch's cached tokens into equal slices per kv head (one wave each, at most
+ * batch * max_splits), where a slice may end inside a sequence and hold
+ * several, widened when the longest sequence would otherwise meet more than
+ * max_splits of them (max_splits 1: one slice per kv head); other pools cut
+ * each sequence into at most max_splits fixed partitions.  Out-of-pool table
  * entries are skipped and counted (air_kv_pool_error_count); seq_lens outside
  * [0, max_blocks * block_size] are clamped and counted.  A sequence of length
  * 0 produces zeros.  The workspace is device

@@ -101,3 +101,23 @@ def rel_err(got, want):
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
     return float(np.max(np.abs(got - want)) / max(np.max(np.abs(want)), 1e-30))
+
+
+def decode_pieces(workspace, seq_lens):
+    """Pieces per sequence of the matrix-core decode that last used
+    `workspace` (one launch: batch <= 4096).  The workspace starts with that
+    launch's tile prefix (int32 [batch + 1], 16-token tiles per sequence) and
+    the slice length in tiles; sequence b's tiles meet slices prefix[b] //
+    chunk .. (prefix[b + 1] - 1) // chunk.  Also checks the prefix against
+    seq_lens.  Empty sequences have 0 pieces."""
+    import numpy as np
+    torch = torch_mod()
+    torch.cuda.synchronize()
+    batch = len(seq_lens)
+    head = workspace[:4 * (batch + 2)].cpu().numpy().view(np.int32)
+    pre, chunk = head[:batch + 1].astype(np.int64), int(head[batch + 1])
+    tiles = (np.asarray(seq_lens, np.int64) + 15) // 16
+    assert np.array_equal(np.diff(pre), tiles), "tile prefix disagrees with seq_lens"
+    assert chunk >= 1
+    w0, w1 = pre[:-1] // chunk, (pre[1:] - 1) // chunk
+    return np.where(tiles > 0, w1 - w0 + 1, 0)

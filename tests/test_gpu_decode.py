@@ -10,7 +10,7 @@ import pytest
 import airkv
 import oracle
 from airkv import workloads
-from gpu_helpers import (assert_floats_bit_equal, device_pool_for, host_pool_for, log, rel_err, run_appends,
+from gpu_helpers import (assert_floats_bit_equal, decode_pieces, device_pool_for, host_pool_for, log, rel_err, run_appends,
                          torch_mod)
 
 pytestmark = pytest.mark.gpu
@@ -19,7 +19,7 @@ TOL = {airkv.F32: 1e-3, airkv.BF16: 1e-3, airkv.INT8: 2e-2, airkv.FP8: 2e-2}
 
 
 def _decode_case(cfg, lens, seed, q_bf16=True, max_splits=64, outliers=None, out_bf16=False,
-                 empty=()):
+                 empty=(), workspace=None):
     """Decode of cfg with prefill `lens` (+1 decode token each) on the GPU and
     on the oracle; sequences listed in `empty` are decoded with length 0."""
     torch = torch_mod()
@@ -37,13 +37,15 @@ def _decode_case(cfg, lens, seed, q_bf16=True, max_splits=64, outliers=None, out
         qt = qt.to(torch.bfloat16)
         q = qt.float().cpu().numpy()
     out = torch.zeros(q.shape, dtype=torch.bfloat16 if out_bf16 else torch.float32, device="cuda")
+    if workspace == "new":
+        workspace = pool.new_workspace(cfg.n_q_heads, cfg.batch, tables.shape[1], max_splits)
     pool.paged_decode(qt, torch.from_numpy(tables).cuda(), torch.from_numpy(seq_lens).cuda(), out,
-                      max_splits=max_splits)
+                      max_splits=max_splits, workspace=workspace)
     torch.cuda.synchronize()
     got = out.float().cpu().numpy()
     want = host.paged_decode(q, tables, seq_lens, chunk=64)
     assert pool.error_count() == 0
-    return got, want, (pool, host, tables, seq_lens, q)
+    return got, want, (pool, host, tables, seq_lens, q, workspace)
 
 
 @pytest.mark.parametrize("dtype", [airkv.F32, airkv.BF16, airkv.INT8, airkv.FP8])
@@ -131,6 +133,26 @@ def test_c4_shape_fp8_many_splits():
     assert err <= 2e-2
 
 
+@pytest.mark.parametrize("dtype,max_splits", [(airkv.FP8, 2), (airkv.FP8, 8), (airkv.FP8, 64),
+                                              (airkv.INT8, 5), (airkv.BF16, 3)])
+def test_pieces_per_sequence_capped_by_max_splits(dtype, max_splits):
+    """max_splits bounds the pieces of every sequence, not only the slice
+    count: with one long and one shorter sequence (configs[3]'s geometry, fp8
+    / int8 / bf16 pages) the balanced slices would cut the long one into
+    ~100 pieces; the kernel widens the slices until it has at most
+    max_splits.  The pieces come from the workspace's tile prefix and slice
+    length; the output agrees with the oracle."""
+    cfg = workloads.Config("c4cap", 64, 8, 128, 32, dtype, 3)
+    got, want, ctx = _decode_case(cfg, [20000, 9000, 300], seed=45, max_splits=max_splits, workspace="new")
+    pieces = decode_pieces(ctx[5], ctx[3])
+    err = rel_err(got, want)
+    log(f"dtype={dtype} max_splits={max_splits}: pieces {pieces.tolist()}, rel err {err:.2e}")
+    assert pieces.max() <= max_splits
+    if max_splits == 64:
+        assert pieces[0] > 8          # the long sequence still spreads over many waves
+    assert err <= TOL[dtype]
+
+
 @pytest.mark.parametrize("dtype", [airkv.INT8, airkv.FP8])
 @pytest.mark.parametrize("head_dim,scale_group", [(64, 32), (128, 16), (128, 64), (256, 128)])
 def test_quantized_pool_geometries(dtype, head_dim, scale_group):
@@ -192,7 +214,7 @@ def test_one_byte_pages_f32_queries(dtype, bs):
     torch = torch_mod()
     cfg = workloads.Config("q32", 64, 8, 128, bs, dtype, 4)
     outl = workloads.outlier_channels(8, 128, seed=9)
-    got, want, (pool, host, tables, lens, q) = _decode_case(cfg, [300, 1700, 4100, 9000], seed=48,
+    got, want, (pool, host, tables, lens, q, _) = _decode_case(cfg, [300, 1700, 4100, 9000], seed=48,
                                                            q_bf16=False, outliers=outl)
     err = rel_err(got, want)
     qb = torch.from_numpy(q).cuda().to(torch.bfloat16)

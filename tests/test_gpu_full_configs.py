@@ -19,7 +19,7 @@ import pytest
 
 import airkv
 from airkv import workloads
-from gpu_helpers import log, torch_mod
+from gpu_helpers import decode_pieces, log, torch_mod
 
 pytestmark = pytest.mark.gpu
 
@@ -83,7 +83,11 @@ def _full_decode(name, lens, tol, seed, outliers=None):
     tt, lt = torch.from_numpy(tables).cuda(), torch.from_numpy(seq_lens).cuda()
     q = torch.randn(cfg.batch, cfg.n_q_heads, cfg.head_dim, device="cuda").to(torch.bfloat16)
     out = torch.empty(cfg.batch, cfg.n_q_heads, cfg.head_dim, device="cuda")
-    pool.paged_decode(q, tt, lt, out, max_splits=cfg.max_splits)
+    ws = pool.new_workspace(cfg.n_q_heads, cfg.batch, tables.shape[1], cfg.max_splits)
+    pool.paged_decode(q, tt, lt, out, max_splits=cfg.max_splits, workspace=ws)
+    pieces = decode_pieces(ws, seq_lens)
+    log(f"full {name}: pieces per sequence {pieces.min()}..{pieces.max()} (max_splits {cfg.max_splits})")
+    assert pieces.max() <= cfg.max_splits
     gdt = airkv.F32 if cfg.dtype in (airkv.INT8, airkv.FP8) else airkv.BF16
     gk, gv, offs = _gathered(pool, tt, lt, seq_lens, gdt)
     worst = _worst_rel_err(out, q, gk, gv, offs, seq_lens, cfg.n_kv_heads, cfg.head_dim)
