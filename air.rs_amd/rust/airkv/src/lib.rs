@@ -1,5 +1,6 @@
 //! Safe Rust wrapper over `airkv-sys` (the C ABI in include/air_kv.h) with the
-//! API surface of the reference's `src/paged_attention.rs` and `src/kv_swap.rs`:
+//! API surface of the reference's `src/paged_attention.rs`, `src/kv_swap.rs`,
+//! `src/kv_cache.rs` (`SessionKvCache`) and `src/flash_decode.rs`:
 //! the same type names, method names, argument meanings and `Option` /
 //! `Result<_, &'static str>` conventions, so `InferenceGenerator` can switch
 //! to it by changing its `use` lines.  Device work goes through [`KvPool`].
@@ -11,9 +12,13 @@
 //! or corrupts state: releasing a free block is refused (the reference
 //! pushes it onto the free list twice), appending to a full block is an
 //! error (the reference asserts), copy-on-write gives the private block the
-//! sequence's own fill, and the swap closures return a status.
+//! sequence's own fill, and `try_evict` / `try_restore` take closures that
+//! return a status (a failed read aborts the evict before any block is
+//! released).  `SessionKvCache` and `flash_decode` take device pointers where
+//! the reference takes candle tensors and host slices.
 
 use std::ffi::c_void;
+use std::marker::PhantomData;
 use std::ptr;
 
 use airkv_sys as sys;
@@ -365,19 +370,59 @@ pub struct KvSwapManager {
     pub seq_mgr: SequenceManager,
 }
 
-struct ReadCtx<'a, F: Fn(PhysicalBlockId, &mut [u8])>(&'a F);
-struct WriteCtx<'a, F: Fn(PhysicalBlockId, &[u8])>(&'a F);
+struct ReadCtx<'a, F: Fn(PhysicalBlockId, &mut [u8]) -> Result<(), AirKvError>>(&'a F);
+struct WriteCtx<'a, F: Fn(PhysicalBlockId, &[u8]) -> Result<(), AirKvError>>(&'a F);
 
-unsafe extern "C" fn read_tramp<F: Fn(PhysicalBlockId, &mut [u8])>(ctx: *mut c_void, b: u32, dst: *mut u8, n: usize) -> i32 {
-    let f = &*(ctx as *const ReadCtx<F>);
-    (f.0)(PhysicalBlockId(b), std::slice::from_raw_parts_mut(dst, n));
-    sys::AIR_KV_OK
+/// The status a failed closure hands back to the library: its own code when
+/// it carries an AIR_KV_E_* value, AIR_KV_E_HIP (a device copy failed) otherwise.
+fn closure_status(e: &AirKvError) -> i32 {
+    if e.code < 0 { e.code } else { sys::AIR_KV_E_HIP }
 }
 
-unsafe extern "C" fn write_tramp<F: Fn(PhysicalBlockId, &[u8])>(ctx: *mut c_void, b: u32, src: *const u8, n: usize) -> i32 {
+unsafe extern "C" fn read_tramp<F>(ctx: *mut c_void, b: u32, dst: *mut u8, n: usize) -> i32
+where
+    F: Fn(PhysicalBlockId, &mut [u8]) -> Result<(), AirKvError>,
+{
+    let f = &*(ctx as *const ReadCtx<F>);
+    match (f.0)(PhysicalBlockId(b), std::slice::from_raw_parts_mut(dst, n)) {
+        Ok(()) => sys::AIR_KV_OK,
+        Err(e) => closure_status(&e),
+    }
+}
+
+unsafe extern "C" fn write_tramp<F>(ctx: *mut c_void, b: u32, src: *const u8, n: usize) -> i32
+where
+    F: Fn(PhysicalBlockId, &[u8]) -> Result<(), AirKvError>,
+{
     let f = &*(ctx as *const WriteCtx<F>);
-    (f.0)(PhysicalBlockId(b), std::slice::from_raw_parts(src, n));
-    sys::AIR_KV_OK
+    match (f.0)(PhysicalBlockId(b), std::slice::from_raw_parts(src, n)) {
+        Ok(()) => sys::AIR_KV_OK,
+        Err(e) => closure_status(&e),
+    }
+}
+
+/// `read_tramp` instantiated for the type of `_f` (a closure's type has no name).
+fn read_tramp_for<F>(_f: &F) -> unsafe extern "C" fn(*mut c_void, u32, *mut u8, usize) -> i32
+where
+    F: Fn(PhysicalBlockId, &mut [u8]) -> Result<(), AirKvError>,
+{
+    read_tramp::<F>
+}
+
+/// The reference's `&'static str` errors for the swap statuses
+/// (src/kv_swap.rs:55-98, src/paged_attention.rs:313-343), one per cause.
+fn swap_status_str(rc: i32, not_found: &'static str) -> &'static str {
+    match rc {
+        sys::AIR_KV_E_NOT_FOUND => not_found,
+        sys::AIR_KV_E_OOM => "out of memory — cannot swap in",
+        sys::AIR_KV_E_HIP => "device block copy failed",
+        sys::AIR_KV_E_INVALID_ARG => "invalid argument",
+        _ => "swap failed",
+    }
+}
+
+fn swap_error(rc: i32) -> AirKvError {
+    AirKvError { code: rc, message: last_error() }
 }
 
 impl KvSwapManager {
@@ -389,11 +434,26 @@ impl KvSwapManager {
         Self { raw, seq_mgr }
     }
 
+    /// evict (src/kv_swap.rs:50-74) with the reference's infallible closure.
     pub fn evict<F>(&mut self, seq_id: SeqId, gpu_read: F) -> Result<Vec<PhysicalBlockId>, &'static str>
     where
         F: Fn(PhysicalBlockId, &mut [u8]),
     {
-        let n = self.seq_mgr.table(seq_id).ok_or("sequence not found")?.physical_blocks.len();
+        self.try_evict(seq_id, |b, dst| {
+            gpu_read(b, dst);
+            Ok(())
+        })
+        .map_err(|e| swap_status_str(e.code, "sequence not found"))
+    }
+
+    /// evict with a fallible device read: the first `Err` aborts the evict
+    /// before any block is released and comes back as the error (its code
+    /// when it is an AIR_KV_E_* value, AIR_KV_E_HIP otherwise).
+    pub fn try_evict<F>(&mut self, seq_id: SeqId, gpu_read: F) -> Result<Vec<PhysicalBlockId>, AirKvError>
+    where
+        F: Fn(PhysicalBlockId, &mut [u8]) -> Result<(), AirKvError>,
+    {
+        let n = self.seq_mgr.table(seq_id).map_or(0, |t| t.physical_blocks.len());
         let ctx = ReadCtx(&gpu_read);
         let mut ids = vec![0u32; n.max(1)];
         let mut got = 0i32;
@@ -401,10 +461,10 @@ impl KvSwapManager {
             sys::air_kv_swap_evict(self.raw, seq_id.0, Some(read_tramp::<F>), &ctx as *const _ as *mut c_void,
                                    ids.as_mut_ptr(), ids.len() as i32, &mut got)
         };
-        match rc {
-            sys::AIR_KV_OK => Ok(ids[..got as usize].iter().map(|&b| PhysicalBlockId(b)).collect()),
-            _ => Err("sequence not found"),
+        if rc != sys::AIR_KV_OK {
+            return Err(swap_error(rc));
         }
+        Ok(ids[..got as usize].iter().map(|&b| PhysicalBlockId(b)).collect())
     }
 
     /// Evicts with the device pool's own read callback (no host closure).
@@ -419,9 +479,24 @@ impl KvSwapManager {
         Ok(ids[..got as usize].iter().map(|&b| PhysicalBlockId(b)).collect())
     }
 
+    /// restore (src/kv_swap.rs:83-98) with the reference's infallible closure.
     pub fn restore<F>(&mut self, seq_id: SeqId, gpu_write: F) -> Result<Vec<PhysicalBlockId>, &'static str>
     where
         F: Fn(PhysicalBlockId, &[u8]),
+    {
+        self.try_restore(seq_id, |b, src| {
+            gpu_write(b, src);
+            Ok(())
+        })
+        .map_err(|e| swap_status_str(e.code, "no evicted data for sequence"))
+    }
+
+    /// restore with a fallible device write; a failed write returns its
+    /// error and leaves the sequence evicted (its new blocks freed, its bytes
+    /// back in the host store).
+    pub fn try_restore<F>(&mut self, seq_id: SeqId, gpu_write: F) -> Result<Vec<PhysicalBlockId>, AirKvError>
+    where
+        F: Fn(PhysicalBlockId, &[u8]) -> Result<(), AirKvError>,
     {
         let ctx = WriteCtx(&gpu_write);
         let mut ids = vec![0u32; 1 << 16];
@@ -430,11 +505,21 @@ impl KvSwapManager {
             sys::air_kv_swap_restore(self.raw, seq_id.0, Some(write_tramp::<F>), &ctx as *const _ as *mut c_void,
                                      ids.as_mut_ptr(), ids.len() as i32, &mut got)
         };
-        match rc {
-            sys::AIR_KV_OK => Ok(ids[..got as usize].iter().map(|&b| PhysicalBlockId(b)).collect()),
-            sys::AIR_KV_E_OOM => Err("out of memory — cannot swap in"),
-            _ => Err("no evicted data for sequence"),
+        if rc != sys::AIR_KV_OK {
+            return Err(swap_error(rc));
         }
+        Ok(ids[..got as usize].iter().map(|&b| PhysicalBlockId(b)).collect())
+    }
+
+    /// Restores with the device pool's own write callback (no host closure).
+    pub fn restore_pool(&mut self, seq_id: SeqId, pool: &KvPool) -> Result<Vec<PhysicalBlockId>, AirKvError> {
+        let mut ids = vec![0u32; 1 << 16];
+        let mut got = 0i32;
+        check(unsafe {
+            sys::air_kv_swap_restore(self.raw, seq_id.0, Some(sys::air_kv_pool_write_cb), pool.raw as *mut c_void,
+                                     ids.as_mut_ptr(), ids.len() as i32, &mut got)
+        })?;
+        Ok(ids[..got as usize].iter().map(|&b| PhysicalBlockId(b)).collect())
     }
 
     pub fn is_evicted(&self, seq_id: SeqId) -> bool {
@@ -449,17 +534,22 @@ impl KvSwapManager {
         unsafe { sys::air_kv_swap_cpu_bytes_used(self.raw) as usize }
     }
 
+    /// maybe_evict (src/kv_swap.rs:112-121): true when an eviction happened.
     pub fn maybe_evict<F>(&mut self, seq_id: SeqId, free_threshold: usize, gpu_read: F) -> bool
     where
         F: Fn(PhysicalBlockId, &mut [u8]),
     {
-        let ctx = ReadCtx(&gpu_read);
+        let f = |b: PhysicalBlockId, dst: &mut [u8]| -> Result<(), AirKvError> {
+            gpu_read(b, dst);
+            Ok(())
+        };
+        let ctx = ReadCtx(&f);
         let mut ev = 0i32;
-        unsafe {
-            sys::air_kv_swap_maybe_evict(self.raw, seq_id.0, free_threshold as i64, Some(read_tramp::<F>),
+        let rc = unsafe {
+            sys::air_kv_swap_maybe_evict(self.raw, seq_id.0, free_threshold as i64, Some(read_tramp_for(&f)),
                                          &ctx as *const _ as *mut c_void, &mut ev)
         };
-        ev != 0
+        rc == sys::AIR_KV_OK && ev != 0
     }
 }
 
@@ -619,6 +709,38 @@ impl KvPool {
         Ok(n)
     }
 
+    /// `flash_decode` (src/flash_decode.rs:153-173) over paged storage for
+    /// one sequence: `out[h] = softmax(q[h] . K^T / sqrt(head_dim)) . V` for
+    /// each of the `n_q_heads` query heads over the sequence's `kv_len`
+    /// cached tokens, kv head `h / (n_q_heads / n_kv_heads)`.  The reference
+    /// cuts the sequence into `chunk_size`-token chunks and merges their
+    /// partials by log-sum-exp; here `chunk_size` sets the split-K bound
+    /// (`ceil(kv_len / chunk_size)` pieces at most, 1..256) and the kernel
+    /// does the same merge.  `q` / `out` are f32 `[n_q_heads][head_dim]`,
+    /// `block_table` int32 `[max_blocks]` and `kv_len_dev` one int32 equal to
+    /// `kv_len`, all device memory; the workspace is
+    /// [`KvPool::decode_workspace_size`]`(n_q_heads, 1, max_blocks, splits)`
+    /// bytes, splits as returned by [`KvPool::flash_decode_splits`].
+    ///
+    /// # Safety
+    /// Every pointer is device memory of the stated shape.
+    #[allow(clippy::too_many_arguments)]
+    pub unsafe fn flash_decode(&self, stream: Stream, q: *const f32, n_q_heads: usize, block_table: *const i32,
+                               max_blocks: usize, kv_len: usize, kv_len_dev: *const i32, chunk_size: usize,
+                               workspace: *mut c_void, ws_bytes: usize, out: *mut f32) -> Result<(), AirKvError> {
+        let scale = 1.0 / (self.desc.head_dim as f32).sqrt();
+        self.paged_decode(stream, q as *const c_void, KvDtype::F32, n_q_heads, block_table, kv_len_dev, 1, max_blocks,
+                          scale, Self::flash_decode_splits(kv_len, chunk_size), workspace, ws_bytes,
+                          out as *mut c_void, KvDtype::F32)
+    }
+
+    /// The split-K bound [`KvPool::flash_decode`] uses: one piece per
+    /// `chunk_size` tokens, 1..256.
+    pub fn flash_decode_splits(kv_len: usize, chunk_size: usize) -> usize {
+        assert!(chunk_size > 0);
+        kv_len.div_ceil(chunk_size).clamp(1, 256)
+    }
+
     pub fn as_raw(&self) -> *mut sys::air_kv_pool {
         self.raw
     }
@@ -631,6 +753,137 @@ impl Drop for KvPool {
 }
 
 unsafe impl Send for KvPool {}
+
+// ---------------------------------------------------------------------------
+// SessionKvCache (src/kv_cache.rs:431-446) over paged pools
+// ---------------------------------------------------------------------------
+
+/// One layer's dense K / V in device memory, `[n_tokens][n_kv_heads][head_dim]`
+/// each as `dtype`: the paged cache's form of `LayerCache::Attention`
+/// (src/kv_cache.rs:121-122) without candle tensors.
+#[derive(Debug, Clone, Copy)]
+pub struct LayerCache {
+    pub k: *mut c_void,
+    pub v: *mut c_void,
+    pub n_tokens: usize,
+    pub dtype: KvDtype,
+}
+
+/// The reference's per-session cache trait (src/kv_cache.rs:431-446), with
+/// device buffers in place of candle tensors and [`AirKvError`] in place of
+/// `candle_core::Error`.
+pub trait SessionKvCache {
+    /// Tokens stored for `layer` (0 if empty).
+    fn seq_len(&self, layer: usize) -> usize;
+    /// The layer's cache becomes `cache`'s rows (f32): rows past the stored
+    /// length are appended; fewer rows shorten the layer.
+    ///
+    /// # Safety
+    /// `cache.k` / `cache.v` are device arrays of `cache.n_tokens` f32 rows.
+    unsafe fn save(&mut self, layer: usize, cache: LayerCache) -> Result<(), AirKvError>;
+    /// Writes the layer's tokens into `into` (F32 or Bf16; 1-byte pools are
+    /// dequantized) and returns it with `n_tokens = seq_len(layer)`.
+    ///
+    /// # Safety
+    /// `into.k` / `into.v` are device arrays of at least `seq_len(layer)` rows.
+    unsafe fn load(&self, layer: usize, into: LayerCache) -> Result<LayerCache, AirKvError>;
+    /// Every layer empty, all blocks released.
+    fn clear(&mut self);
+    /// Every layer keeps at most `pos` tokens.
+    fn truncate_to(&mut self, pos: usize);
+}
+
+/// A session's KV cache on paged device pools (one per layer), for one
+/// sequence of a [`SequenceManager`]: the `KvCacheManager` of
+/// src/kv_cache.rs:205-414 with paged storage.  It borrows the manager and
+/// the pools; it is neither `Send` nor `Sync` (sessions of one manager
+/// mutate it through the C ABI and must stay on one thread).
+pub struct PagedSessionCache<'a> {
+    raw: *mut sys::air_kv_session,
+    /// Stream for the device work of `save` / `load` / `append`.
+    pub stream: Stream,
+    _borrow: PhantomData<(&'a SequenceManager, &'a KvPool)>,
+}
+
+impl<'a> PagedSessionCache<'a> {
+    /// A new sequence in `mgr` with one pool per layer.
+    pub fn new(mgr: &'a SequenceManager, layer_pools: &[&'a KvPool], stream: Stream) -> Result<Self, AirKvError> {
+        let raws: Vec<*mut sys::air_kv_pool> = layer_pools.iter().map(|p| p.raw).collect();
+        let mut raw = ptr::null_mut();
+        check(unsafe { sys::air_kv_session_create(mgr.raw, raws.as_ptr(), raws.len() as i32, &mut raw) })?;
+        Ok(Self { raw, stream, _borrow: PhantomData })
+    }
+
+    /// A session on `fork_sequence` of this one (src/paged_attention.rs:290-310):
+    /// blocks are shared until either session writes into one.
+    pub fn fork(&self) -> Result<PagedSessionCache<'a>, AirKvError> {
+        let mut raw = ptr::null_mut();
+        check(unsafe { sys::air_kv_session_fork(self.raw, &mut raw) })?;
+        Ok(Self { raw, stream: self.stream, _borrow: PhantomData })
+    }
+
+    pub fn seq_id(&self) -> SeqId {
+        let mut s = 0u32;
+        check(unsafe { sys::air_kv_session_seq_id(self.raw, &mut s) }).expect("air_kv_session_seq_id");
+        SeqId(s)
+    }
+
+    /// Appends `n_new` f32 rows after the layer's stored tokens (the decode
+    /// step's reshape-and-cache).
+    ///
+    /// # Safety
+    /// `k` / `v` are device arrays of `n_new` f32 rows.
+    pub unsafe fn append(&mut self, layer: usize, k: *const f32, v: *const f32, n_new: usize)
+                         -> Result<(), AirKvError> {
+        check(sys::air_kv_session_append(self.raw, self.stream, layer as i32, k, v, n_new as i64)).map(|_| ())
+    }
+
+    /// Device bytes of the session's blocks over all layers (src/kv_cache.rs:388-414).
+    pub fn memory_usage(&self) -> usize {
+        let mut n = 0usize;
+        check(unsafe { sys::air_kv_session_memory_usage(self.raw, &mut n) }).expect("air_kv_session_memory_usage");
+        n
+    }
+}
+
+impl SessionKvCache for PagedSessionCache<'_> {
+    fn seq_len(&self, layer: usize) -> usize {
+        let mut n = 0i64;
+        match check(unsafe { sys::air_kv_session_seq_len(self.raw, layer as i32, &mut n) }) {
+            Ok(_) => n as usize,
+            Err(_) => 0,
+        }
+    }
+
+    unsafe fn save(&mut self, layer: usize, cache: LayerCache) -> Result<(), AirKvError> {
+        if cache.dtype != KvDtype::F32 {
+            return Err(AirKvError { code: sys::AIR_KV_E_INVALID_ARG, message: "save takes f32 rows".into() });
+        }
+        check(sys::air_kv_session_save(self.raw, self.stream, layer as i32, cache.k as *const f32,
+                                       cache.v as *const f32, cache.n_tokens as i64))
+            .map(|_| ())
+    }
+
+    unsafe fn load(&self, layer: usize, into: LayerCache) -> Result<LayerCache, AirKvError> {
+        check(sys::air_kv_session_load(self.raw, self.stream, layer as i32, into.k, into.v, into.dtype as i32))?;
+        Ok(LayerCache { n_tokens: self.seq_len(layer), ..into })
+    }
+
+    fn clear(&mut self) {
+        check(unsafe { sys::air_kv_session_clear(self.raw) }).expect("air_kv_session_clear");
+    }
+
+    fn truncate_to(&mut self, pos: usize) {
+        check(unsafe { sys::air_kv_session_truncate_to(self.raw, pos.min(i64::MAX as usize) as i64) })
+            .expect("air_kv_session_truncate_to");
+    }
+}
+
+impl Drop for PagedSessionCache<'_> {
+    fn drop(&mut self) {
+        unsafe { sys::air_kv_session_destroy(self.raw) };
+    }
+}
 
 // ---------------------------------------------------------------------------
 // KvBlock wire format (src/pd_disagg.rs:39-104)

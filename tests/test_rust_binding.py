@@ -41,5 +41,41 @@ def test_safe_wrapper_calls_only_declared_functions():
                  "num_sequences", "can_schedule", "swap_out", "swap_in", "allocate", "share", "release",
                  "ref_count", "num_free_blocks", "num_used_blocks", "cow_write", "can_allocate",
                  "num_blocks_for_tokens", "utilization", "evict", "restore", "is_evicted", "evicted_count",
-                 "maybe_evict", "serialise", "deserialise"):
-        assert re.search(rf"pub fn {name}\b", wrapper), name
+                 "maybe_evict", "serialise", "deserialise", "try_evict", "try_restore", "restore_pool",
+                 "flash_decode"):
+        assert re.search(rf"pub (unsafe )?fn {name}\b", wrapper), name
+
+
+def test_safe_wrapper_has_session_cache_and_flash_decode():
+    """SessionKvCache (src/kv_cache.rs:431-446) as a trait with its five
+    methods, implemented by PagedSessionCache over the air_kv_session_*
+    calls; flash_decode (src/flash_decode.rs:153-173) as a one-sequence paged
+    decode through air_paged_decode."""
+    wrapper = open(os.path.join(RUST, "airkv", "src", "lib.rs")).read()
+    trait = wrapper[wrapper.index("pub trait SessionKvCache"):]
+    trait = trait[:trait.index("\n}\n")]
+    for name in ("seq_len", "save", "load", "clear", "truncate_to"):
+        assert re.search(rf"fn {name}\(", trait), name
+    impl = wrapper[wrapper.index("impl SessionKvCache for PagedSessionCache"):]
+    impl = impl[:impl.index("\n}\n")]
+    for call in ("air_kv_session_seq_len", "air_kv_session_save", "air_kv_session_load", "air_kv_session_clear",
+                 "air_kv_session_truncate_to"):
+        assert f"sys::{call}(" in impl, call
+    for call in ("air_kv_session_create", "air_kv_session_fork", "air_kv_session_append",
+                 "air_kv_session_destroy", "air_kv_session_memory_usage"):
+        assert f"sys::{call}(" in wrapper, call
+    fd = wrapper[wrapper.index("pub unsafe fn flash_decode("):]
+    fd = fd[:fd.index("\n    }\n")]
+    assert "self.paged_decode(" in fd and "sqrt()" in fd
+
+
+def test_swap_closures_report_failures():
+    """The fallible swap closures map Err to an AIR_KV_E_* status in the
+    trampolines, and evict / restore map each status to its own message
+    instead of one catch-all."""
+    wrapper = open(os.path.join(RUST, "airkv", "src", "lib.rs")).read()
+    for tramp in ("read_tramp", "write_tramp"):
+        body = wrapper[wrapper.index(f"unsafe extern \"C\" fn {tramp}"):]
+        body = body[:body.index("\n}\n")]
+        assert "Err(e) => closure_status(&e)" in body, tramp
+    assert "sys::AIR_KV_E_HIP => \"device block copy failed\"" in wrapper
