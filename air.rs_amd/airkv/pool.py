@@ -194,7 +194,8 @@ class KvPool:
                             max_splits=64, workspace=None, stream=None):
         """One decode step in one launch: append k_new / v_new (float32
         [batch, n_kv_heads, head_dim]) as each sequence's token seq_lens[b] - 1,
-        then attend as paged_decode (BF16 pools, head_dim 128)."""
+        then attend as paged_decode (pools on the matrix-core decode: head_dim 128,
+        BF16, or INT8 / FP8 quantized as append quantizes)."""
         head, tail = self._decode_args(q, block_tables, seq_lens, out, scale, max_splits, workspace, stream)
         rows = self._new_rows(q, k_new, v_new)
         _lib.check(_lib.load().air_paged_decode_append(*head, *rows, *tail), "air_paged_decode_append")

@@ -62,6 +62,50 @@ __device__ __forceinline__ void load8(const void *pages, const float *scales, in
 }
 
 
+// The INT8 / FP8 codes (lo: elements 0..3, hi: 4..7, one byte each) and the
+// group scale of 8 f32 of one scale group: the lanes_per_group consecutive
+// lanes holding the group reduce its absmax with butterfly shuffles (every
+// lane of the group must call this).  The absmax folds from 0.0 with a
+// NaN-ignoring max (src/kv_cache.rs:60, src/fp8.rs:228-232); max is order
+// independent, so the lane-parallel reduction equals the reference's
+// sequential fold.  Shared by the append kernel and the fused append of the
+// decode kernel, so both write the same bytes.
+template <int DT>
+__device__ __forceinline__ void quantize_chunk(const float (&x)[8], int lanes_per_group, uint32_t &lo,
+                                               uint32_t &hi, float &scale) {
+    static_assert(DT == AIR_KV_INT8 || DT == AIR_KV_FP8, "1-byte pages only");
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = absmax_step(m, x[j]);
+    for (int mask = 1; mask < lanes_per_group; mask <<= 1) m = absmax_step(m, __shfl_xor(m, mask));
+    lo = 0;
+    hi = 0;
+    if constexpr (DT == AIR_KV_INT8) {
+        scale = q8_scale(m);
+        float inv;
+        {
+#pragma clang fp contract(off)
+            inv = 1.0f / scale;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) lo |= (uint32_t)(uint8_t)q8_code(x[j], inv) << (8 * j);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hi |= (uint32_t)(uint8_t)q8_code(x[4 + j], inv) << (8 * j);
+    } else {
+        scale = fp8_scale(m);
+        float y;
+        {
+#pragma clang fp contract(off)
+            y = 1.0f / scale;
+        }
+        const bool mark = __builtin_isnormal(scale) && __builtin_isnormal(y);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) lo |= (uint32_t)fp8_code(x[j], scale, y, mark) << (8 * j);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hi |= (uint32_t)fp8_code(x[4 + j], scale, y, mark) << (8 * j);
+    }
+}
+
 // 8 f32 -> page: F32 stored as is, BF16 rounded to nearest even, INT8 / FP8
 // quantized with one scale per scale_group elements; the lanes_per_group
 // consecutive lanes holding one group reduce its absmax with butterfly
@@ -87,39 +131,9 @@ __device__ __forceinline__ void store_row_chunk(const float (&x)[8], void *pages
             pio_store(w, reinterpret_cast<pio_u32x4 *>((uint16_t *)pages + elem));
         }
     } else {
-        // absmax fold from 0.0 with a NaN-ignoring max (src/kv_cache.rs:60,
-        // src/fp8.rs:228-232); max is order independent, so the lane-parallel
-        // reduction equals the reference's sequential fold.
-        float m = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) m = absmax_step(m, x[j]);
-        for (int mask = 1; mask < lanes_per_group; mask <<= 1) m = absmax_step(m, __shfl_xor(m, mask));
-        uint32_t lo = 0, hi = 0;
+        uint32_t lo, hi;
         float scale;
-        if constexpr (DT == AIR_KV_INT8) {
-            scale = q8_scale(m);
-            float inv;
-            {
-#pragma clang fp contract(off)
-                inv = 1.0f / scale;
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) lo |= (uint32_t)(uint8_t)q8_code(x[j], inv) << (8 * j);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) hi |= (uint32_t)(uint8_t)q8_code(x[4 + j], inv) << (8 * j);
-        } else {
-            scale = fp8_scale(m);
-            float y;
-            {
-#pragma clang fp contract(off)
-                y = 1.0f / scale;
-            }
-            const bool mark = __builtin_isnormal(scale) && __builtin_isnormal(y);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) lo |= (uint32_t)fp8_code(x[j], scale, y, mark) << (8 * j);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) hi |= (uint32_t)fp8_code(x[4 + j], scale, y, mark) << (8 * j);
-        }
+        quantize_chunk<DT>(x, lanes_per_group, lo, hi, scale);
         if (valid) {
             pio_store(pio_u32x2{lo, hi}, reinterpret_cast<pio_u32x2 *>((uint8_t *)pages + elem));
             if (lead) scales[scale_idx] = scale;

@@ -48,6 +48,7 @@
 #include "../pool.hpp"
 #include "codecs.hpp"
 #include "decode_common.hpp"
+#include "page_io.hpp"
 
 namespace airkv {
 namespace {
@@ -71,7 +72,7 @@ constexpr int kMinChunk = 4;               // tiles per slice at least
 #define AIRKV_DECODE_QWAVES_PER_EU 3       // the same for int8 pages (fewer raw registers per tile)
 #endif
 #ifndef AIRKV_DECODE_FP8_WAVES_PER_EU
-#define AIRKV_DECODE_FP8_WAVES_PER_EU 4    // fp8 pages (c4 2% faster at 4 than at 3; int8 slower)
+#define AIRKV_DECODE_FP8_WAVES_PER_EU 3    // fp8 pages
 #endif
 #ifndef AIRKV_DECODE_RING
 #define AIRKV_DECODE_RING 1               // tile register sets per wave, bf16 pages (ring - 1 in flight)
@@ -281,6 +282,11 @@ template <int DT> struct Tile {
     u32x4 k16[2];        // 16-byte K loads: head_dim 64*m + 16*g4 .. +16
     u32x4 v[2];
     uint32_t ks, vs;
+    // fused-append kernels, a sequence's last tile: the new token's codes
+    // (lanes 0..15: K head_dim 8*lane .. +8, lanes 16..31: V head_dim
+    // 8*(lane - 16) .. +8) and the scale of the lane's group
+    uint32_t qlo, qhi;
+    float qs;
 };
 template <> struct Tile<AIR_KV_BF16> {
     u32x4 k[4], v[4];
@@ -349,18 +355,23 @@ constexpr int waves_per_simd(int dt) {
                               : AIRKV_DECODE_QWAVES_PER_EU;
 }
 
-// Every build of a page dtype has the same register budget (f32 queries on
-// 1-byte pages are rounded to bf16 once, below, so they carry no lo halves).
-constexpr int kernel_waves_per_simd(int dt, bool) { return waves_per_simd(dt); }
+// The register budget of a build: every query dtype of a page dtype has the
+// same one (f32 queries on 1-byte pages are rounded to bf16 once, below, so
+// they carry no lo halves); the fused append on fp8 pages, whose new rows are
+// quantized inside the tile loop, is built for 3 waves per SIMD (at 4 its
+// encoder's temporaries spilled to scratch inside the loop).
+constexpr int kernel_waves_per_simd(int dt, bool append) {
+    return (append && dt == AIR_KV_FP8) ? 3 : waves_per_simd(dt);
+}
 
 // APPEND (bf16 pages): the launch also writes each sequence's new token,
 // a.k_new / a.v_new, as described at the fused append below.
 template <int D, int BS, bool QF32, int DT, bool APPEND>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kernel_waves_per_simd(DT, QF32))))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kernel_waves_per_simd(DT, APPEND))))
 void decode_mfma_kernel(DecodeArgs a) {
     static_assert(D == 128, "lane mappings assume head_dim 128");
     constexpr bool QUANT = DT != AIR_KV_BF16;
-    static_assert(!(APPEND && QUANT), "the fused append writes bf16 pages");
+    static_assert(!(APPEND && QUANT && !AIRKV_DECODE_K16), "the fused 1-byte append fills 16-byte K loads");
     constexpr int EB = QUANT ? 1 : 2;         // bytes per cache element
     constexpr int KSTEPS = D / 32;            // QK k-steps
     constexpr int DTILES = D / 16;            // PV output tiles along head_dim
@@ -542,6 +553,49 @@ void decode_mfma_kernel(DecodeArgs a) {
         const __amdgpu_buffer_rsrc_t rv =
             __builtin_amdgcn_make_buffer_rsrc((void *)(vp + row0 * D * EB), (short)0, 16 * D * EB, kBufferWord3);
         if constexpr (QUANT) {
+            if constexpr (APPEND) {
+                // Fused append, 1-byte pages, a sequence's last tile: before
+                // the tile's loads are issued (few registers are live here),
+                // the new token's K and V rows load, are quantized as
+                // air_kv_append quantizes them (quantize_chunk: 16 lanes per
+                // row, 8 elements each, scale_group / 8 lanes per group) and
+                // are written to page row nv - 1 with their group scales.
+                // The tile loads below may read that row before or after the
+                // write: compute_tile replaces it in registers either way.
+                if (ok && ((seqend_m >> idx) & 1)) {
+                    const int bq = __builtin_amdgcn_readlane(seq_l, idx);
+                    const int rn = __builtin_amdgcn_readlane(nv_l, idx) - 1;
+                    const int64_t prow = row0 + rn;
+                    const int64_t src = ((int64_t)bq * a.n_kv_heads + kh) * D;
+                    // lanes 0..15 read K, 16..31 V, 8 floats each; the other
+                    // lanes fall outside both descriptors and read zeros
+                    const __amdgpu_buffer_rsrc_t rkn = __builtin_amdgcn_make_buffer_rsrc(
+                        (void *)(a.k_new + src), (short)0, D * 4, kBufferWord3);
+                    const __amdgpu_buffer_rsrc_t rvn = __builtin_amdgcn_make_buffer_rsrc(
+                        (void *)(a.v_new + src), (short)0, D * 4, kBufferWord3);
+                    const int koff = lane < 16 ? 32 * lane : D * 4;
+                    const int voff = (lane >= 16 && lane < 32) ? 32 * (lane - 16) : D * 4;
+                    float x[8];
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        const f32x4 kx = __builtin_bit_cast(
+                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rkn, koff + 16 * i, 0, 0));
+                        const f32x4 vx = __builtin_bit_cast(
+                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rvn, voff + 16 * i, 0, 0));
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) x[4 * i + j] = lane < 16 ? kx[j] : vx[j];
+                    }
+                    const int lpg = a.scale_group >> 3;
+                    quantize_chunk<DT>(x, lpg, t.qlo, t.qhi, t.qs);
+                    const int c = lane & 15;                         // chunk: head_dim 8c .. +8
+                    if (lane < 32) {
+                        uint8_t *pg = (uint8_t *)(lane < 16 ? a.k_pages : a.v_pages);
+                        *reinterpret_cast<u32x2 *>(pg + prow * D + 8 * c) = u32x2{t.qlo, t.qhi};
+                        if (c % lpg == 0)
+                            const_cast<float *>(lane < 16 ? a.k_scales : a.v_scales)[prow * n_sc + c / lpg] = t.qs;
+                    }
+                }
+            }
             if constexpr (AIRKV_DECODE_K16) {
 #pragma unroll
                 for (int m = 0; m < 2; ++m)
@@ -629,7 +683,45 @@ void decode_mfma_kernel(DecodeArgs a) {
         // consumed on all paths and the loads in flight never need draining.
         if (!ok && lane == 0) atomicAdd(a.errors, 1ull);
         const int nv = ok ? __builtin_amdgcn_readlane(nv_l, idx) : 0;   // valid tokens
-        if constexpr (APPEND) {
+        if constexpr (APPEND && QUANT) {
+            // Fused append, 1-byte pages: the new token's codes and scales,
+            // quantized and written to the page by load_tile, move by lane
+            // permutes into the tile registers of row nv - 1, in place of
+            // whatever the tile loads read there.
+            if (ok && ((seqend_m >> idx) & 1)) {
+                const int rn = nv - 1;
+                const int lpg = a.scale_group >> 3;                  // lanes per scale group
+                const uint32_t lo = t.qlo, hi = t.qhi;
+                const float qs = t.qs;
+                // K row rn: lane (rn, g4) holds head_dim 64m + 16 g4 .. +16 in
+                // k16[m], chunks 8m + 2 g4 and the next; its scale is group
+                // 32 g4 / scale_group's
+                const bool krow = r16 == rn;
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    const int sl = 8 * m + 2 * g4;
+                    const u32x4 w = {(uint32_t)__shfl((int)lo, sl), (uint32_t)__shfl((int)hi, sl),
+                                     (uint32_t)__shfl((int)lo, sl + 1), (uint32_t)__shfl((int)hi, sl + 1)};
+                    t.k16[m] = krow ? w : t.k16[m];
+                }
+                const float kq = __shfl(qs, (32 * g4) / a.scale_group * lpg);
+                t.ks = krow ? __float_as_uint(kq) : t.ks;
+                // V row rn: lanes with vrow = rn hold head_dim vcol .. +32,
+                // chunks 16 + vcol / 8 .. +4
+                const bool vhit = vrow == rn;
+                const int sv0 = 16 + vcol / 8;
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int sl = sv0 + 2 * i;
+                    const u32x4 w = {(uint32_t)__shfl((int)lo, sl), (uint32_t)__shfl((int)hi, sl),
+                                     (uint32_t)__shfl((int)lo, sl + 1), (uint32_t)__shfl((int)hi, sl + 1)};
+                    t.v[i] = vhit ? w : t.v[i];
+                }
+                const float vq = __shfl(qs, 16 + vcol / a.scale_group * lpg);
+                t.vs = vhit ? __float_as_uint(vq) : t.vs;
+            }
+        }
+        if constexpr (APPEND && !QUANT) {
             // Fused append: the decode step's new token is row nv - 1 of its
             // sequence's last tile, which this wave alone reads (a sequence
             // longer than its table has no such tile: it appends nothing).
@@ -952,14 +1044,10 @@ template <int BS, bool QF32, int DT>
 hipError_t launch_cfg(const DecodeArgs &a, hipStream_t s) {
     const int64_t waves = (int64_t)a.n_kv_heads * a.slices;
     const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves));
-    if constexpr (DT == AIR_KV_BF16) {
-        if (a.k_new)
-            hipLaunchKernelGGL((decode_mfma_kernel<128, BS, QF32, DT, true>), grid, dim3(kThreads), 0, s, a);
-        else
-            hipLaunchKernelGGL((decode_mfma_kernel<128, BS, QF32, DT, false>), grid, dim3(kThreads), 0, s, a);
-    } else {
+    if (a.k_new)
+        hipLaunchKernelGGL((decode_mfma_kernel<128, BS, QF32, DT, true>), grid, dim3(kThreads), 0, s, a);
+    else
         hipLaunchKernelGGL((decode_mfma_kernel<128, BS, QF32, DT, false>), grid, dim3(kThreads), 0, s, a);
-    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // Sequences average slices / batch pieces: past one round trip's worth,
@@ -1028,7 +1116,8 @@ int plan_decode_mfma(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int
     plan->slices = (int32_t)slices;
     // the f32-query build's slices (what is resident at once; the workspace,
     // sized for plan->slices, holds them whenever that build runs fewer waves)
-    plan->slices_qf32 = (int32_t)slices_for(kernel_waves_per_simd(p.desc.dtype, true));
+    plan->slices_qf32 = (int32_t)slices_for(kernel_waves_per_simd(p.desc.dtype, false));
+    plan->slices_append = (int32_t)slices_for(kernel_waves_per_simd(p.desc.dtype, true));
     plan->batch_per_launch = nb;
     plan->slots = (int32_t)(slices + nb);
     plan->ws_bytes = align256((size_t)(nb + 2) * 4) + align256((size_t)n_q_heads * plan->slots * 2 * 4) +
@@ -1042,7 +1131,7 @@ hipError_t launch_decode_mfma(const DecodeArgs &base, const DecodePlan &plan, vo
         DecodeArgs a = base;
         a.batch = base.batch - b0 < plan.batch_per_launch ? base.batch - b0 : plan.batch_per_launch;
         // partial rows are laid out for plan.slots; fewer slices use a prefix of them
-        a.slices = base.q_dtype == AIR_KV_F32 ? plan.slices_qf32 : plan.slices;
+        a.slices = base.k_new ? plan.slices_append : base.q_dtype == AIR_KV_F32 ? plan.slices_qf32 : plan.slices;
         a.slots = a.slices + plan.batch_per_launch;
         const int64_t q_row = (int64_t)b0 * a.n_q_heads * 128;
         a.q = (const char *)base.q + q_row * (base.q_dtype == AIR_KV_F32 ? 4 : 2);

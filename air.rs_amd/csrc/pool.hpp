@@ -42,6 +42,7 @@ struct DecodePlan {
     // balanced slices (matrix-core kernel)
     int32_t slices;       // slices per kv head (one wave each)
     int32_t slices_qf32;  // the same for f32 queries (their kernel may hold fewer waves per SIMD)
+    int32_t slices_append;  // the same for the fused append + decode
     int32_t batch_per_launch;
     int32_t max_splits;   // pieces per sequence at most
     int32_t slots;        // partial rows per (kv head, q head of the group): slices + batch

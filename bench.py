@@ -311,6 +311,31 @@ def config_decode(torch, name, iters=20):
            "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4), "cached_tokens": tok,
            "batch": cfg.batch, "kv_dtype": {airkv.BF16: "bf16", airkv.INT8: "int8", airkv.FP8: "fp8"}[cfg.dtype],
            "block_size": cfg.block_size, "n_q_heads": cfg.n_q_heads}
+    # the decode step as one launch (air_paged_decode_append: each
+    # sequence's new K / V row -- quantized on 1-byte pages -- written by the
+    # wave that attends over it) and as two calls (append, then decode); the
+    # step rewrites each sequence's last token, so every call moves the same
+    # bytes
+    kn = torch.randn(cfg.batch, cfg.n_kv_heads, cfg.head_dim, device="cuda")
+    vn = torch.randn_like(kn)
+    last = (lens.astype(np.int64) - 1)
+    step_slots = torch.from_numpy(tables[np.arange(cfg.batch), last // cfg.block_size].astype(np.int64)
+                                  * cfg.block_size + last % cfg.block_size).cuda()
+    fused = alternating([p.bind_decode_append(q, kn, vn, tt, lt, out, ws, max_splits=cfg.max_splits)
+                         for p in (pool, twin)])
+    fused()
+    ms_f = timed_loop(torch, fused, iters)
+    apps = [p.bind_append(kn, vn, step_slots) for p in (pool, twin)]
+    decs = [p.bind_decode(q, tt, lt, out, ws, max_splits=cfg.max_splits) for p in (pool, twin)]
+    two = alternating([(lambda a=a, d=d: (a(), d())) for a, d in zip(apps, decs)])
+    two()
+    ms_2 = timed_loop(torch, two, iters)
+    app_bytes = cfg.batch * (cfg.n_kv_heads * cfg.head_dim * 2 * 4 + per_tok)   # f32 rows in, page row out
+    step_bytes = nbytes + app_bytes
+    res["step_fused"] = {"us": round(ms_f * 1e3, 1), "gbps": round(step_bytes / (ms_f * 1e-3) / 1e9, 1),
+                         "frac": round(step_bytes / (ms_f * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+    res["step_two_call"] = {"us": round(ms_2 * 1e3, 1),
+                            "gbps": round((step_bytes + 8 * cfg.batch) / (ms_2 * 1e-3) / 1e9, 1)}
     if cfg.dtype in (airkv.INT8, airkv.FP8):
         # the dequantizing gather of every sequence to contiguous f32
         # [head][len][dim] (code * scale, src/kv_cache.rs:78-92,

@@ -281,9 +281,11 @@ int air_paged_decode(air_kv_pool *pool, void *stream, const void *q, int32_t q_d
  * the wave that attends over it, so no launch orders the two.  Sequences of
  * length 0 append nothing; a sequence longer than its table, or whose last
  * block is outside the pool, appends nothing and is counted as by
- * air_paged_decode.  BF16 pools on the matrix-core decode only (head_dim 128,
- * group 1..16); other pools return AIR_KV_E_INVALID_ARG (use air_kv_append,
- * then air_paged_decode).  k_new and v_new are 16-byte aligned device
+ * air_paged_decode.  Pools on the matrix-core decode only (head_dim 128,
+ * block_size 16 or 32, group 1..16; BF16, or INT8 / FP8 with scale_group >=
+ * 32, whose new rows are quantized exactly as air_kv_append quantizes them:
+ * the same codes and group scales); other pools return AIR_KV_E_INVALID_ARG
+ * (use air_kv_append, then air_paged_decode).  k_new and v_new are 16-byte aligned device
  * pointers.  The workspace is air_paged_decode's. */
 int air_paged_decode_append(air_kv_pool *pool, void *stream, const void *q, int32_t q_dtype,
                             int32_t n_q_heads, const float *k_new, const float *v_new,
@@ -331,7 +333,11 @@ int air_paged_decode_noalloc(air_kv_pool *pool, void *stream, const void *q, int
  * once); a work group whose result that way is not finite, or whose outputs
  * of a query row are all below 2^-14 in magnitude, is recomputed with bf16
  * operands: probabilities as two bf16 halves on BF16 pools, keys as two bf16
- * halves on INT8 / FP8 pools.  A sequence whose rows do not lie in
+ * halves on INT8 / FP8 pools.  The f16 pass bounds each output's error
+ * relative to the largest output of its query row, not to its own value
+ * channel: a channel whose values lie far below the others' (under 2^-17
+ * while others are near 1) keeps f16's absolute resolution, errors up to
+ * 2^-24, not 1e-3 of its own magnitude.  A sequence whose rows do not lie in
  * [0, total_q], whose seq_len is outside [0, max_blocks * block_size] or
  * whose q_len exceeds its seq_len is counted (air_kv_pool_error_count) and its
  * rows (when they lie in [0, total_q]) are zero-filled; out-of-pool table

@@ -7,8 +7,9 @@ Covered: sequences of 1 token and with full and partial last tiles,
 sequences whose last tile sits in a later slice than their first, a batch
 that takes two launches, GQA groups 1, 2, 4, 8 and 16, bf16 and f32 queries, page sizes
 16 and 32, a sequence of length 0, a last block outside the pool, a sequence
-longer than its table, repeated calls, and the pools the fused path
-rejects."""
+longer than its table, repeated calls, int8 (Q8_0) and fp8 pools (the new
+rows quantized in the launch: codes and scales bit-exact with air_kv_append
+and with the oracle), and the pools the fused path rejects."""
 import ctypes
 
 import numpy as np
@@ -75,14 +76,25 @@ def _run_pair(cfg, pa, pb, host, tables, lens, k_new, v_new, q, q_f32, out_f32=T
     pa.paged_decode(qt, t, sl, out_a, max_splits=cfg.max_splits, workspace=ws)
     pb.paged_decode_append(qt, kn, vn, t, sl, out_b, max_splits=cfg.max_splits, workspace=ws)
     torch.cuda.synchronize()
-    ka, va, _, _ = pa.snapshot()
-    kb, vb, _, _ = pb.snapshot()
+    ka, va, ksa, vsa = pa.snapshot()
+    kb, vb, ksb, vsb = pb.snapshot()
     assert_bits_equal(kb, ka, "k pages")
     assert_bits_equal(vb, va, "v pages")
+    if ksa is not None:                               # 1-byte pools: the group scales too
+        assert_bits_equal(ksb.view(np.uint32), ksa.view(np.uint32), "k scales")
+        assert_bits_equal(vsb.view(np.uint32), vsa.view(np.uint32), "v scales")
     got_a, got_b = out_a.float().cpu().numpy(), out_b.float().cpu().numpy()
     assert_floats_bit_equal(got_b, got_a, "decode output")
     if len(idx):
         assert host.append(k_new[idx], v_new[idx], slots) == 0
+    # the fused pool against the oracle's append of the same rows
+    assert_bits_equal(kb.reshape(host.k.shape), host.k, "k pages vs oracle")
+    assert_bits_equal(vb.reshape(host.v.shape), host.v, "v pages vs oracle")
+    if ksa is not None:
+        assert_bits_equal(ksb.reshape(host.k_scales.shape).view(np.uint32), host.k_scales.view(np.uint32),
+                          "k scales vs oracle")
+        assert_bits_equal(vsb.reshape(host.v_scales.shape).view(np.uint32), host.v_scales.view(np.uint32),
+                          "v scales vs oracle")
     return q, got_b
 
 
@@ -102,6 +114,51 @@ def test_decode_append_matches_append_then_decode(n_q, bs, q_f32):
     log(f"  identical to append + decode; rel err vs oracle {err:.2e}")
     assert err <= TOL_BF16
     assert pa.error_count() == 0 and pb.error_count() == 0
+
+
+@pytest.mark.parametrize("dtype,n_q,bs,q_f32", [(airkv.INT8, 64, 16, False), (airkv.INT8, 32, 32, True),
+                                                (airkv.FP8, 64, 32, False), (airkv.FP8, 32, 16, True),
+                                                (airkv.INT8, 128, 16, False), (airkv.FP8, 8, 32, False)])
+def test_decode_append_quantized_pools(dtype, n_q, bs, q_f32):
+    """int8 (Q8_0) and fp8 pools: the fused launch quantizes each new K / V
+    row into its page -- codes and group scales bit-exact with air_kv_append
+    and with the oracle's append -- and its outputs are bit-exact with
+    air_kv_append + air_paged_decode and within 2e-2 of the oracle.  The new
+    rows carry outliers (channels x20) and a row of zeros, so scales of
+    several magnitudes and the zero-group scale rule are exercised."""
+    log(f"decode_append quantized dtype={dtype} n_q={n_q} bs={bs} q_f32={q_f32}")
+    ctx = [0, 15, 16, 31, 32, 100, 700, 1500, 2200, 4095]
+    cfg = workloads.Config("decode_append_q", n_q, 8, 128, bs, dtype, len(ctx))
+    w, pa, pb, host, tables, lens, k_new, v_new = _setup(cfg, ctx, seed=171 + bs + n_q + dtype)
+    k_new, v_new = k_new.copy(), v_new.copy()
+    k_new[:, :, 5] *= 20.0
+    v_new[:, :, 77] *= 20.0
+    k_new[3] = 0.0                                     # an all-zero row: scale 1.0, codes 0
+    v_new[4, 2, :40] = -0.0
+    q = np.random.default_rng(173).standard_normal((cfg.batch, n_q, 128)).astype(np.float32)
+    q, got = _run_pair(cfg, pa, pb, host, tables, lens, k_new, v_new, q, q_f32)
+    want = host.paged_decode(q, tables, lens, chunk=64)   # (f32 queries: the device rounds them to bf16)
+    err = rel_err(got, want)
+    log(f"  identical to append + decode (pages, scales, outputs); rel err vs oracle {err:.2e}")
+    assert err <= 2e-2
+    assert pa.error_count() == 0 and pb.error_count() == 0
+
+
+@pytest.mark.parametrize("dtype", [airkv.INT8, airkv.FP8])
+def test_decode_append_quantized_long_sequences(dtype):
+    """1-byte pools with two long sequences spread over many slices: the last
+    tile of each is computed by a later slice than the first, and pieces
+    merge; pages, scales and outputs identical to the two-call path."""
+    log(f"decode_append quantized multi-slice dtype={dtype}")
+    ctx = [20000, 9000]
+    cfg = workloads.Config("decode_append_qlong", 64, 8, 128, 32, dtype, len(ctx))
+    w, pa, pb, host, tables, lens, k_new, v_new = _setup(cfg, ctx, seed=181 + dtype)
+    q = np.random.default_rng(182).standard_normal((cfg.batch, 64, 128)).astype(np.float32)
+    q, got = _run_pair(cfg, pa, pb, host, tables, lens, k_new, v_new, q, q_f32=False, out_f32=False)
+    want = host.paged_decode(q, tables, lens, chunk=256)
+    err = rel_err(got, want)
+    log(f"  identical; rel err vs oracle {err:.2e}")
+    assert err <= 2e-2 + 2 ** -8
 
 
 def test_decode_append_multi_slice_sequences():
@@ -175,13 +232,14 @@ def test_decode_append_repeat_is_stable():
     assert_bits_equal(v2, v1, "v pages")
 
 
-@pytest.mark.parametrize("dtype,n_q,head_dim,bs", [(airkv.INT8, 32, 128, 16), (airkv.FP8, 32, 128, 16),
-                                                    (airkv.BF16, 32, 64, 16), (airkv.F32, 32, 128, 16)])
-def test_decode_append_rejects_other_pools(dtype, n_q, head_dim, bs):
-    """1-byte and f32 pools and head_dim 64 decode on the two-call path: the
-    fused entry returns AIR_KV_E_INVALID_ARG before any device work."""
+@pytest.mark.parametrize("dtype,n_q,head_dim,bs,group", [(airkv.INT8, 32, 64, 16, 32), (airkv.FP8, 32, 128, 16, 16),
+                                                          (airkv.BF16, 32, 64, 16, 32), (airkv.F32, 32, 128, 16, 32)])
+def test_decode_append_rejects_other_pools(dtype, n_q, head_dim, bs, group):
+    """Pools off the matrix-core decode -- f32 pages, head_dim 64, 1-byte
+    pages with scale groups of 16 -- decode on the two-call path: the fused
+    entry returns AIR_KV_E_INVALID_ARG before any device work."""
     torch = torch_mod()
-    pool = airkv.KvPool(64, bs, 8, head_dim, dtype)
+    pool = airkv.KvPool(64, bs, 8, head_dim, dtype, group)
     q = torch.zeros((2, n_q, head_dim), device="cuda")
     kn = torch.zeros((2, 8, head_dim), device="cuda")
     t = torch.zeros((2, 4), dtype=torch.int32, device="cuda")
