@@ -16,6 +16,9 @@
 //             4 KB slots: the gather's pattern
 //   page_mix21 8 KB of contiguous rows read per 4 KB page written in a
 //             shuffled order: the append's pattern
+//   copy / mix21 persistent: the same contiguous patterns as grid-stride
+//             loops over 8 workgroups per CU with 128 or 256 bytes of loads
+//             in flight per thread
 //
 // Each pattern has a plain and a non-temporal (`nt`: streaming) variant of
 // its loads and of its stores; the bench reports the faster.  Every thread
@@ -151,6 +154,55 @@ __global__ __launch_bounds__(kThreads) void page_mix21_kernel(const u32x4 *src, 
     for (int i = 0; i < 4; ++i) st16<NTS>(dst + 64 * i, x[2 * i] ^ x[2 * i + 1]);
 }
 
+// Persistent grid-stride forms of copy and mix21: a grid of 8 workgroups per
+// CU, each thread keeping U 16-byte loads in flight (U = 8: 128 B, U = 16:
+// 256 B) before its stores, the loads of one step a grid apart so each wave
+// instruction still covers 1 KB of consecutive lines.
+template <bool NTL, bool NTS, int U>
+__global__ __launch_bounds__(kThreads) void copy_persist_kernel(const u32x4 *src, u32x4 *dst, int64_t n16) {
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t base = (int64_t)blockIdx.x * kThreads + threadIdx.x; base + (U - 1) * stride < n16;
+         base += U * stride) {
+        u32x4 v[U];
+#pragma unroll
+        for (int i = 0; i < U; ++i) v[i] = ld16<NTL>(src + base + i * stride);
+#pragma unroll
+        for (int i = 0; i < U; ++i) st16<NTS>(dst + base + i * stride, v[i]);
+    }
+}
+
+// U loads in flight, U / 2 stores (two bytes read per byte written).
+template <bool NTL, bool NTS, int U>
+__global__ __launch_bounds__(kThreads) void mix21_persist_kernel(const u32x4 *src, u32x4 *dst, int64_t n16) {
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    int64_t obase = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    for (int64_t base = obase; base + (U - 1) * stride < n16; base += U * stride, obase += U / 2 * stride) {
+        u32x4 v[U];
+#pragma unroll
+        for (int i = 0; i < U; ++i) v[i] = ld16<NTL>(src + base + i * stride);
+#pragma unroll
+        for (int i = 0; i < U / 2; ++i) st16<NTS>(dst + obase + i * stride, v[2 * i] ^ v[2 * i + 1]);
+    }
+}
+
+template <int U>
+void launch_persist(bool mix, bool ntl, bool nts, dim3 g, dim3 b, hipStream_t s, const u32x4 *in, u32x4 *out,
+                    int64_t n16) {
+#define AIRKV_PERSIST(K, L, S) hipLaunchKernelGGL((K<L, S, U>), g, b, 0, s, in, out, n16)
+    if (mix) {
+        if (ntl && nts) AIRKV_PERSIST(mix21_persist_kernel, true, true);
+        else if (ntl) AIRKV_PERSIST(mix21_persist_kernel, true, false);
+        else if (nts) AIRKV_PERSIST(mix21_persist_kernel, false, true);
+        else AIRKV_PERSIST(mix21_persist_kernel, false, false);
+    } else {
+        if (ntl && nts) AIRKV_PERSIST(copy_persist_kernel, true, true);
+        else if (ntl) AIRKV_PERSIST(copy_persist_kernel, true, false);
+        else if (nts) AIRKV_PERSIST(copy_persist_kernel, false, true);
+        else AIRKV_PERSIST(copy_persist_kernel, false, false);
+    }
+#undef AIRKV_PERSIST
+}
+
 dim3 grid_for(int64_t n16) { return dim3((unsigned)(n16 / (kThreads * 4))); }
 
 }  // namespace
@@ -161,7 +213,9 @@ extern "C" {
 // (src = K pool, dst = V pool, bytes = one pool's bytes, pages / n_pages =
 // the page list), 5 page_copy (as page_read, written to `sink`, which holds
 // 2 * n_pages * 4 KB), 6 page_mix21 (src holds 2 * n_pages * 8 KB of rows,
-// dst = K pool, sink = V pool).  nt_load / nt_store pick the non-temporal variants.
+// dst = K pool, sink = V pool), 7 / 8 persistent copy with 128 / 256 B in
+// flight per thread, 9 / 10 persistent mix21 likewise.  nt_load / nt_store
+// pick the non-temporal variants.
 // Returns 0 or the hipError_t of the launch.
 int air_ceiling_launch(int kind, int nt_load, int nt_store, const void *src, void *dst, int64_t bytes,
                        const int32_t *pages, int64_t n_pages, void *sink, void *stream) {
@@ -234,6 +288,20 @@ int air_ceiling_launch(int kind, int nt_load, int nt_store, const void *src, voi
             hipLaunchKernelGGL((page_mix21_kernel<false, true>), gp, b, 0, s, in, out, vp, pages, n_pages, pool_pages);
         else
             hipLaunchKernelGGL((page_mix21_kernel<false, false>), gp, b, 0, s, in, out, vp, pages, n_pages, pool_pages);
+        break;
+    }
+    case 7:    // copy, persistent, 128 B in flight per thread
+    case 8:    // copy, persistent, 256 B
+    case 9:    // mix21, persistent, 128 B (bytes = bytes read)
+    case 10: { // mix21, persistent, 256 B
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            return (int)hipErrorInvalidValue;
+        const dim3 gp((unsigned)(cus * 8));
+        const bool mix = kind >= 9;
+        if (kind == 7 || kind == 9) launch_persist<8>(mix, nt_load, nt_store, gp, b, s, in, out, n16);
+        else launch_persist<16>(mix, nt_load, nt_store, gp, b, s, in, out, n16);
         break;
     }
     default:

@@ -36,6 +36,57 @@ struct AppendArgs {
     unsigned long long *errors;
 };
 
+// F32 / BF16 pages, head_dim 128: each wave covers four consecutive tokens of
+// one head as above, but lane l moves 4 elements at 4l and 4 at 256 + 4l of
+// the wave's 512, so every 16-byte source load instruction reads two whole
+// 512-byte rows and every page store instruction writes two whole page rows
+// (8 consecutive elements per lane made each load instruction read half of
+// every cache line it touched).
+template <int DT>
+__global__ __launch_bounds__(kThreads) void kv_append_rows_kernel(AppendArgs a) {
+    static_assert(DT == AIR_KV_F32 || DT == AIR_KV_BF16, "unquantized pages");
+    constexpr int D = 128;
+    const int lane = threadIdx.x & 63;
+    const int64_t wave_g = ((int64_t)blockIdx.x * kThreads + threadIdx.x) >> 6;   // (token group of 4, head)
+    const int h = (int)(wave_g % a.n_kv_heads);
+    const int64_t t0 = (wave_g / a.n_kv_heads) * 4;
+    f32x4 kx[2], vx[2];
+    int64_t dst[2];
+    bool ok[2];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        const int e = 256 * half + 4 * lane;               // element of the wave's four rows
+        const int64_t t = t0 + e / D;
+        const int col = e % D;
+        const bool active = t < a.n_tokens;
+        const int64_t slot = active ? a.slots[t] : -1;
+        ok[half] = slot >= 0 && slot < a.num_slots;
+        if (active && slot >= a.num_slots && col == 0 && h == 0) atomicAdd(a.errors, 1ull);
+        const int64_t src = (active ? t * a.n_kv_heads + h : 0) * D + col;
+        kx[half] = active ? __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a.k + src)) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        vx[half] = active ? __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a.v + src)) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        const int64_t blk = ok[half] ? slot / a.block_size : 0;
+        const int64_t off = ok[half] ? slot - blk * a.block_size : 0;
+        dst[half] = ((blk * a.n_kv_heads + h) * a.block_size + off) * D + col;
+    }
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        if (!ok[half]) continue;
+        if constexpr (DT == AIR_KV_F32) {
+            pio_store(kx[half], reinterpret_cast<f32x4 *>((float *)a.k_pages + dst[half]));
+            pio_store(vx[half], reinterpret_cast<f32x4 *>((float *)a.v_pages + dst[half]));
+        } else {
+            const f32x4 k = kx[half], v = vx[half];
+            pio_store(u32x2{(uint32_t)bf16_rne(k[0]) | ((uint32_t)bf16_rne(k[1]) << 16),
+                            (uint32_t)bf16_rne(k[2]) | ((uint32_t)bf16_rne(k[3]) << 16)},
+                      reinterpret_cast<u32x2 *>((uint16_t *)a.k_pages + dst[half]));
+            pio_store(u32x2{(uint32_t)bf16_rne(v[0]) | ((uint32_t)bf16_rne(v[1]) << 16),
+                            (uint32_t)bf16_rne(v[2]) | ((uint32_t)bf16_rne(v[3]) << 16)},
+                      reinterpret_cast<u32x2 *>((uint16_t *)a.v_pages + dst[half]));
+        }
+    }
+}
+
 template <int DT>
 __global__ __launch_bounds__(kThreads) void kv_append_kernel(AppendArgs a) {
     // thread -> (chunk c, token t % 4, kv head h, token t / 4), chunk fastest:
@@ -118,9 +169,16 @@ hipError_t launch_append(const air_kv_pool &p, hipStream_t s, const float *k, co
         c.n_tokens = nt;
         const int64_t threads = (nt + 3) / 4 * 4 * per_token;
         dim3 grid((unsigned)((threads + kThreads - 1) / kThreads));
+        const bool rows128 = p.desc.head_dim == 128;     // the whole-line form above
         switch (p.desc.dtype) {
-        case AIR_KV_F32: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_F32>, grid, dim3(kThreads), 0, s, c); break;
-        case AIR_KV_BF16: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_BF16>, grid, dim3(kThreads), 0, s, c); break;
+        case AIR_KV_F32:
+            if (rows128) hipLaunchKernelGGL(kv_append_rows_kernel<AIR_KV_F32>, grid, dim3(kThreads), 0, s, c);
+            else hipLaunchKernelGGL(kv_append_kernel<AIR_KV_F32>, grid, dim3(kThreads), 0, s, c);
+            break;
+        case AIR_KV_BF16:
+            if (rows128) hipLaunchKernelGGL(kv_append_rows_kernel<AIR_KV_BF16>, grid, dim3(kThreads), 0, s, c);
+            else hipLaunchKernelGGL(kv_append_kernel<AIR_KV_BF16>, grid, dim3(kThreads), 0, s, c);
+            break;
         case AIR_KV_INT8: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_INT8>, grid, dim3(kThreads), 0, s, c); break;
         default: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_FP8>, grid, dim3(kThreads), 0, s, c); break;
         }

@@ -59,6 +59,36 @@ __device__ __forceinline__ void store8(void *out, int64_t elem, const float (&x)
     }
 }
 
+// Page -> 4 f32 (one 16-byte output store): 4 consecutive elements of one row,
+// dequantized as load8 does (INT8/FP8: q as f32 * scale, src/kv_cache.rs:88,
+// src/fp8.rs:263-264; BF16 widened exactly; F32 as stored).
+template <int DT>
+__device__ __forceinline__ f32x4 load4(const void *pages, const float *scales, int64_t elem, int64_t scale_idx) {
+    if constexpr (DT == AIR_KV_F32) {
+        return __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>((const float *)pages + elem));
+    } else if constexpr (DT == AIR_KV_BF16) {
+        const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>((const uint16_t *)pages + elem));
+        return f32x4{__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xFFFF0000u),
+                     __uint_as_float(w[1] << 16), __uint_as_float(w[1] & 0xFFFF0000u)};
+    } else {
+        const uint32_t w = __builtin_nontemporal_load((const uint32_t *)((const uint8_t *)pages + elem));
+        const float sc = scales[scale_idx];
+        f32x4 x;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t byte = (w >> (8 * j)) & 0xFFu;
+            float val;
+            if constexpr (DT == AIR_KV_INT8) val = (float)(int32_t)(int8_t)byte;
+            else val = fp8_decode(byte);
+            {
+#pragma clang fp contract(off)
+                x[j] = val * sc;
+            }
+        }
+        return x;
+    }
+}
+
 template <int DT, int OUT>
 __global__ __launch_bounds__(kThreads) void kv_gather_kernel(GatherArgs a) {
     __shared__ int32_t s_prefix[kMaxSeqsPerLaunch + 1];
@@ -125,6 +155,50 @@ __global__ __launch_bounds__(kThreads) void kv_gather_kernel(GatherArgs a) {
             continue;
         }
         const int64_t out_base = a.out_offsets[b];
+        if constexpr (OUT == AIR_KV_F32) {
+            // f32 outputs: lane l of a wave takes 4 elements at 4l and 4 at
+            // 256 + 4l of the wave's 512, so each 16-byte store instruction
+            // writes 1 KB of whole cache lines (8 elements per lane as two
+            // stores 16 bytes apart left every instruction half of each line)
+            const int wbase = (tid >> 6) * 512 + 4 * lane;
+            for (int e0 = wbase; e0 < tile_elems; e0 += kThreads * 8) {
+                for (int h0 = 0; h0 < a.n_kv_heads; h0 += kHeadUnroll) {
+                    f32x4 xk[kHeadUnroll][2], xv[kHeadUnroll][2];
+#pragma unroll
+                    for (int half = 0; half < 2; ++half) {
+                        const int e = e0 + 256 * half;
+                        const int r = e / d, col = e - r * d;
+#pragma unroll
+                        for (int u = 0; u < kHeadUnroll; ++u) {
+                            const int h = h0 + u < a.n_kv_heads ? h0 + u : a.n_kv_heads - 1;
+                            const int64_t src_row = ((int64_t)blk * a.n_kv_heads + h) * rows + r;
+                            const int64_t src = src_row * d + col;
+                            const int64_t sidx = src_row * ng + col / (a.scale_group > 0 ? a.scale_group : 1);
+                            xk[u][half] = load4<DT>(a.k_pages, a.k_scales, src, sidx);
+                            xv[u][half] = load4<DT>(a.v_pages, a.v_scales, src, sidx);
+                        }
+                    }
+#pragma unroll
+                    for (int half = 0; half < 2; ++half) {
+                        const int e = e0 + 256 * half;
+                        const int r = e / d, col = e - r * d;
+                        const int64_t t = (int64_t)p * rows + r;
+                        if (e >= tile_elems || t >= len) continue;
+#pragma unroll
+                        for (int u = 0; u < kHeadUnroll; ++u) {
+                            const int h = h0 + u;
+                            if (h >= a.n_kv_heads) break;
+                            const int64_t dst = out_base + (a.layout == AIR_KV_LAYOUT_HEAD_MAJOR
+                                                                ? ((int64_t)h * len + t) * d + col
+                                                                : (t * a.n_kv_heads + h) * d + col);
+                            __builtin_nontemporal_store(xk[u][half], reinterpret_cast<f32x4 *>((float *)a.out_k + dst));
+                            __builtin_nontemporal_store(xv[u][half], reinterpret_cast<f32x4 *>((float *)a.out_v + dst));
+                        }
+                    }
+                }
+            }
+            continue;
+        }
         for (int e = tid * 8; e < tile_elems; e += kThreads * 8) {
             const int r = e / d, col = e - r * d;
             const int64_t t = (int64_t)p * rows + r;
