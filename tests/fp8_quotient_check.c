@@ -47,10 +47,37 @@ static uint64_t next(void) { state ^= state << 13; state ^= state >> 7; state ^=
 
 int main(int argc, char **argv) {
     long n = argc > 1 ? atol(argv[1]) : 20000000L, tested = 0, bad = 0;
+    /* quotients exactly at the rounding boundary of zero: |x| / scale = 2^-150
+     * (ties to the even zero) and one step either side of it */
+    for (int k = 1; k <= 64; ++k) {
+        for (int sgn = 0; sgn < 2; ++sgn) {
+            for (int d = -1; d <= 1; ++d) {
+                float x = ffrom((uint32_t)k);                          /* k * 2^-149 */
+                float m = ldexpf(448.0f * (float)k, 1);                /* scale = 2k: x / scale = 2^-150 */
+                m = ffrom(fbits(m) + (uint32_t)d);
+                if (sgn) x = -x;
+                float s = scale_of(m);
+                volatile float qd = x / s;
+                uint8_t want = encode(qd), got = code_product(x, s);
+                ++tested;
+                if (want != got) {
+                    if (bad < 8) printf("tie x=%a absmax=%a: division %02x, product %02x\n", x, m, want, got);
+                    ++bad;
+                }
+            }
+        }
+    }
     for (long i = 0; i < n; ++i) {
         uint64_t r = next(), r2 = next();
         float x, m;
-        switch (i % 5) {
+        switch (i % 6) {
+        case 5: { /* a group holding an infinity or a NaN (scale not normal) */
+            const uint32_t kind = (uint32_t)(r2 % 4);
+            m = kind == 0 ? NAN : INFINITY;
+            x = kind == 1 ? INFINITY : ffrom((uint32_t)(r & 0x7F7FFFFFu));
+            if (kind == 3) x = ffrom((uint32_t)(r & 0x007FFFFFu));
+            break;
+        }
         case 0:   /* x a random fraction of a random absmax */
             m = ffrom((uint32_t)(r & 0x7F7FFFFFu));
             x = m * (float)((double)(r2 >> 11) / 9007199254740992.0);
@@ -79,9 +106,11 @@ int main(int argc, char **argv) {
             m = fabsf(x) / (float)((double)(((r2 >> 23) & 0xFFFFFF) | 1) / 16777216.0);
             break;
         }
-        if (!(m == m) || isinf(m) || m < fabsf(x)) m = fabsf(x);
+        if (i % 6 != 5 && (!(m == m) || isinf(m) || m < fabsf(x))) m = fabsf(x);
         if (r & (1ull << 63)) x = -x;
-        float s = scale_of(m);
+        /* a NaN absmax is skipped by the fold (Rust's f32::max); an infinite
+         * one gives scale = inf */
+        float s = m != m ? 1.0f : scale_of(m);
         volatile float qd = x / s;
         uint8_t want = encode(qd), got = code_product(x, s);
         ++tested;

@@ -4,11 +4,12 @@ of a division per element (air.rs_amd/csrc/kernels/codecs.hpp fp8_code).
 tests/fp8_quotient_check.c compares the two on 2e7 random and boundary cases
 (random fractions of random absmax values, subnormal elements, quotients at
 the smallest subnormal and at the encoder's half-up mantissa boundaries,
-every code range); built with gcc here, on the CPU, whose f32 arithmetic and
-fma round as the GPU's do.  Skipping the correction step makes codes at the
-mantissa boundaries differ.  The exact division the GPU keeps for quotients
-that come out subnormal or zero changed no code in these cases; it guards
-the sign of a quotient at the smallest subnormal."""
+every code range, groups holding an infinity, and quotients exactly at the
+zero rounding boundary 2^-150); built with gcc here, on the CPU, whose f32
+arithmetic and fma round as the GPU's do.  Skipping the correction step makes
+codes at the mantissa boundaries differ.  The exact division the GPU keeps
+for quotients that come out subnormal or zero guards the sign of a quotient
+at the zero boundary, and groups holding an infinity divide."""
 import os
 import shutil
 import subprocess
