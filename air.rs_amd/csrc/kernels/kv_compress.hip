@@ -63,8 +63,10 @@ __device__ __forceinline__ bool row_elem(const RowSource &s, int64_t r, int dim,
 // consecutive loads of one lane and must stay in cache between them (a
 // streaming load would fetch it again).  INT8 / FP8 rows are dequantized as
 // q * scale with one rounding (src/kv_cache.rs:88, src/fp8.rs:263-264).
-// Rows of out-of-pool blocks read as zeros and `live` is false for them.
-template <int DT, int D, int N = D>
+// Rows of out-of-pool blocks read as zeros (block 0's bytes when ZERO_DEAD is
+// false: for callers that overwrite every output of such a row) and `live`
+// is false for them.
+template <int DT, int D, int N = D, bool ZERO_DEAD = true>
 __device__ __forceinline__ void load_row(const RowSource &s, int64_t r, float (&x)[N], bool &live,
                                          int first = 0) {
     typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -104,7 +106,7 @@ __device__ __forceinline__ void load_row(const RowSource &s, int64_t r, float (&
             }
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[8 * c + j] = live ? v[j] : 0.0f;
+        for (int j = 0; j < 8; ++j) x[8 * c + j] = (!ZERO_DEAD || live) ? v[j] : 0.0f;
     }
 }
 
@@ -306,7 +308,9 @@ __global__ __launch_bounds__(kThreads) void value_compress_kernel(CompressArgs a
         const int64_t r = t / P;
         float x[N];
         bool live;
-        load_row<DT, D, N>(a.src, r, x, live, part * N);
+        // a row of an out-of-pool block gets zero codes, scale and min below,
+        // whatever its loaded values were, so they are not zeroed first
+        load_row<DT, D, N, false>(a.src, r, x, live, part * N);
         if (!live && a.errors && part == 0 && (r % a.src.rows_per_block) == 0) atomicAdd(a.errors, 1ull);
         // (:198-199).  The folds' value is the row's NaN-ignoring min / max,
         // which the hardware min / max give in one instruction per element

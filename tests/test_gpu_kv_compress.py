@@ -221,6 +221,7 @@ def test_compress_blocks_out_of_pool_ids_counted_and_zeroed(n_kv):
     rows = n_kv * 16
     assert torch.all(out["key_magnitude"][rows:] == 0) and torch.all(out["value_codes"][rows:] == 0)
     assert torch.all(out["value_scale"][rows:] == 0) and torch.all(out["key_mean"][rows:] == 0)
+    assert torch.all(out["value_min"][rows:] == 0)
     assert torch.all(out["key_magnitude"][:rows] > 0)
 
 
