@@ -305,8 +305,13 @@ int air_paged_decode_append(air_kv_pool *pool, void *stream, const void *q, int3
  * it calls no hipMalloc / hipFree.  A launch whose
  * air_paged_decode_workspace_size exceeds the array returns
  * AIR_KV_E_INVALID_ARG (32 MiB holds configs c2-c5: c4 needs 17.3 MB).
- * Every call on one GPU shares that GPU's array: calls that overlap in time
- * on one GPU (other streams or threads) race and must be serialised. */
+ * Every call on one GPU shares that GPU's array, so the library orders them:
+ * each call records an event on its stream after its launch, and a call on
+ * another stream first makes its stream wait for the previous call's event
+ * (an event created once per GPU, with the array's address lookup).  Calls
+ * from several threads are serialised by a lock.  A caller capturing a HIP
+ * graph should keep its no-alloc calls on the capturing stream: a switch of
+ * stream adds a wait on an event recorded outside the capture. */
 int air_paged_decode_noalloc(air_kv_pool *pool, void *stream, const void *q, int32_t q_dtype,
                              int32_t n_q_heads, const int32_t *block_tables, const int32_t *seq_lens,
                              int32_t batch, int32_t max_blocks, float scale, int32_t max_splits,

@@ -91,3 +91,45 @@ def test_noalloc_rejects_a_launch_above_the_array():
                                     0.088, 64, None, airkv.F32)
     assert rc == airkv.AIR_KV_E_INVALID_ARG
     assert "scratch" in airkv.last_error()
+
+
+def test_noalloc_calls_on_two_streams_are_ordered():
+    """Two no-alloc calls issued back to back on two streams share the GPU's
+    scratch array: the second waits for the first (an event the library
+    records after each call), so both outputs equal their workspace-path
+    results, bit for bit, the larger call first."""
+    torch = torch_mod()
+    L = _lib.load()
+    log("noalloc two streams")
+    cfg = workloads.Config("noalloc2", 32, 8, 128, 16, airkv.BF16, 48)
+    rng = np.random.default_rng(71)
+    lens = rng.integers(500, 4000, size=48).tolist()
+    w = workloads.build_prefill_decode(cfg, lens, seed=72, decode_steps=1)
+    k, v = next(workloads.kv_rows(w.n_rows, 8, 128, seed=73, chunk_rows=1 << 24))
+    pool = device_pool_for(w)
+    run_appends(w, k, v, pool, None)
+    tables, seq_lens = w.tables()
+    tt, lt = torch.from_numpy(tables).cuda(), torch.from_numpy(seq_lens).cuda()
+    small = 8
+    tt2, lt2 = tt[:small].contiguous(), lt[:small].contiguous()
+    q = torch.randn(cfg.batch, 32, 128, device="cuda").to(torch.bfloat16)
+    q2 = torch.randn(small, 32, 128, device="cuda").to(torch.bfloat16)
+    want1, _ = _decode_both(pool, q, tt, lt)
+    want2, _ = _decode_both(pool, q2, tt2, lt2)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    out1 = torch.full((cfg.batch, 32, 128), float("nan"), device="cuda")
+    out2 = torch.full((small, 32, 128), float("nan"), device="cuda")
+    torch.cuda.synchronize()
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(128)))
+    for _ in range(3):
+        _lib.check(L.air_paged_decode_noalloc(pool.handle, ctypes.c_void_p(s1.cuda_stream), _p(q), airkv.BF16, 32,
+                                              _p(tt), _p(lt), cfg.batch, tables.shape[1], scale, 64, _p(out1),
+                                              airkv.F32), "air_paged_decode_noalloc (s1)")
+        _lib.check(L.air_paged_decode_noalloc(pool.handle, ctypes.c_void_p(s2.cuda_stream), _p(q2), airkv.BF16,
+                                              32, _p(tt2), _p(lt2), small, tables.shape[1], scale, 64, _p(out2),
+                                              airkv.F32), "air_paged_decode_noalloc (s2)")
+        torch.cuda.synchronize()
+        assert np.array_equal(out1.cpu().numpy().view(np.uint32), want1.view(np.uint32))
+        assert np.array_equal(out2.cpu().numpy().view(np.uint32), want2.view(np.uint32))
+    assert pool.error_count() == 0
+
