@@ -144,6 +144,26 @@ def test_decode_append_quantized_pools(dtype, n_q, bs, q_f32):
     assert pa.error_count() == 0 and pb.error_count() == 0
 
 
+@pytest.mark.parametrize("dtype,group", [(airkv.INT8, 64), (airkv.FP8, 64), (airkv.INT8, 128), (airkv.FP8, 128)])
+def test_decode_append_quantized_scale_groups(dtype, group):
+    """1-byte pools whose scale groups span 64 or 128 elements (8 or 16 lanes
+    of the fused quantizer per group, one or two scales per row): pages,
+    scales and outputs bit-exact with air_kv_append + air_paged_decode and
+    the pages and scales with the oracle's append."""
+    log(f"decode_append quantized dtype={dtype} scale_group={group}")
+    ctx = [0, 15, 31, 200, 1500]
+    cfg = workloads.Config("decode_append_sg", 32, 8, 128, 16, dtype, len(ctx), scale_group=group)
+    w, pa, pb, host, tables, lens, k_new, v_new = _setup(cfg, ctx, seed=191 + group + dtype)
+    k_new, v_new = k_new.copy(), v_new.copy()
+    k_new[:, :, 70] *= 30.0                            # one outlier channel in the second half of the row
+    q = np.random.default_rng(192).standard_normal((cfg.batch, 32, 128)).astype(np.float32)
+    q, got = _run_pair(cfg, pa, pb, host, tables, lens, k_new, v_new, q, q_f32=False)
+    want = host.paged_decode(q, tables, lens, chunk=64)
+    err = rel_err(got, want)
+    log(f"  identical to append + decode; rel err vs oracle {err:.2e}")
+    assert err <= 2e-2
+
+
 @pytest.mark.parametrize("dtype", [airkv.INT8, airkv.FP8])
 def test_decode_append_quantized_long_sequences(dtype):
     """1-byte pools with two long sequences spread over many slices: the last
