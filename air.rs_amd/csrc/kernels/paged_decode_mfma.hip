@@ -364,10 +364,14 @@ constexpr int kernel_waves_per_simd(int dt, bool append) {
     return (append && dt == AIR_KV_FP8) ? 3 : waves_per_simd(dt);
 }
 
+// The build's waves per SIMD are its minimum and its maximum: with the
+// maximum the register allocator plans for that occupancy, not a higher one
+// the launch never uses (c4 fp8 355 against 362-364 us, same box, two runs
+// each; c2 104.1-104.4 against 104.7-105.0; c3 and c5 unchanged).
 // APPEND (bf16 pages): the launch also writes each sequence's new token,
 // a.k_new / a.v_new, as described at the fused append below.
 template <int D, int BS, bool QF32, int DT, bool APPEND>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kernel_waves_per_simd(DT, APPEND))))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kernel_waves_per_simd(DT, APPEND), kernel_waves_per_simd(DT, APPEND))))
 void decode_mfma_kernel(DecodeArgs a) {
     static_assert(D == 128, "lane mappings assume head_dim 128");
     constexpr bool QUANT = DT != AIR_KV_BF16;
