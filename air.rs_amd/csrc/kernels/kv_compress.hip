@@ -168,7 +168,10 @@ __global__ __launch_bounds__(kThreads) void key_compress_kernel(CompressArgs a) 
 // distinct 4-bank groups) and reads its own row back.  The folds then run in
 // the reference's order on the row kept in registers in its stored form
 // (f32, bf16 pairs or 1-byte codes, converted on each pass exactly as the
-// per-row loader converts them).
+// per-row loader converts them).  All passes' loads are issued before the
+// first staging (one memory round trip per 64 rows, not one per pass) and are
+// non-temporal: each byte is read once, and these loads measured 4-5% faster
+// than cached ones.
 constexpr int kStagePiece = 128;                     // row bytes staged per pass
 constexpr int kStagePitch = kStagePiece + 16;
 
@@ -198,16 +201,18 @@ __global__ __launch_bounds__(kThreads) void key_compress_staged_kernel(CompressA
         const bool live = row_elem(a.src, r0, D, e0);    // the 64 rows share one block
         const uint8_t *gbase = (const uint8_t *)a.src.base + e0 * EB;
         uint32_t raw[RB / 4];
+        u32x4 call[RB / PB][CPR];                        // chunk k = 64 i + lane: row k / CPR
+#pragma unroll
+        for (int p = 0; p < RB / PB; ++p)
+#pragma unroll
+            for (int i = 0; i < CPR; ++i) {
+                const int k = 64 * i + lane, row = k / CPR, ch = k % CPR;
+                const u32x4 *src = reinterpret_cast<const u32x4 *>(gbase + (int64_t)row * RB + p * PB + 16 * ch);
+                call[p][i] = live && r0 + row < a.n_rows ? __builtin_nontemporal_load(src) : u32x4{0u, 0u, 0u, 0u};
+            }
 #pragma unroll
         for (int p = 0; p < RB / PB; ++p) {
-            u32x4 c[CPR];
-#pragma unroll
-            for (int i = 0; i < CPR; ++i) {              // chunk k = 64 i + lane: row k / CPR
-                const int k = 64 * i + lane, row = k / CPR, ch = k % CPR;
-                c[i] = live && r0 + row < a.n_rows
-                           ? *reinterpret_cast<const u32x4 *>(gbase + (int64_t)row * RB + p * PB + 16 * ch)
-                           : u32x4{0u, 0u, 0u, 0u};
-            }
+            const u32x4 (&c)[CPR] = call[p];
 #pragma unroll
             for (int i = 0; i < CPR; ++i) {
                 const int k = 64 * i + lane, row = k / CPR, ch = k % CPR;
@@ -219,7 +224,7 @@ __global__ __launch_bounds__(kThreads) void key_compress_staged_kernel(CompressA
 #pragma unroll
                 for (int j = 0; j < 4; ++j) raw[(p * PB + 16 * ch) / 4 + j] = v[j];
             }
-            __builtin_amdgcn_sched_barrier(0);           // one pass's chunks live at a time
+            __builtin_amdgcn_sched_barrier(0);           // one pass's LDS writes and reads at a time
         }
         if (r >= a.n_rows) continue;
         if (!live && a.errors && (r % a.src.rows_per_block) == 0) atomicAdd(a.errors, 1ull);
