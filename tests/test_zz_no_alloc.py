@@ -133,3 +133,44 @@ def test_noalloc_calls_on_two_streams_are_ordered():
         assert np.array_equal(out2.cpu().numpy().view(np.uint32), want2.view(np.uint32))
     assert pool.error_count() == 0
 
+
+
+def test_noalloc_calls_allocate_no_device_memory():
+    """After two warm-up calls (code objects loaded, the scratch array's
+    address looked up, the ordering event created), further no-alloc calls of
+    both sizes leave the device's free memory (hipMemGetInfo, which sees
+    every allocation of the process, not only torch's) unchanged."""
+    torch = torch_mod()
+    L = _lib.load()
+    log("noalloc allocates nothing")
+    cfg = workloads.Config("noalloc3", 32, 8, 128, 16, airkv.BF16, 16)
+    rng = np.random.default_rng(81)
+    lens = rng.integers(200, 3000, size=16).tolist()
+    w = workloads.build_prefill_decode(cfg, lens, seed=82, decode_steps=1)
+    k, v = next(workloads.kv_rows(w.n_rows, 8, 128, seed=83, chunk_rows=1 << 24))
+    pool = device_pool_for(w)
+    run_appends(w, k, v, pool, None)
+    tables, seq_lens = w.tables()
+    tt, lt = torch.from_numpy(tables).cuda(), torch.from_numpy(seq_lens).cuda()
+    tt2, lt2 = tt[:4].contiguous(), lt[:4].contiguous()
+    q = torch.randn(cfg.batch, 32, 128, device="cuda").to(torch.bfloat16)
+    out = torch.empty((cfg.batch, 32, 128), device="cuda")
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(128)))
+
+    def call(n, t, sl):
+        _lib.check(L.air_paged_decode_noalloc(pool.handle, None, _p(q), airkv.BF16, 32, _p(t), _p(sl), n,
+                                              tables.shape[1], scale, 64, _p(out), airkv.F32),
+                   "air_paged_decode_noalloc")
+
+    call(cfg.batch, tt, lt)
+    call(4, tt2, lt2)
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    for _ in range(3):
+        call(cfg.batch, tt, lt)
+        call(4, tt2, lt2)
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    log(f"  free device memory before {free0} after {free1}")
+    assert free1 == free0
+    assert pool.error_count() == 0
