@@ -3,9 +3,12 @@
 // The reference's flash_decode (src/flash_decode.rs:153-173) splits one
 // head's contiguous KV into chunks, computes a normalised partial per chunk
 // (:70-109) and merges the partials by log-sum-exp (:114-142).  Here the KV
-// lives in pages: a workgroup owns one (partition, kv head, sequence) and all
-// `G` query heads that share the kv head (GQA, src/chunked_attn.rs:240-243),
-// so every K/V byte is read once for the whole group.  Within a partition the
+// lives in pages: a workgroup owns one (partition, kv head, sequence) and the
+// query heads that share the kv head (GQA, src/chunked_attn.rs:240-243), GC
+// of them at a time: groups of up to 8 heads take one workgroup per kv head
+// (GC the next power of two, heads past the group masked), so every K/V byte
+// is read once for the whole group; larger groups (multi-query attention)
+// take ceil(group / 8) workgroups of 8 heads each.  Within a partition the
 // workgroup runs an online softmax over 64-token tiles; the partial output is
 // left unnormalised together with its running max and sum (log2 domain), and
 // a second kernel merges the partitions of each (sequence, query head).
@@ -103,6 +106,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 template <int DT, int G, int D>
 __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
+    // G: heads per workgroup, the group's heads g0 .. g0 + gn - 1
     constexpr int LPR = D / 8;                  // lanes per token row
     constexpr int RPW = 64 / LPR;               // rows per wave per pass
     constexpr int RPP = RPW * kWaves;           // rows per workgroup pass
@@ -113,7 +117,11 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     __shared__ float s_m[G], s_l[G], s_alpha[G];
     __shared__ float s_red[(kWaves - 1) * G * D];
 
-    const int part = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+    const int chunks = (a.group + G - 1) / G;
+    const int part = blockIdx.x, kh = blockIdx.y / chunks, b = blockIdx.z;
+    const int g0 = (blockIdx.y % chunks) * G;
+    const int gn = a.group - g0 < G ? a.group - g0 : G;   // heads of the group in this workgroup
+    const int64_t head0 = (int64_t)kh * a.group + g0;       // its first query head
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t max_len = (int64_t)a.max_blocks * a.block_size;
     int64_t len = a.lens[b];
@@ -127,12 +135,16 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     const int ng = (DT == AIR_KV_INT8 || DT == AIR_KV_FP8) ? D / a.scale_group : 1;
     const int sg = (DT == AIR_KV_INT8 || DT == AIR_KV_FP8) ? a.scale_group : 1;
 
-    // this lane's 8 elements of each of the G query rows, as f32
+    // this lane's 8 elements of each of the G query rows, as f32 (zeros for
+    // rows past the group)
     float qr[G][8];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const int64_t qoff = ((int64_t)b * a.n_q_heads + kh * G + g) * D + chunk * 8;
-        if (a.q_dtype == AIR_KV_F32) {
+        const int64_t qoff = ((int64_t)b * a.n_q_heads + head0 + g) * D + chunk * 8;
+        if (g >= gn) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qr[g][j] = 0.0f;
+        } else if (a.q_dtype == AIR_KV_F32) {
             const float4 *qp = reinterpret_cast<const float4 *>((const float *)a.q + qoff);
             float4 x0 = qp[0], x1 = qp[1];
             qr[g][0] = x0.x; qr[g][1] = x0.y; qr[g][2] = x0.z; qr[g][3] = x0.w;
@@ -255,7 +267,8 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     if (wave == 0 && lane < LPR) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const int64_t slot = ((int64_t)b * a.n_q_heads + kh * G + g) * a.num_parts + part;
+            if (g >= gn) break;
+            const int64_t slot = ((int64_t)b * a.n_q_heads + head0 + g) * a.num_parts + part;
             float o[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -306,7 +319,8 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(DecodeArgs a) {
 
 template <int DT, int G, int D>
 hipError_t launch_typed(const DecodeArgs &a, hipStream_t s, int n_kv_heads) {
-    dim3 grid((unsigned)a.num_parts, (unsigned)n_kv_heads, (unsigned)a.batch);
+    const int chunks = (a.group + G - 1) / G;
+    dim3 grid((unsigned)a.num_parts, (unsigned)(n_kv_heads * chunks), (unsigned)a.batch);
     hipLaunchKernelGGL((decode_split_kernel<DT, G, D>), grid, dim3(kThreads), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -324,14 +338,13 @@ hipError_t launch_d(const DecodeArgs &a, hipStream_t s, int n_kv_heads, int d) {
     }
 }
 
+// Heads per workgroup: the group rounded up to a power of two, at most 8.
 template <int DT>
 hipError_t launch_g(const DecodeArgs &a, hipStream_t s, int n_kv_heads, int d, int g) {
-    switch (g) {
-    case 1: return launch_d<DT, 1>(a, s, n_kv_heads, d);
-    case 2: return launch_d<DT, 2>(a, s, n_kv_heads, d);
-    case 4: return launch_d<DT, 4>(a, s, n_kv_heads, d);
-    default: return launch_d<DT, 8>(a, s, n_kv_heads, d);
-    }
+    if (g == 1) return launch_d<DT, 1>(a, s, n_kv_heads, d);
+    if (g == 2) return launch_d<DT, 2>(a, s, n_kv_heads, d);
+    if (g <= 4) return launch_d<DT, 4>(a, s, n_kv_heads, d);
+    return launch_d<DT, 8>(a, s, n_kv_heads, d);
 }
 
 }  // namespace
@@ -343,8 +356,6 @@ int plan_decode(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int32_t 
         return fail(AIR_KV_E_INVALID_ARG, "n_q_heads %d is not a multiple of n_kv_heads %d", n_q_heads, nkv);
     const int g = n_q_heads / nkv;
     if (!decode_mfma_supported(p.desc.dtype, d, bs, g, p.desc.scale_group)) {
-        if (g != 1 && g != 2 && g != 4 && g != 8)
-            return fail(AIR_KV_E_INVALID_ARG, "GQA group %d unsupported for this pool (1, 2, 4 or 8)", g);
         if (d != 64 && d != 128 && d != 256)
             return fail(AIR_KV_E_INVALID_ARG, "decode supports head_dim 64, 128 or 256 (pool has %d)", d);
     }

@@ -259,8 +259,11 @@ int air_paged_decode_workspace_size(const air_kv_pool *pool, int32_t n_q_heads, 
  * batch's cached tokens into equal slices per kv head (one wave each, at most
  * batch * max_splits), where a slice may end inside a sequence and hold
  * several, widened when the longest sequence would otherwise meet more than
- * max_splits of them (max_splits 1: one slice per kv head); other pools cut
- * each sequence into at most max_splits fixed partitions.  Out-of-pool table
+ * max_splits of them (max_splits 1: one slice per kv head); other pools
+ * (F32 pages, head_dim 64 or 256, groups above 16) cut each sequence into at
+ * most max_splits fixed partitions, each workgroup serving up to 8 query
+ * heads of a kv head (any group: the reference's head map takes any
+ * n_q_heads / n_kv_heads, src/chunked_attn.rs:65-72).  Out-of-pool table
  * entries are skipped and counted (air_kv_pool_error_count); seq_lens outside
  * [0, max_blocks * block_size] are clamped and counted.  A sequence of length
  * 0 produces zeros.  The workspace is device

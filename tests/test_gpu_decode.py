@@ -49,13 +49,31 @@ def _decode_case(cfg, lens, seed, q_bf16=True, max_splits=64, outliers=None, out
 
 
 @pytest.mark.parametrize("dtype", [airkv.F32, airkv.BF16, airkv.INT8, airkv.FP8])
-@pytest.mark.parametrize("group", [1, 4, 8])
+@pytest.mark.parametrize("group", [1, 4, 6, 8, 16])
 def test_decode_matches_oracle_small(dtype, group):
+    """Groups of 1 .. 16 query heads per kv head (the matrix-core path takes
+    any group up to 16; lanes of heads past the group read zeros), including
+    one that is not a power of two."""
     log(f"decode small dtype={dtype} group={group}")
-    nkv = 2 if group == 8 else 4
+    nkv = 2 if group >= 8 else 4
     cfg = workloads.Config("small", nkv * group, nkv, 128, 16, dtype, 5)
     lens = [1, 17, 64, 300, 777]
     got, want, _ = _decode_case(cfg, lens, seed=30 + group)
+    err = rel_err(got, want)
+    log(f"  rel err {err:.2e}")
+    assert err <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype,n_kv,group", [(airkv.F32, 2, 12), (airkv.BF16, 1, 32), (airkv.INT8, 2, 20),
+                                              (airkv.FP8, 1, 24)])
+def test_decode_groups_above_16(dtype, n_kv, group):
+    """Query heads per kv head beyond the matrix-core kernel's 16 (multi-query
+    attention: one kv head for all heads; the reference takes any ratio,
+    src/chunked_attn.rs:65-72): the split kernel serves the group eight heads
+    per workgroup, the last workgroup's heads past the group masked."""
+    log(f"decode group {group} dtype={dtype}")
+    cfg = workloads.Config("mqa", n_kv * group, n_kv, 128, 16, dtype, 4)
+    got, want, _ = _decode_case(cfg, [5, 64, 333, 900], seed=90 + group)
     err = rel_err(got, want)
     log(f"  rel err {err:.2e}")
     assert err <= TOL[dtype]

@@ -55,18 +55,31 @@ def _prefill_case(cfg, ctx_lens, q_lens, seed, q_bf16=True, out_bf16=False, max_
 
 
 @pytest.mark.parametrize("dtype", [airkv.BF16, airkv.INT8, airkv.FP8])
-@pytest.mark.parametrize("group", [1, 2, 4, 8])
+@pytest.mark.parametrize("group", [1, 2, 4, 6, 8, 16])
 def test_prefill_matches_oracle_small(dtype, group):
     """Chunks of 1, 31, 32, 33 and 100 rows over prefixes of 0 .. 300 tokens
-    (a whole-sequence prefill, partial token blocks, a single row)."""
+    (a whole-sequence prefill, partial token blocks, a single row), for GQA
+    groups of 1 .. 16 query heads per kv head (6: work items of a token
+    block that do not fill whole workgroups)."""
     log(f"prefill small dtype={dtype} group={group}")
-    nkv = 1 if group == 8 else 2
+    nkv = 1 if group >= 8 else 2
     cfg = workloads.Config("small", nkv * group, nkv, 128, 16, dtype, 5)
     q_lens = [1, 31, 32, 33, 100]
     ctx = [1, 31 + 17, 32 + 300, 33, 100 + 45]
     got, want = _prefill_case(cfg, ctx, q_lens, seed=60 + group)
     err = rel_err(got, want)
     log(f"  rel err {err:.2e}")
+    assert err <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [airkv.BF16, airkv.INT8])
+def test_prefill_multi_query(dtype):
+    """One kv head for 32 query heads (multi-query attention; the reference
+    takes any ratio, src/chunked_attn.rs:65-72)."""
+    cfg = workloads.Config("mqa", 32, 1, 128, 16, dtype, 3)
+    got, want = _prefill_case(cfg, [40, 200, 530], [40, 64, 130], seed=95)
+    err = rel_err(got, want)
+    log(f"prefill multi-query dtype={dtype}: rel err {err:.2e}")
     assert err <= TOL[dtype]
 
 
