@@ -20,7 +20,7 @@ struct DecodeArgs {
     int32_t slices, slots;           // balanced slices (matrix-core kernel)
     int32_t max_splits;              // pieces per sequence at most (matrix-core kernel)
     float scale_log2;              // softmax scale * log2(e): exp(x*s) == exp2(x*scale_log2)
-    int32_t n_kv_heads, block_size, scale_group, group;
+    int32_t n_kv_heads, block_size, scale_group, group, head_dim;
     int64_t num_blocks;
     const void *k_pages, *v_pages;
     const float *k_scales, *v_scales;
@@ -36,6 +36,11 @@ struct DecodeArgs {
     // [batch][n_kv_heads][head_dim] f32, written as each sequence's token
     // seq_lens[b] - 1 by the wave that computes that token's tile (NULL: none)
     const float *k_new, *v_new;
+    // Vector kernel as a prefill (NULL: decode): sequence b's query rows
+    // cu_q[b] .. cu_q[b + 1] - 1 of total_q, each attending causally,
+    // num_parts row slots per sequence
+    const int32_t *cu_q;
+    int32_t total_q;
 };
 
 bool decode_mfma_supported(int dtype, int head_dim, int block_size, int group, int scale_group);

@@ -212,8 +212,9 @@ int air_paged_prefill_workspace_size(const air_kv_pool *p, int32_t n_q_heads, in
         return fail(AIR_KV_E_INVALID_ARG, "n_q_heads %d is not a multiple of n_kv_heads %d", n_q_heads,
                     p->desc.n_kv_heads);
     if (batch < 0 || max_q_len < 0) return fail(AIR_KV_E_INVALID_ARG, "negative batch or max_q_len");
-    if (batch == 0) {
-        *bytes = 0;
+    const air_kv_pool_desc &d = p->desc;
+    if (batch == 0 || !airkv::prefill_supported(d.dtype, d.head_dim, d.block_size, d.scale_group)) {
+        *bytes = 0;             // the vector prefill splits nothing
         return AIR_KV_OK;
     }
     const airkv::PrefillPlan pl =
@@ -229,10 +230,6 @@ int air_paged_prefill(air_kv_pool *p, void *stream, const void *q, int32_t q_dty
                       int32_t out_dtype) {
     if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
     const air_kv_pool_desc &d = p->desc;
-    if (!airkv::prefill_supported(d.dtype, d.head_dim, d.block_size, d.scale_group))
-        return fail(AIR_KV_E_INVALID_ARG,
-                    "paged prefill needs a BF16, INT8 or FP8 pool with head_dim 128 (pool dtype %d, head_dim %d)",
-                    d.dtype, d.head_dim);
     if (n_q_heads <= 0 || n_q_heads % d.n_kv_heads)
         return fail(AIR_KV_E_INVALID_ARG, "n_q_heads %d is not a multiple of n_kv_heads %d", n_q_heads,
                     d.n_kv_heads);
@@ -249,6 +246,15 @@ int air_paged_prefill(air_kv_pool *p, void *stream, const void *q, int32_t q_dty
         return fail(AIR_KV_E_INVALID_ARG, "prefill scale must be finite and > 0");
     if ((int64_t)max_blocks * d.block_size > INT32_MAX)
         return fail(AIR_KV_E_INVALID_ARG, "max_blocks * block_size exceeds int32");
+    if (!airkv::prefill_supported(d.dtype, d.head_dim, d.block_size, d.scale_group)) {
+        // F32 pages, head_dim other than 128, small scale groups: the
+        // vector kernel, one query row per workgroup and head chunk
+        if (batch > 65535) return fail(AIR_KV_E_INVALID_ARG, "batch %d above 65535 for this pool", batch);
+        hipError_t e = airkv::launch_prefill_rows(*p, (hipStream_t)stream, q, q_dtype, n_q_heads, cu_q, total_q,
+                                                  max_q_len, block_tables, seq_lens, batch, max_blocks, scale,
+                                                  out, out_dtype);
+        return e == hipSuccess ? AIR_KV_OK : hip_fail(e, "air_paged_prefill launch");
+    }
     airkv::PrefillArgs a;
     a.q = q; a.q_dtype = q_dtype; a.n_q_heads = n_q_heads;
     a.cu_q = cu_q; a.tables = block_tables; a.lens = seq_lens;

@@ -62,6 +62,12 @@ hipError_t launch_decode(const air_kv_pool &pool, hipStream_t s, const DecodePla
                          const int32_t *lens, int32_t batch, int32_t max_blocks, float scale,
                          void *workspace, void *out, int32_t out_dtype,
                          const float *k_new = nullptr, const float *v_new = nullptr);
+// Paged prefill on the vector decode kernel, for pools the matrix-core
+// prefill does not take (arguments as air_paged_prefill's, validated).
+hipError_t launch_prefill_rows(const air_kv_pool &pool, hipStream_t s, const void *q, int32_t q_dtype,
+                               int32_t n_q_heads, const int32_t *cu_q, int32_t total_q, int32_t max_q_len,
+                               const int32_t *tables, const int32_t *lens, int32_t batch, int32_t max_blocks,
+                               float scale, void *out, int32_t out_dtype);
 hipError_t launch_copy_blocks(const air_kv_pool &pool, hipStream_t s, const int32_t *src,
                               const int32_t *dst, int32_t n);
 hipError_t launch_stage_blocks(const air_kv_pool &pool, hipStream_t s, const int32_t *ids, int32_t n,

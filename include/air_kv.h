@@ -333,9 +333,11 @@ int air_paged_decode_noalloc(air_kv_pool *pool, void *stream, const void *q, int
  * out_dtype (AIR_KV_F32 or AIR_KV_BF16); cu_q: int32 [batch + 1] (device).
  * max_q_len sizes the launch (an upper bound of the q_len values; a larger
  * q_len is still computed in full).  scale must be finite and > 0 (the
- * reference's is 1/sqrt(head_dim)).  Supports BF16, INT8 and FP8 pools with
- * head_dim 128 (quantized pages are dequantized q * scale in registers); other
- * pools return AIR_KV_E_INVALID_ARG.  BF16 pools run the probability x value
+ * reference's is 1/sqrt(head_dim)).  BF16, INT8 and FP8 pools with head_dim
+ * 128 take the matrix-core kernel (quantized pages are dequantized q * scale
+ * in registers); every other pool (F32 pages, other head dims) runs each
+ * query row on air_paged_decode's split kernel over its causal keys, with f32
+ * products, no workspace and the same error handling.  BF16 pools run the probability x value
  * products with f16 operands (11 significant bits each), INT8 / FP8 pools the
  * key x query products as well (keys, values and F32 queries rounded to f16
  * once); a work group whose result that way is not finite, or whose outputs

@@ -79,6 +79,19 @@ def test_decode_groups_above_16(dtype, n_kv, group):
     assert err <= TOL[dtype]
 
 
+@pytest.mark.parametrize("dtype,head_dim,group", [(airkv.F32, 96, 4), (airkv.BF16, 160, 2), (airkv.INT8, 32, 8),
+                                                  (airkv.FP8, 224, 3), (airkv.BF16, 192, 16)])
+def test_decode_other_head_dims(dtype, head_dim, group):
+    """head_dim a multiple of 32 that is not 64, 128 or 256 (the pool takes any
+    up to 256): the split kernel's lanes past head_dim idle."""
+    log(f"decode head_dim {head_dim} dtype={dtype} group={group}")
+    cfg = workloads.Config("hd", 2 * group, 2, head_dim, 16, dtype, 4)
+    got, want, _ = _decode_case(cfg, [3, 70, 257, 640], seed=110 + head_dim)
+    err = rel_err(got, want)
+    log(f"  rel err {err:.2e}")
+    assert err <= TOL[dtype]
+
+
 def test_c2_shape_bf16_scaled():
     """configs[1] geometry (32 q / 8 kv, d 128, bs 16) at batch 8 and
     contexts U[512, 1500], q in bf16."""

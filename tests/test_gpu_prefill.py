@@ -72,6 +72,58 @@ def test_prefill_matches_oracle_small(dtype, group):
     assert err <= TOL[dtype]
 
 
+@pytest.mark.parametrize("dtype,head_dim,n_kv,group,bs", [
+    (airkv.F32, 128, 2, 4, 16), (airkv.F32, 64, 2, 2, 32), (airkv.F32, 96, 1, 6, 16),
+    (airkv.BF16, 64, 2, 4, 16), (airkv.BF16, 96, 2, 2, 32), (airkv.BF16, 256, 1, 8, 16),
+    (airkv.INT8, 160, 2, 2, 16), (airkv.FP8, 32, 4, 1, 32), (airkv.INT8, 224, 1, 12, 16)])
+def test_prefill_vector_path_vs_oracle(dtype, head_dim, n_kv, group, bs):
+    """Pools the matrix-core prefill does not take -- f32 pages (the
+    reference's own cache dtype) and head_dim other than 128 -- run each
+    query row on the split kernel over its causal keys: the oracle's
+    blockwise attention, within the same tolerance."""
+    cfg = workloads.Config("vec", n_kv * group, n_kv, head_dim, bs, dtype, 4)
+    got, want = _prefill_case(cfg, [1, 37, 300, 700], [1, 37, 64, 100], seed=97 + head_dim)
+    err = rel_err(got, want)
+    log(f"prefill vector path dtype={dtype} d={head_dim} group={group}: rel err {err:.2e}")
+    assert err <= TOL.get(dtype, 1e-3)
+
+
+def test_prefill_vector_path_invalid_sequences():
+    """The vector prefill keeps the matrix-core prefill's error handling: a
+    chunk longer than its sequence and a seq_len beyond the table are each
+    counted once with their rows zero-filled, the valid sequence matches the
+    oracle, and an out-of-pool table entry inside a sequence is counted once."""
+    torch = torch_mod()
+    cfg = workloads.Config("badvec", 8, 2, 128, 16, airkv.F32, 3)
+    pool, host, tables, lens = _setup(cfg, [40, 50, 60], seed=79)
+    q_lens = [10, 60, 5]
+    lens_bad = lens.copy()
+    lens_bad[2] = tables.shape[1] * 16 + 1
+    cu = np.zeros(4, np.int32)
+    cu[1:] = np.cumsum(q_lens)
+    q = torch.randn((int(cu[-1]), 8, 128), device="cuda")
+    out = torch.full((int(cu[-1]), 8, 128), 7.0, device="cuda")
+    pool.error_count(reset=True)
+    pool.paged_prefill(q, torch.from_numpy(cu).cuda(), torch.from_numpy(tables).cuda(),
+                       torch.from_numpy(lens_bad).cuda(), out)
+    torch.cuda.synchronize()
+    assert pool.error_count(reset=True) == 2
+    got = out.cpu().numpy()
+    assert np.all(got[10:] == 0.0)
+    want = host.paged_prefill(q.cpu().numpy()[:10], cu[:2], tables[:1], lens[:1])
+    assert rel_err(got[:10], want) <= 1e-3
+    t2 = tables.copy()
+    t2[0, 1] = 1 << 30
+    cu1 = np.array([0, 10], np.int32)
+    out1 = torch.zeros((10, 8, 128), device="cuda")
+    pool.paged_prefill(q[:10].contiguous(), torch.from_numpy(cu1).cuda(), torch.from_numpy(t2[:1]).cuda(),
+                       torch.from_numpy(lens[:1]).cuda(), out1)
+    torch.cuda.synchronize()
+    assert pool.error_count(reset=True) == 1
+    assert torch.isfinite(out1).all()
+    assert pool.prefill_workspace_size(8, 3, 60) == 0
+
+
 @pytest.mark.parametrize("dtype", [airkv.BF16, airkv.INT8])
 def test_prefill_multi_query(dtype):
     """One kv head for 32 query heads (multi-query attention; the reference
@@ -388,20 +440,13 @@ def test_prefill_key_split_rows_past_total_q_write_nothing():
     assert bool((big == 7.0).all())                      # rows inside and past `out` untouched
 
 
-def test_prefill_rejects_unsupported_pools_and_args():
+def test_prefill_rejects_bad_args():
     torch = torch_mod()
     L = airkv.load()
-    p32 = airkv.KvPool(8, 16, 2, 128, airkv.F32)
     q = torch.zeros((4, 8, 128), device="cuda")
     cu = torch.tensor([0, 4], dtype=torch.int32, device="cuda")
     tb = torch.zeros((1, 1), dtype=torch.int32, device="cuda")
     ln = torch.tensor([4], dtype=torch.int32, device="cuda")
-    with pytest.raises(airkv.AirKvError):
-        p32.paged_prefill(q, cu, tb, ln, torch.empty_like(q))
-    pb = airkv.KvPool(8, 16, 2, 64, airkv.BF16)
-    with pytest.raises(airkv.AirKvError):
-        pb.paged_prefill(torch.zeros((4, 8, 64), device="cuda"), cu, tb, ln,
-                         torch.zeros((4, 8, 64), device="cuda"))
     pb = airkv.KvPool(8, 16, 2, 128, airkv.BF16)
     rc = L.air_paged_prefill(pb.handle, None, ctypes.c_void_p(q.data_ptr()), airkv.F32, 7,
                              ctypes.c_void_p(cu.data_ptr()), 4, 4, ctypes.c_void_p(tb.data_ptr()),
