@@ -192,10 +192,11 @@ class KvPool:
 
     def paged_decode_append(self, q, k_new, v_new, block_tables, seq_lens, out, scale=None,
                             max_splits=64, workspace=None, stream=None):
-        """One decode step in one launch: append k_new / v_new (float32
-        [batch, n_kv_heads, head_dim]) as each sequence's token seq_lens[b] - 1,
-        then attend as paged_decode (pools on the matrix-core decode: head_dim 128,
-        BF16, or INT8 / FP8 quantized as append quantizes)."""
+        """One decode step: append k_new / v_new (float32 [batch, n_kv_heads,
+        head_dim]) as each sequence's token seq_lens[b] - 1, then attend as
+        paged_decode.  One launch on pools of the matrix-core decode (head_dim
+        128, BF16, or INT8 / FP8 quantized as append quantizes); every other
+        pool appends, then decodes, with the same result."""
         head, tail = self._decode_args(q, block_tables, seq_lens, out, scale, max_splits, workspace, stream)
         rows = self._new_rows(q, k_new, v_new)
         _lib.check(_lib.load().air_paged_decode_append(*head, *rows, *tail), "air_paged_decode_append")

@@ -412,6 +412,22 @@ hipError_t launch_d(const DecodeArgs &a, hipStream_t s, int n_kv_heads, int d) {
     return launch_typed<DT, G, 256>(a, s, n_kv_heads);
 }
 
+// The decode step's append slot of each sequence on the vector path: token
+// seq_lens[b] - 1 through its block table, or -1 (nothing appended) for an
+// empty sequence, one longer than its table or a last block outside the
+// pool -- the cases the decode itself counts.
+__global__ __launch_bounds__(256) void step_slots_kernel(DecodeArgs a, int64_t *slots) {
+    const int b = blockIdx.x * 256 + threadIdx.x;
+    if (b >= a.batch) return;
+    const int64_t len = a.lens[b], max_len = (int64_t)a.max_blocks * a.block_size;
+    int64_t slot = -1;
+    if (len > 0 && len <= max_len) {
+        const int32_t blk = a.tables[(int64_t)b * a.max_blocks + (len - 1) / a.block_size];
+        if (blk >= 0 && blk < a.num_blocks) slot = (int64_t)blk * a.block_size + (len - 1) % a.block_size;
+    }
+    slots[b] = slot;
+}
+
 // Heads per workgroup: the group rounded up to a power of two, at most 8.
 template <int DT>
 hipError_t launch_g(const DecodeArgs &a, hipStream_t s, int n_kv_heads, int d, int g) {
@@ -422,6 +438,11 @@ hipError_t launch_g(const DecodeArgs &a, hipStream_t s, int n_kv_heads, int d, i
 }
 
 }  // namespace
+
+// Byte offset of the vector path's append slots in its workspace.
+static size_t step_slots_offset(int64_t batch, int64_t n_q_heads, int64_t parts, int64_t d) {
+    return ((size_t)(batch * n_q_heads * parts * (d + 2)) * sizeof(float) + 255) & ~(size_t)255;
+}
 
 int plan_decode(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int32_t max_blocks,
                 int32_t max_splits, DecodePlan *plan) {
@@ -453,7 +474,8 @@ int plan_decode(const air_kv_pool &p, int32_t n_q_heads, int32_t batch, int32_t 
     parts = (max_ctx + part_tokens - 1) / part_tokens;
     plan->part_tokens = (int32_t)part_tokens;
     plan->num_parts = (int32_t)parts;
-    plan->ws_bytes = (size_t)batch * n_q_heads * (size_t)parts * (size_t)(d + 2) * sizeof(float);
+    // partial outputs and (max, sum), then the decode step's append slots
+    plan->ws_bytes = step_slots_offset(batch, n_q_heads, parts, d) + (size_t)batch * sizeof(int64_t);
     return AIR_KV_OK;
 }
 
@@ -463,7 +485,7 @@ hipError_t launch_decode(const air_kv_pool &p, hipStream_t s, const DecodePlan &
                          void *workspace, void *out, int32_t out_dtype, const float *k_new,
                          const float *v_new) {
     DecodeArgs a;
-    a.k_new = plan.mfma ? k_new : nullptr;   // the vector kernels take no new rows
+    a.k_new = plan.mfma ? k_new : nullptr;   // the vector path appends them before its kernels
     a.v_new = plan.mfma ? v_new : nullptr;
     a.q = q; a.q_dtype = q_dtype; a.n_q_heads = n_q_heads;
     a.tables = tables; a.lens = lens;
@@ -485,6 +507,17 @@ hipError_t launch_decode(const air_kv_pool &p, hipStream_t s, const DecodePlan &
     const size_t n_slots = (size_t)batch * n_q_heads * plan.num_parts;
     a.part_o = (float *)workspace;
     a.part_ml = a.part_o + n_slots * p.desc.head_dim;
+    if (k_new && batch > 0) {
+        // the decode step on the vector path: each sequence's new row
+        // appended by air_kv_append's kernel at the slot its table gives
+        // token seq_lens[b] - 1, then the decode
+        int64_t *slots = (int64_t *)((char *)workspace +
+                                     step_slots_offset(batch, n_q_heads, plan.num_parts, p.desc.head_dim));
+        hipLaunchKernelGGL(step_slots_kernel, dim3((unsigned)((batch + 255) / 256)), dim3(256), 0, s, a, slots);
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess) e = launch_append(p, s, k_new, v_new, slots, batch);
+        if (e != hipSuccess) return e;
+    }
     const int d = p.desc.head_dim, g = plan.group, nkv = p.desc.n_kv_heads;
     switch (p.desc.dtype) {
     case AIR_KV_F32: return launch_g<AIR_KV_F32>(a, s, nkv, d, g);

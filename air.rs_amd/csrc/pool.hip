@@ -182,11 +182,6 @@ int air_paged_decode_append(air_kv_pool *p, void *stream, const void *q, int32_t
     if (!p) return fail(AIR_KV_E_INVALID_ARG, "pool is NULL");
     airkv::DecodePlan plan;
     if (int rc = airkv::plan_decode(*p, n_q_heads, batch, max_blocks, max_splits, &plan)) return rc;
-    if (!plan.mfma)
-        return fail(AIR_KV_E_INVALID_ARG,
-                    "fused append + decode needs a pool on the matrix-core decode (head_dim 128, block_size "
-                    "16 or 32, group 1..16; BF16, or INT8 / FP8 with scale_group >= 32); use air_kv_append, "
-                    "then air_paged_decode");
     if (batch == 0) return AIR_KV_OK;
     if (!q || !k_new || !v_new || !block_tables || !seq_lens || !out || !workspace)
         return fail(AIR_KV_E_INVALID_ARG, "NULL decode buffer");

@@ -284,12 +284,14 @@ int air_paged_decode(air_kv_pool *pool, void *stream, const void *q, int32_t q_d
  * the wave that attends over it, so no launch orders the two.  Sequences of
  * length 0 append nothing; a sequence longer than its table, or whose last
  * block is outside the pool, appends nothing and is counted as by
- * air_paged_decode.  Pools on the matrix-core decode only (head_dim 128,
- * block_size 16 or 32, group 1..16; BF16, or INT8 / FP8 with scale_group >=
- * 32, whose new rows are quantized exactly as air_kv_append quantizes them:
- * the same codes and group scales); other pools return AIR_KV_E_INVALID_ARG
- * (use air_kv_append, then air_paged_decode).  k_new and v_new are 16-byte aligned device
- * pointers.  The workspace is air_paged_decode's. */
+ * air_paged_decode.  On the matrix-core decode (head_dim 128, block_size 16
+ * or 32, group 1..16; BF16, or INT8 / FP8 with scale_group >= 32, whose new
+ * rows are quantized exactly as air_kv_append quantizes them: the same codes
+ * and group scales) this is one launch; every other pool takes the same
+ * call as three launches on the stream (each sequence's slot from its
+ * table, air_kv_append's kernel, then the decode), with the same pages and
+ * outputs.  k_new and v_new are 16-byte aligned device pointers.  The
+ * workspace is air_paged_decode's. */
 int air_paged_decode_append(air_kv_pool *pool, void *stream, const void *q, int32_t q_dtype,
                             int32_t n_q_heads, const float *k_new, const float *v_new,
                             const int32_t *block_tables, const int32_t *seq_lens, int32_t batch,

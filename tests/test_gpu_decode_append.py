@@ -9,14 +9,13 @@ that takes two launches, GQA groups 1, 2, 4, 8 and 16, bf16 and f32 queries, pag
 16 and 32, a sequence of length 0, a last block outside the pool, a sequence
 longer than its table, repeated calls, int8 (Q8_0) and fp8 pools (the new
 rows quantized in the launch: codes and scales bit-exact with air_kv_append
-and with the oracle), and the pools the fused path rejects."""
-import ctypes
-
+and with the oracle), and pools off the matrix-core decode (f32 pages, other
+head dims, small scale groups, groups above 16: append, then decode)."""
 import numpy as np
 import pytest
 
 import airkv
-from airkv import _lib, workloads
+from airkv import workloads
 from gpu_helpers import (assert_bits_equal, assert_floats_bit_equal, device_pool_for, host_pool_for, log,
                          rel_err, torch_mod)
 
@@ -208,12 +207,14 @@ def test_decode_append_batch_above_one_launch():
     log("  identical to append + decode")
 
 
-def test_decode_append_skips_invalid_sequences():
+@pytest.mark.parametrize("dtype", [airkv.BF16, airkv.F32])
+def test_decode_append_skips_invalid_sequences(dtype):
     """Length 0, a last block outside the pool and a sequence longer than its
-    table append nothing, as the reference path appends nothing for them."""
-    log("decode_append invalid sequences")
+    table append nothing, as the reference path appends nothing for them (the
+    matrix-core step on bf16 pages, the vector path's slots on f32 pages)."""
+    log(f"decode_append invalid sequences dtype={dtype}")
     ctx = [50, 63, 200, 17, 90]
-    cfg = workloads.Config("decode_append_bad", 32, 8, 128, 16, airkv.BF16, len(ctx))
+    cfg = workloads.Config("decode_append_bad", 32, 8, 128, 16, dtype, len(ctx))
     w, pa, pb, host, tables, lens, k_new, v_new = _setup(cfg, ctx, seed=91)
     lens = lens.copy()
     tables = tables.copy()
@@ -253,25 +254,23 @@ def test_decode_append_repeat_is_stable():
 
 
 @pytest.mark.parametrize("dtype,n_q,head_dim,bs,group", [(airkv.INT8, 32, 64, 16, 32), (airkv.FP8, 32, 128, 16, 16),
-                                                          (airkv.BF16, 32, 64, 16, 32), (airkv.F32, 32, 128, 16, 32)])
-def test_decode_append_rejects_other_pools(dtype, n_q, head_dim, bs, group):
-    """Pools off the matrix-core decode -- f32 pages, head_dim 64, 1-byte
-    pages with scale groups of 16 -- decode on the two-call path: the fused
-    entry returns AIR_KV_E_INVALID_ARG before any device work."""
-    torch = torch_mod()
-    pool = airkv.KvPool(64, bs, 8, head_dim, dtype, group)
-    q = torch.zeros((2, n_q, head_dim), device="cuda")
-    kn = torch.zeros((2, 8, head_dim), device="cuda")
-    t = torch.zeros((2, 4), dtype=torch.int32, device="cuda")
-    sl = torch.full((2,), 3, dtype=torch.int32, device="cuda")
-    out = torch.empty_like(q)
-    with pytest.raises(_lib.AirKvError, match="fused append"):
-        pool.paged_decode_append(q, kn, kn, t, sl, out)
-    L = _lib.load()
-    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
-    rc = L.air_paged_decode_append(pool.handle, None, ctypes.c_void_p(q.data_ptr()), airkv.F32, n_q,
-                                   ctypes.c_void_p(kn.data_ptr()), ctypes.c_void_p(kn.data_ptr()),
-                                   ctypes.c_void_p(t.data_ptr()), ctypes.c_void_p(sl.data_ptr()), 2, 4,
-                                   ctypes.c_float(0.1), 64, ctypes.c_void_p(ws.data_ptr()), 1 << 20,
-                                   ctypes.c_void_p(out.data_ptr()), airkv.F32)
-    assert rc == _lib.AIR_KV_E_INVALID_ARG
+                                                          (airkv.BF16, 32, 64, 16, 32), (airkv.F32, 32, 128, 16, 32),
+                                                          (airkv.BF16, 192, 128, 32, 32), (airkv.F32, 16, 96, 32, 32)])
+def test_decode_append_vector_path_pools(dtype, n_q, head_dim, bs, group):
+    """Pools off the matrix-core decode -- f32 pages, head_dim 64 or 96, 1-byte
+    pages with scale groups of 16, 24 query heads per kv head -- take the
+    same entry point: each sequence's slot from its table, the rows appended
+    by air_kv_append's kernel, then the split decode.  Pages, scales and
+    outputs equal air_kv_append + air_paged_decode bit for bit, the pages and
+    scales the oracle's append."""
+    log(f"decode_append vector path dtype={dtype} n_q={n_q} d={head_dim} bs={bs} scale_group={group}")
+    ctx = [0, 15, 31, 200, 1500]
+    cfg = workloads.Config("decode_append_vec", n_q, 8, head_dim, bs, dtype, len(ctx), scale_group=group)
+    w, pa, pb, host, tables, lens, k_new, v_new = _setup(cfg, ctx, seed=201 + dtype + head_dim)
+    q = np.random.default_rng(202).standard_normal((cfg.batch, n_q, head_dim)).astype(np.float32)
+    q, got = _run_pair(cfg, pa, pb, host, tables, lens, k_new, v_new, q, q_f32=True)
+    want = host.paged_decode(q, tables, lens, chunk=64)
+    err = rel_err(got, want)
+    log(f"  identical to append + decode; rel err vs oracle {err:.2e}")
+    assert err <= (1e-3 if dtype in (airkv.F32, airkv.BF16) else 2e-2)
+    assert pa.error_count() == 0 and pb.error_count() == 0
