@@ -103,6 +103,36 @@ def test_c1_append_gather_bitexact(dtype):
             assert_bits_equal(gk[offs[b]:offs[b] + n], oracle.q8_dequantize(q, s), "Q8Tensor pin")
 
 
+@pytest.mark.parametrize("dtype,head_dim,bs,scale_group", [
+    (airkv.F32, 96, 16, 32), (airkv.BF16, 160, 32, 32), (airkv.INT8, 224, 16, 32), (airkv.FP8, 32, 32, 32),
+    (airkv.BF16, 256, 16, 32), (airkv.INT8, 96, 32, 16), (airkv.FP8, 256, 16, 128), (airkv.BF16, 32, 16, 32)])
+def test_append_gather_other_head_dims(dtype, head_dim, bs, scale_group):
+    """head_dim 32 .. 256 beyond 64 and 128 (the pool takes any multiple of
+    32): pages, scales and both gather layouts bit-exact with the oracle."""
+    log(f"append/gather dtype={dtype} head_dim={head_dim} bs={bs} scale_group={scale_group}")
+    cfg = workloads.Config("hd", 8, 4, head_dim, bs, dtype, 5, scale_group=scale_group)
+    w = workloads.build_prefill_decode(cfg, [1, 33, 100, 257, 600], seed=120 + head_dim, decode_steps=3)
+    k, v = next(workloads.kv_rows(w.n_rows, 4, head_dim, seed=121 + head_dim, chunk_rows=1 << 20))
+    pool, host = device_pool_for(w), host_pool_for(w)
+    run_appends(w, k, v, pool, host)
+    pk, pv, pks, pvs = pool.snapshot()
+    assert_bits_equal(pk, host.k, "k pages")
+    assert_bits_equal(pv, host.v, "v pages")
+    if dtype in (airkv.INT8, airkv.FP8):
+        assert_bits_equal(pks, host.k_scales, "k scales")
+        assert_bits_equal(pvs, host.v_scales, "v scales")
+    tables, lens = w.tables()
+    outs = [airkv.F32] if dtype == airkv.F32 else [airkv.F32, airkv.BF16]
+    for out_dtype in outs:
+        for layout in (airkv.LAYOUT_HEAD_MAJOR, airkv.LAYOUT_TOKEN_MAJOR):
+            gk, gv, offs = _gather(pool, tables, lens, out_dtype, layout)
+            hk, hv, hoffs, bad = host.gather(tables, lens, out_dtype, layout)
+            assert bad == 0 and np.array_equal(offs, hoffs)
+            assert_bits_equal(gk, hk, f"gathered k out={out_dtype} layout={layout}")
+            assert_bits_equal(gv, hv, f"gathered v out={out_dtype} layout={layout}")
+    assert pool.error_count() == 0
+
+
 @pytest.mark.parametrize("name", ["f32", "bf16", "int8", "fp8"])
 def test_c1_against_committed_digests(name):
     """The GPU's c1 pages, scales and gathered views hash to the digests the

@@ -171,7 +171,7 @@ def test_unpack_blocks_matches_oracle_append(dtype):
         assert_bits_equal(gvs, host.v_scales, "unpack V scales")
 
 
-@pytest.mark.parametrize("geom", [(16, 8, 128), (32, 3, 64), (16, 5, 32)])
+@pytest.mark.parametrize("geom", [(16, 8, 128), (32, 3, 64), (16, 5, 32), (16, 4, 96), (32, 2, 256)])
 def test_bf16_special_bits_and_geometries(geom):
     """bf16 pools of several geometries (head counts that are not powers of
     two, head_dim 32..128) whose pages hold the special bit patterns:
