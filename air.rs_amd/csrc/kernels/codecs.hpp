@@ -26,19 +26,20 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_floa
 // F8E4M3::from_f32 (src/fp8.rs:54-91): -0.0 -> 0x00 (sign is x < 0), |x| >= 448
 // and exponent field 15 saturate to 0x7E, the mantissa rounds half-up and is
 // capped at 7 (no carry), subnormal results flush to signed zero, NaN -> 0x7F.
+// Written as selects, no branches: |x| >= 448 (infinity included) has an
+// exponent field of at least 15 and saturates with it, and zero has field
+// -120 and flushes with the subnormals; the sign joins every non-zero,
+// non-NaN value.
 __device__ __forceinline__ uint8_t fp8_encode(float x) {
-    if (x != x) return 0x7F;
-    uint32_t sign = x < 0.0f ? 0x80u : 0u;
-    uint32_t bits = __float_as_uint(x) & 0x7FFFFFFFu;
-    float a = __uint_as_float(bits);
-    if (a == 0.0f) return (uint8_t)sign;
-    if (a >= 448.0f) return (uint8_t)(sign | 0x7Eu);
-    int exp8 = (int)(bits >> 23) - 120;
-    if (exp8 <= 0) return (uint8_t)sign;
-    if (exp8 >= 15) return (uint8_t)(sign | 0x7Eu);
-    uint32_t mant3 = ((bits & 0x007FFFFFu) + (1u << 19)) >> 20;
+    const uint32_t bits = __float_as_uint(x), a = bits & 0x7FFFFFFFu;
+    const int exp8 = (int)(a >> 23) - 120;
+    uint32_t mant3 = ((a & 0x007FFFFFu) + (1u << 19)) >> 20;
     mant3 = mant3 > 7u ? 7u : mant3;
-    return (uint8_t)(sign | ((uint32_t)exp8 << 3) | mant3);
+    uint32_t v = ((uint32_t)exp8 << 3) | mant3;
+    v = exp8 >= 15 ? 0x7Eu : v;
+    v = exp8 <= 0 ? 0u : v;
+    v |= a != 0u ? (bits >> 24) & 0x80u : 0u;
+    return (uint8_t)(a > 0x7F800000u ? 0x7Fu : v);
 }
 
 // F8E4M3::to_f32 (src/fp8.rs:94-112): 0x7F is NaN, exponent field 0 decodes to
@@ -125,6 +126,51 @@ __device__ __forceinline__ uint8_t fp8_code(float x, float scale, float y, bool 
         if (__builtin_fabsf(q) >= 0x1p-126f) return fp8_encode(q);
     }
     return fp8_encode(x / scale);
+}
+
+// fp8_encode of a value known to be neither zero nor NaN (|x| >= 2^-126 or
+// infinite): the sign always joins, and NaN cannot occur.
+__device__ __forceinline__ uint32_t fp8_encode_nonzero(float x) {
+    const uint32_t bits = __float_as_uint(x), a = bits & 0x7FFFFFFFu;
+    const int exp8 = (int)(a >> 23) - 120;
+    uint32_t mant3 = ((a & 0x007FFFFFu) + (1u << 19)) >> 20;
+    mant3 = mant3 > 7u ? 7u : mant3;
+    uint32_t v = ((uint32_t)exp8 << 3) | mant3;
+    v = exp8 >= 15 ? 0x7Eu : v;
+    v = exp8 <= 0 ? 0u : v;
+    return v | ((bits >> 24) & 0x80u);
+}
+
+// fp8_code of eight elements sharing a scale: the corrected products for
+// all eight, and one branch (rarely taken) that divides those whose quotient
+// needs the exact division, then the codes, four per word.
+__device__ __forceinline__ void fp8_codes8(const float (&x)[8], float scale, float y, bool mark, uint32_t &lo,
+                                           uint32_t &hi) {
+#pragma clang fp contract(off)
+    float q[8];
+    bool slow = !mark;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float p = x[j] * y;
+        q[j] = __builtin_fmaf(__builtin_fmaf(-p, scale, x[j]), y, p);
+        slow |= !(__builtin_fabsf(q[j]) >= 0x1p-126f);
+    }
+    lo = 0;
+    hi = 0;
+    if (__builtin_expect(slow, 0)) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (!mark || !(__builtin_fabsf(q[j]) >= 0x1p-126f)) q[j] = x[j] / scale;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) lo |= (uint32_t)fp8_encode(q[j]) << (8 * j);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hi |= (uint32_t)fp8_encode(q[4 + j]) << (8 * j);
+    } else {                    // every quotient at least 2^-126 in magnitude (or infinite)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) lo |= fp8_encode_nonzero(q[j]) << (8 * j);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hi |= fp8_encode_nonzero(q[4 + j]) << (8 * j);
+    }
 }
 
 }  // namespace airkv

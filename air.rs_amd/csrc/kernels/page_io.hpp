@@ -99,10 +99,7 @@ __device__ __forceinline__ void quantize_chunk(const float (&x)[8], int lanes_pe
             y = 1.0f / scale;
         }
         const bool mark = __builtin_isnormal(scale) && __builtin_isnormal(y);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) lo |= (uint32_t)fp8_code(x[j], scale, y, mark) << (8 * j);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) hi |= (uint32_t)fp8_code(x[4 + j], scale, y, mark) << (8 * j);
+        fp8_codes8(x, scale, y, mark, lo, hi);
     }
 }
 
