@@ -141,35 +141,33 @@ __device__ __forceinline__ uint32_t fp8_encode_nonzero(float x) {
     return v | ((bits >> 24) & 0x80u);
 }
 
-// fp8_code of eight elements sharing a scale: the corrected products for
-// all eight, and one branch (rarely taken) that divides those whose quotient
-// needs the exact division, then the codes, four per word.
-__device__ __forceinline__ void fp8_codes8(const float (&x)[8], float scale, float y, bool mark, uint32_t &lo,
-                                           uint32_t &hi) {
+// fp8_code of N elements sharing a scale: the corrected products for all
+// N, and one branch (rarely taken) that divides those whose quotient needs
+// the exact division, then the codes, four per word (element 4i + j in byte
+// j of w[i]).
+template <int N>
+__device__ __forceinline__ void fp8_codes(const float (&x)[N], float scale, float y, bool mark,
+                                          uint32_t (&w)[N / 4]) {
 #pragma clang fp contract(off)
-    float q[8];
+    float q[N];
     bool slow = !mark;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < N; ++j) {
         const float p = x[j] * y;
         q[j] = __builtin_fmaf(__builtin_fmaf(-p, scale, x[j]), y, p);
         slow |= !(__builtin_fabsf(q[j]) >= 0x1p-126f);
     }
-    lo = 0;
-    hi = 0;
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) w[i] = 0;
     if (__builtin_expect(slow, 0)) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < N; ++j)
             if (!mark || !(__builtin_fabsf(q[j]) >= 0x1p-126f)) q[j] = x[j] / scale;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) lo |= (uint32_t)fp8_encode(q[j]) << (8 * j);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) hi |= (uint32_t)fp8_encode(q[4 + j]) << (8 * j);
+        for (int j = 0; j < N; ++j) w[j / 4] |= (uint32_t)fp8_encode(q[j]) << (8 * (j % 4));
     } else {                    // every quotient at least 2^-126 in magnitude (or infinite)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) lo |= fp8_encode_nonzero(q[j]) << (8 * j);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) hi |= fp8_encode_nonzero(q[4 + j]) << (8 * j);
+        for (int j = 0; j < N; ++j) w[j / 4] |= fp8_encode_nonzero(q[j]) << (8 * (j % 4));
     }
 }
 

@@ -62,24 +62,44 @@ __device__ __forceinline__ void load8(const void *pages, const float *scales, in
 }
 
 
-// The INT8 / FP8 codes (lo: elements 0..3, hi: 4..7, one byte each) and the
-// group scale of 8 f32 of one scale group: the lanes_per_group consecutive
-// lanes holding the group reduce its absmax with butterfly shuffles (every
-// lane of the group must call this).  The absmax folds from 0.0 with a
+// A lane's value from lane (l & ~3) | perm[l & 3] of its quad, or from the
+// mirror image of its 8- or 16-lane row (DPP: no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// The absmax of m over each aligned run of lanes_per_group (a power of two,
+// at most 64) lanes, in every lane of the run: after the two quad steps a
+// lane holds its quad's maximum, the half-row mirror joins the other quad of
+// its 8 lanes, the row mirror the other half of its 16, and shuffles the
+// rest.  Every lane of a run must be active.
+__device__ __forceinline__ float group_absmax(float m, int lanes_per_group) {
+    if (lanes_per_group > 1) m = absmax_step(m, dpp_f32<0xB1>(m));     // quad_perm [1, 0, 3, 2]
+    if (lanes_per_group > 2) m = absmax_step(m, dpp_f32<0x4E>(m));     // quad_perm [2, 3, 0, 1]
+    if (lanes_per_group > 4) m = absmax_step(m, dpp_f32<0x141>(m));    // row_half_mirror
+    if (lanes_per_group > 8) m = absmax_step(m, dpp_f32<0x140>(m));    // row_mirror
+    for (int mask = 16; mask < lanes_per_group; mask <<= 1) m = absmax_step(m, __shfl_xor(m, mask));
+    return m;
+}
+
+// The INT8 / FP8 codes (element 4i + j in byte j of w[i]) and the group
+// scale of a lane's N f32 of one scale group: the lanes_per_group
+// consecutive lanes holding the group reduce its absmax with butterfly
+// shuffles (every lane of the group must call this).  The absmax folds from 0.0 with a
 // NaN-ignoring max (src/kv_cache.rs:60, src/fp8.rs:228-232); max is order
 // independent, so the lane-parallel reduction equals the reference's
 // sequential fold.  Shared by the append kernel and the fused append of the
 // decode kernel, so both write the same bytes.
-template <int DT>
-__device__ __forceinline__ void quantize_chunk(const float (&x)[8], int lanes_per_group, uint32_t &lo,
-                                               uint32_t &hi, float &scale) {
+template <int DT, int N>
+__device__ __forceinline__ void quantize_elems(const float (&x)[N], int lanes_per_group, uint32_t (&w)[N / 4],
+                                               float &scale) {
     static_assert(DT == AIR_KV_INT8 || DT == AIR_KV_FP8, "1-byte pages only");
+    static_assert(N % 4 == 0, "whole code words");
     float m = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) m = absmax_step(m, x[j]);
-    for (int mask = 1; mask < lanes_per_group; mask <<= 1) m = absmax_step(m, __shfl_xor(m, mask));
-    lo = 0;
-    hi = 0;
+    for (int j = 0; j < N; ++j) m = absmax_step(m, x[j]);
+    m = group_absmax(m, lanes_per_group);
     if constexpr (DT == AIR_KV_INT8) {
         scale = q8_scale(m);
         float inv;
@@ -88,9 +108,9 @@ __device__ __forceinline__ void quantize_chunk(const float (&x)[8], int lanes_pe
             inv = 1.0f / scale;
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) lo |= (uint32_t)(uint8_t)q8_code(x[j], inv) << (8 * j);
+        for (int i = 0; i < N / 4; ++i) w[i] = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) hi |= (uint32_t)(uint8_t)q8_code(x[4 + j], inv) << (8 * j);
+        for (int j = 0; j < N; ++j) w[j / 4] |= (uint32_t)(uint8_t)q8_code(x[j], inv) << (8 * (j % 4));
     } else {
         scale = fp8_scale(m);
         float y;
@@ -99,8 +119,18 @@ __device__ __forceinline__ void quantize_chunk(const float (&x)[8], int lanes_pe
             y = 1.0f / scale;
         }
         const bool mark = __builtin_isnormal(scale) && __builtin_isnormal(y);
-        fp8_codes8(x, scale, y, mark, lo, hi);
+        fp8_codes<N>(x, scale, y, mark, w);
     }
+}
+
+// quantize_elems of a lane's 8 elements: codes of elements 0..3 in lo, 4..7 in hi.
+template <int DT>
+__device__ __forceinline__ void quantize_chunk(const float (&x)[8], int lanes_per_group, uint32_t &lo,
+                                               uint32_t &hi, float &scale) {
+    uint32_t w[2];
+    quantize_elems<DT, 8>(x, lanes_per_group, w, scale);
+    lo = w[0];
+    hi = w[1];
 }
 
 // 8 f32 -> page: F32 stored as is, BF16 rounded to nearest even, INT8 / FP8

@@ -105,10 +105,13 @@ def test_c1_append_gather_bitexact(dtype):
 
 @pytest.mark.parametrize("dtype,head_dim,bs,scale_group", [
     (airkv.F32, 96, 16, 32), (airkv.BF16, 160, 32, 32), (airkv.INT8, 224, 16, 32), (airkv.FP8, 32, 32, 32),
-    (airkv.BF16, 256, 16, 32), (airkv.INT8, 96, 32, 16), (airkv.FP8, 256, 16, 128), (airkv.BF16, 32, 16, 32)])
+    (airkv.BF16, 256, 16, 32), (airkv.INT8, 96, 32, 16), (airkv.FP8, 256, 16, 128), (airkv.BF16, 32, 16, 32),
+    (airkv.INT8, 128, 16, 8), (airkv.FP8, 128, 32, 8), (airkv.INT8, 128, 32, 128), (airkv.FP8, 128, 16, 16)])
 def test_append_gather_other_head_dims(dtype, head_dim, bs, scale_group):
     """head_dim 32 .. 256 beyond 64 and 128 (the pool takes any multiple of
-    32): pages, scales and both gather layouts bit-exact with the oracle."""
+    32), and 1-byte pages at head_dim 128 with scale groups of 8 .. 128
+    elements (2 .. 32 lanes of the whole-line append): pages, scales and
+    both gather layouts bit-exact with the oracle."""
     log(f"append/gather dtype={dtype} head_dim={head_dim} bs={bs} scale_group={scale_group}")
     cfg = workloads.Config("hd", 8, 4, head_dim, bs, dtype, 5, scale_group=scale_group)
     w = workloads.build_prefill_decode(cfg, [1, 33, 100, 257, 600], seed=120 + head_dim, decode_steps=3)
