@@ -63,11 +63,16 @@ __device__ __forceinline__ void load8(const void *pages, const float *scales, in
 
 
 // A lane's value from lane (l & ~3) | perm[l & 3] of its quad, or from the
-// mirror image of its 8- or 16-lane row (DPP: no LDS round trip).
+// mirror image of its 8- or 16-lane row (DPP: no LDS round trip).  The
+// source lanes must be active.
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
 }
+constexpr int kQuadXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]: lane l ^ 1
+constexpr int kQuadXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]: lane l ^ 2
+constexpr int kRowHalfMirror = 0x141;  // lane 7 - l within each 8 lanes
+constexpr int kRowMirror = 0x140;      // lane 15 - l within each 16 lanes
 
 // The absmax of m over each aligned run of lanes_per_group (a power of two,
 // at most 64) lanes, in every lane of the run: after the two quad steps a
@@ -75,10 +80,10 @@ __device__ __forceinline__ float dpp_f32(float v) {
 // its 8 lanes, the row mirror the other half of its 16, and shuffles the
 // rest.  Every lane of a run must be active.
 __device__ __forceinline__ float group_absmax(float m, int lanes_per_group) {
-    if (lanes_per_group > 1) m = absmax_step(m, dpp_f32<0xB1>(m));     // quad_perm [1, 0, 3, 2]
-    if (lanes_per_group > 2) m = absmax_step(m, dpp_f32<0x4E>(m));     // quad_perm [2, 3, 0, 1]
-    if (lanes_per_group > 4) m = absmax_step(m, dpp_f32<0x141>(m));    // row_half_mirror
-    if (lanes_per_group > 8) m = absmax_step(m, dpp_f32<0x140>(m));    // row_mirror
+    if (lanes_per_group > 1) m = absmax_step(m, dpp_f32<kQuadXor1>(m));
+    if (lanes_per_group > 2) m = absmax_step(m, dpp_f32<kQuadXor2>(m));
+    if (lanes_per_group > 4) m = absmax_step(m, dpp_f32<kRowHalfMirror>(m));
+    if (lanes_per_group > 8) m = absmax_step(m, dpp_f32<kRowMirror>(m));
     for (int mask = 16; mask < lanes_per_group; mask <<= 1) m = absmax_step(m, __shfl_xor(m, mask));
     return m;
 }
