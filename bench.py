@@ -86,6 +86,25 @@ def timed_loop(torch, fn, iters, lead_sleep=True):
     return e0.elapsed_time(e1) / iters   # ms
 
 
+def per_call_us(torch, fn, iters=100, warmup=10):
+    """(p10, p50, p90) in us of single launches of fn(): events recorded
+    between back-to-back launches (a sleep kernel first lets the host queue
+    them all), after `warmup` untimed launches."""
+    import numpy as np
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
+    torch.cuda._sleep(20_000_000)
+    ev[0].record()
+    for i in range(iters):
+        fn()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    d = np.array([ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(iters)])
+    return tuple(round(float(x), 2) for x in np.percentile(d, [10, 50, 90]))
+
+
 def twin_pool(torch, pool):
     """A second pool of the same geometry holding the same bytes (device to
     device copy of pages and scales), so timed calls can alternate between
@@ -926,8 +945,11 @@ def main():
     dec_bytes = decode_bytes(np.array(lens0) + n_steps)
     dec_gbps = dec_bytes / (ms_dec * 1e-3) / 1e9
     log(f"decode {ms_dec * 1e3:.1f} us, {dec_gbps:.0f} GB/s ({dec_gbps / PEAK_HBM_GBPS:.1%} of peak)")
+    dec_pct = per_call_us(torch, last)
+    log(f"decode per call p10 / p50 / p90: {dec_pct} us")
 
     extra = dict(extra_step)
+    extra["decode_us_p10_p50_p90"] = list(dec_pct)
     legs = set(args.legs.split(",")) if args.legs != "all" else {
         "gather_append", "ceilings", "configs", "quant_append", "c5_step", "prefill", "compress", "blocks"}
     if args.only_decode:
