@@ -642,10 +642,11 @@ impl KvPool {
             .map(|_| ())
     }
 
-    /// One decode step in one launch (bf16 pools, head_dim 128, group
-    /// 1..16): appends `k_new` / `v_new` (f32 `[batch][n_kv_heads][head_dim]`,
-    /// 16-byte aligned) as each sequence's token `lens[b] - 1`, then attends
-    /// as [`KvPool::paged_decode`] (src/model.rs:569-577).
+    /// One decode step: appends `k_new` / `v_new` (f32
+    /// `[batch][n_kv_heads][head_dim]`, 16-byte aligned) as each sequence's
+    /// token `lens[b] - 1`, then attends as [`KvPool::paged_decode`]
+    /// (src/model.rs:569-577).  One launch on bf16, int8 and fp8 pools with
+    /// head_dim 128 and group 1..16; append, then decode, on every other pool.
     ///
     /// # Safety
     /// As [`KvPool::paged_decode`]; `k_new` / `v_new` are device arrays of
