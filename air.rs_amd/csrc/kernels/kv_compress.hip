@@ -301,22 +301,17 @@ __global__ __launch_bounds__(kThreads) void key_compress_staged_kernel(CompressA
 // the quarters left to right reproduces the reference's left fold bit for
 // bit (signed zeros and NaN skipping included).  A wave then reads 16 whole
 // rows and writes 16 contiguous code rows.
-template <int DT, int D>
-__global__ __launch_bounds__(kThreads) void value_compress_kernel(CompressArgs a) {
+// Row r's codes, scale and min from its quarter `part` (elements part * D / 4
+// .. + D / 4) in x, held by the lane; the row's four lanes are one quad of
+// the wave and call this together.  A row of an out-of-pool block (live
+// false) gets zero codes, scale and min whatever x holds.
+template <int D>
+__device__ __forceinline__ void value_encode_row(const CompressArgs &a, int64_t r, int part,
+                                                 const float (&x)[D / 4], bool live) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    constexpr int P = 4, N = D / P;                // lanes per row, elements per lane
-    const int part = threadIdx.x & (P - 1);
-    // the four lanes of a row share r, so they run the loop in lockstep
-    for (int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x; t / P < a.n_rows;
-         t += (int64_t)gridDim.x * kThreads) {
-        const int64_t r = t / P;
-        float x[N];
-        bool live;
-        // a row of an out-of-pool block gets zero codes, scale and min below,
-        // whatever its loaded values were, so they are not zeroed first
-        load_row<DT, D, N, false>(a.src, r, x, live, part * N);
-        if (!live && a.errors && part == 0 && (r % a.src.rows_per_block) == 0) atomicAdd(a.errors, 1ull);
+    constexpr int N = D / 4;
+    {
         // (:198-199).  The folds' value is the row's NaN-ignoring min / max,
         // which the hardware min / max give in one instruction per element
         // once signalling NaNs are quieted (given one, they return a NaN
@@ -420,6 +415,96 @@ __global__ __launch_bounds__(kThreads) void value_compress_kernel(CompressArgs a
             a.f0[r] = scale;
             a.f1[r] = lo;
         }
+    }
+}
+
+// The value codec with staged loads: a wave takes 16 consecutive rows (one
+// pool block's, or dense rows: contiguous either way), reads their bytes as
+// consecutive 16-byte pieces (each load instruction covers whole lines;
+// non-temporal, each byte is read once), parks them in its own LDS slice
+// and gives lane 4 i + p quarter p of row i, converted as load_row converts
+// it.  Per-row loads made each instruction touch 32 lines and use a quarter
+// of each.
+template <int DT, int D>
+__global__ __launch_bounds__(kThreads) void value_compress_staged_kernel(CompressArgs a) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    constexpr int EB = elem_bytes<DT>();
+    constexpr int RB = D * EB, QB = RB / 4;           // row and quarter-row bytes
+    constexpr int PITCH = RB + 16;
+    constexpr int CPL = RB / 64;                      // 16-byte pieces per lane for 16 rows
+    constexpr int N = D / 4;
+    if constexpr (QB % 16 != 0) {
+        // quarter rows under 16 bytes (1-byte rows of 32): the per-row loader
+        const int part = threadIdx.x & 3;
+        for (int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x; t / 4 < a.n_rows;
+             t += (int64_t)gridDim.x * kThreads) {
+            const int64_t r = t / 4;
+            float x[N];
+            bool live;
+            load_row<DT, D, N, false>(a.src, r, x, live, part * N);
+            if (!live && a.errors && part == 0 && (r % a.src.rows_per_block) == 0) atomicAdd(a.errors, 1ull);
+            value_encode_row<D>(a, r, part, x, live);
+        }
+        return;
+    } else {
+    __shared__ __align__(16) uint8_t smem[kThreads / 64][16 * PITCH];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint8_t *lds = smem[wave];
+    const int row = lane >> 2, part = lane & 3;
+    const int64_t groups = (a.n_rows + 15) / 16;
+    for (int64_t g = (int64_t)blockIdx.x * (kThreads / 64) + wave; g < groups;
+         g += (int64_t)gridDim.x * (kThreads / 64)) {
+        const int64_t r0 = 16 * g, r = r0 + row;
+        int64_t e0;
+        const bool live = row_elem(a.src, r0, D, e0);    // the 16 rows share one block
+        const uint8_t *gbase = (const uint8_t *)a.src.base + e0 * EB;
+        u32x4 c[CPL];
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {                   // piece k = 64 i + lane: row 16 k / RB
+            const int k = 64 * i + lane, kr = (16 * k) / RB, kb = (16 * k) % RB;
+            const u32x4 *src = reinterpret_cast<const u32x4 *>(gbase + (int64_t)kr * RB + kb);
+            c[i] = live && r0 + kr < a.n_rows ? __builtin_nontemporal_load(src) : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int k = 64 * i + lane, kr = (16 * k) / RB, kb = (16 * k) % RB;
+            *reinterpret_cast<u32x4 *>(lds + kr * PITCH + kb) = c[i];
+        }
+        float x[N];
+#pragma unroll
+        for (int i = 0; i < QB / 16; ++i) {
+            const u32x4 w = *reinterpret_cast<const u32x4 *>(lds + row * PITCH + part * QB + 16 * i);
+            if constexpr (DT == AIR_KV_F32) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) x[4 * i + j] = __uint_as_float(w[j]);
+            } else if constexpr (DT == AIR_KV_BF16) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    x[8 * i + 2 * j] = __uint_as_float(w[j] << 16);
+                    x[8 * i + 2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+                }
+            } else {
+                // 16 codes: elements part * N + 16 i .. + 16 of the row, their
+                // group scales as load_row reads them (groups of >= 8)
+                const int64_t el = e0 + (int64_t)row * D + part * N + 16 * i;
+                const float s0 = live ? a.src.scales[el / a.src.scale_group] : 0.0f;
+                const float s1 = live ? a.src.scales[(el + 8) / a.src.scale_group] : 0.0f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const uint32_t byte = (w[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+                    const float val = DT == AIR_KV_INT8 ? (float)(int32_t)(int8_t)byte : fp8_decode(byte);
+                    {
+#pragma clang fp contract(off)
+                        x[16 * i + j] = val * (j < 8 ? s0 : s1);
+                    }
+                }
+            }
+        }
+        if (r >= a.n_rows) continue;          // a quad's lanes share r: whole quads leave
+        if (!live && a.errors && part == 0 && (r % a.src.rows_per_block) == 0) atomicAdd(a.errors, 1ull);
+        value_encode_row<D>(a, r, part, x, live);
+    }
     }
 }
 
@@ -545,8 +630,7 @@ bool compress_dim_supported(int dim) { return dim == 32 || dim == 64 || dim == 1
 
 hipError_t launch_compress(CompressKind kind, const CompressArgs &a, int cus, hipStream_t s) {
     if (a.n_rows == 0) return hipSuccess;
-    const int lanes_per_row = kind == CompressKind::Value ? 4 : 1;
-    const dim3 grid((unsigned)grid_for(a.n_rows * lanes_per_row, kThreads, cus));
+    const dim3 grid((unsigned)grid_for(a.n_rows, kThreads, cus));
     // rows in contiguous runs of 64: the staged key codec, one wave per 64 rows
     const bool runs64 = !a.src.ids || a.src.rows_per_block % 64 == 0;
     if (kind == CompressKind::Key && runs64) {
@@ -554,9 +638,15 @@ hipError_t launch_compress(CompressKind kind, const CompressArgs &a, int cus, hi
         AIRKV_LAUNCH_D(key_compress_staged_kernel, a, s, g)
         return hipGetLastError();
     }
+    if (kind == CompressKind::Value) {
+        // one wave per 16 rows (a pool block holds n_kv_heads * block_size
+        // rows, a multiple of 16, so they share one block)
+        const dim3 g((unsigned)grid_for((a.n_rows + 15) / 16 * 64, kThreads, cus));
+        AIRKV_LAUNCH_D(value_compress_staged_kernel, a, s, g)
+        return hipGetLastError();
+    }
     switch (kind) {
     case CompressKind::Key: AIRKV_LAUNCH_D(key_compress_kernel, a, s, grid) break;
-    case CompressKind::Value: AIRKV_LAUNCH_D(value_compress_kernel, a, s, grid) break;
     default: AIRKV_LAUNCH_D(qjl_compress_kernel, a, s, grid) break;
     }
     return hipGetLastError();

@@ -178,20 +178,26 @@ def _pool_rows_f32(host, dtype, which):
     return (vals * sc[..., None]).reshape(-1, host.head_dim)
 
 
-@pytest.mark.parametrize("dtype", [airkv.F32, airkv.BF16, airkv.INT8, airkv.FP8])
-def test_compress_blocks_matches_oracle(dtype):
+@pytest.mark.parametrize("dtype,d,sg", [(airkv.F32, 128, 32), (airkv.BF16, 128, 32), (airkv.INT8, 128, 32),
+                                        (airkv.FP8, 128, 32), (airkv.INT8, 64, 8), (airkv.FP8, 64, 16),
+                                        (airkv.INT8, 32, 16), (airkv.FP8, 32, 32), (airkv.BF16, 32, 32),
+                                        (airkv.F32, 64, 32)])
+def test_compress_blocks_matches_oracle(dtype, d, sg):
+    """Codecs straight from pool blocks of every page dtype, head_dim 32 .. 128
+    and scale groups of 8 .. 32 elements (1-byte rows of 32 take the per-row
+    loader, the others the staged loads)."""
     torch = torch_mod()
-    cfg = workloads.Config("cb", 8, 4, 128, 16, dtype, 3)
+    cfg = workloads.Config("cb", 8, 4, d, 16, dtype, 3, scale_group=sg)
     w = workloads.build_prefill_decode(cfg, [40, 70, 33], seed=13, decode_steps=0)
-    k, v = next(workloads.kv_rows(w.n_rows, 4, 128, seed=14, chunk_rows=1 << 20))
+    k, v = next(workloads.kv_rows(w.n_rows, 4, d, seed=14, chunk_rows=1 << 20))
     pool, host = device_pool_for(w), host_pool_for(w)
     run_appends(w, k, v, pool, host)
     ids = np.array([3, 0, w.num_blocks - 1, 7], np.int32)
     out = kc.compress_blocks(pool, torch.from_numpy(ids).cuda())
-    proj = oracle.qjl_projection_matrix(64, 128, seed=3)
+    proj = oracle.qjl_projection_matrix(64, d, seed=3)
     qbits, qmag = kc.qjl_compress_blocks(pool, torch.from_numpy(ids).cuda(), torch.from_numpy(proj).cuda(), 64)
-    kr = _pool_rows_f32(host, dtype, "k").reshape(w.num_blocks, -1, 128)[ids].reshape(-1, 128)
-    vr = _pool_rows_f32(host, dtype, "v").reshape(w.num_blocks, -1, 128)[ids].reshape(-1, 128)
+    kr = _pool_rows_f32(host, dtype, "k").reshape(w.num_blocks, -1, d)[ids].reshape(-1, d)
+    vr = _pool_rows_f32(host, dtype, "v").reshape(w.num_blocks, -1, d)[ids].reshape(-1, d)
     ob, om, omean = _oracle_keys(kr)
     oc, osc, omn = _oracle_values(vr)
     assert_bits_equal(kc.as_u64(out["key_bits"]), ob, "block key bits")
