@@ -168,8 +168,10 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     // wave and over the waves, the total in wave 0's lanes < LPR.  An
     // out-of-pool table entry is counted (count) by every row that meets it
     // (kCountRows) or once, at its block's first token (kCountBlocks), or not
-    // at all (kCountNone).
-    auto attend = [&](int64_t start, int64_t end, int count) {
+    // at all (kCountNone); its tokens are skipped (decode) or read as zero
+    // keys and values (oob_zero: prefill, as the matrix-core prefill reads
+    // them).
+    auto attend = [&](int64_t start, int64_t end, int count, bool oob_zero) {
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -186,14 +188,16 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
                 const int64_t t = t0 + r;
                 bool ok = t < end;
                 int32_t blk = ok ? table[t / a.block_size] : 0;
+                bool in_pool = true;
                 if (ok && (blk < 0 || blk >= a.num_blocks)) {
-                    ok = false;
+                    in_pool = false;
+                    ok = oob_zero;
                     if (chunk == 0 && (count == kCountRows ||
                                        (count == kCountBlocks && (t % a.block_size == 0 || t == start))))
                         atomicAdd(a.errors, 1ull);
                 }
                 Raw8<DT> kraw;
-                if (ok && cv) {
+                if (ok && cv && in_pool) {
                     const int64_t row = ((int64_t)blk * a.n_kv_heads + kh) * a.block_size + t % a.block_size;
                     const int64_t sidx = row * ng + (chunk * 8) / sg;
                     load_raw<DT>(a.k_pages, a.k_scales, row * d + chunk * 8, sidx, kraw);
@@ -312,7 +316,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
             load_q(qrow);
             // the last row reads every key: its first head chunk counts each
             // out-of-pool entry once
-            attend(0, len - qlen + r + 1, r == qlen - 1 && blockIdx.y == 0 ? kCountBlocks : kCountNone);
+            attend(0, len - qlen + r + 1, r == qlen - 1 && blockIdx.y == 0 ? kCountBlocks : kCountNone, true);
             if (wave == 0 && lane < LPR && cv) {
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
@@ -345,7 +349,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     if (start >= len) return;
     const int64_t end = start + a.part_tokens < len ? start + a.part_tokens : len;
     load_q(b);
-    attend(start, end, kCountRows);
+    attend(start, end, kCountRows, false);
     if (wave == 0 && lane < LPR && cv) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {

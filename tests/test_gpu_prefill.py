@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 
 import airkv
+import oracle
 from airkv import workloads
 from gpu_helpers import device_pool_for, host_pool_for, log, rel_err, run_appends, torch_mod
 
@@ -92,7 +93,8 @@ def test_prefill_vector_path_invalid_sequences():
     """The vector prefill keeps the matrix-core prefill's error handling: a
     chunk longer than its sequence and a seq_len beyond the table are each
     counted once with their rows zero-filled, the valid sequence matches the
-    oracle, and an out-of-pool table entry inside a sequence is counted once."""
+    oracle, and an out-of-pool table entry inside a sequence is counted once
+    and read as zero keys and values."""
     torch = torch_mod()
     cfg = workloads.Config("badvec", 8, 2, 128, 16, airkv.F32, 3)
     pool, host, tables, lens = _setup(cfg, [40, 50, 60], seed=79)
@@ -120,7 +122,16 @@ def test_prefill_vector_path_invalid_sequences():
                        torch.from_numpy(lens[:1]).cuda(), out1)
     torch.cuda.synchronize()
     assert pool.error_count(reset=True) == 1
-    assert torch.isfinite(out1).all()
+    # the entry's tokens read as zero keys and values (as the matrix-core
+    # prefill reads them): the oracle over a host pool with one more block,
+    # all zeros, in the entry's place
+    hz = oracle.HostPool(host.num_blocks + 1, 16, 2, 128, oracle.F32)
+    hz.k[:-1], hz.v[:-1] = host.k, host.v
+    hz.k[-1], hz.v[-1] = 0.0, 0.0
+    tz = t2[:1].copy()
+    tz[0, 1] = host.num_blocks
+    want1 = hz.paged_prefill(q[:10].cpu().numpy(), cu1, tz, lens[:1])
+    assert rel_err(out1.cpu().numpy(), want1) <= 1e-3
     assert pool.prefill_workspace_size(8, 3, 60) == 0
 
 
