@@ -378,8 +378,17 @@ def test_prefill_invalid_sequences_counted_and_zeroed():
     out1 = torch.zeros((10, 8, 128), device="cuda")
     pool.paged_prefill(q[:10].contiguous(), torch.from_numpy(cu1).cuda(), torch.from_numpy(t2[:1]).cuda(),
                        torch.from_numpy(lens[:1]).cuda(), out1)
+    torch.cuda.synchronize()
     assert pool.error_count(reset=True) == 1
     assert torch.isfinite(out1).all()
+    # its tokens read as zero keys and values: the oracle over a host pool
+    # with one more block, all zeros, in the entry's place
+    hz = oracle.HostPool(host.num_blocks + 1, 16, 2, 128, oracle.BF16)
+    hz.k[:-1], hz.v[:-1] = host.k, host.v
+    tz = t2[:1].copy()
+    tz[0, 1] = host.num_blocks
+    want1 = hz.paged_prefill(q[:10].float().cpu().numpy(), cu1, tz, lens[:1])
+    assert rel_err(out1.cpu().numpy(), want1) <= 1e-3
 
 
 def _long_split_pool(bs=16, L=12288, seed=161):
