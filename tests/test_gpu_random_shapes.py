@@ -7,6 +7,8 @@ included), query and output dtypes.  Each case checks, through the C ABI:
   * the decode step as one call (air_paged_decode_append) against the
     append + decode calls on a second pool: pages, scales and outputs bit
     for bit, and the outputs within tolerance of the oracle's decode;
+  * the gather of every sequence (a random layout; f32, and bf16 for
+    non-f32 pools), bit-exact with the oracle's;
   * the paged prefill of the newest rows of a few sequences (chunks of 0 ..
     32 rows) within tolerance of the oracle's blockwise attention.
 
@@ -111,6 +113,25 @@ def test_random_shape(seed):
     err = rel_err(got_a, want)
     log(f"  decode rel err {err:.2e}")
     assert err <= tol
+
+    # gather: both layouts, f32 views (quantized pages dequantized) and the
+    # cache dtype's bf16 views, bit-exact with the oracle's
+    per = lens.astype(np.int64) * n_kv * d
+    offs = np.concatenate([[0], np.cumsum(per)[:-1]]).astype(np.int64)
+    for out_dtype in ([airkv.F32] if dtype == airkv.F32 else [airkv.F32, airkv.BF16]):
+        layout = int(rng.choice([airkv.LAYOUT_HEAD_MAJOR, airkv.LAYOUT_TOKEN_MAJOR]))
+        gdt = torch.float32 if out_dtype == airkv.F32 else torch.bfloat16
+        gk = torch.zeros(int(per.sum()), dtype=gdt, device="cuda")
+        gv = torch.zeros_like(gk)
+        pa.gather(tt, lt, dev(offs), gk, gv, out_dtype, layout)
+        torch.cuda.synchronize()
+        hk, hv, hoffs, bad = host.gather(tables, lens, out_dtype, layout)
+        assert bad == 0 and np.array_equal(offs, hoffs)
+        view = np.uint32 if out_dtype == airkv.F32 else np.uint16
+        assert_bits_equal(gk.cpu().view(torch.int32 if out_dtype == airkv.F32 else torch.int16).numpy().view(view),
+                          hk.view(view), f"gathered k out={out_dtype} layout={layout}")
+        assert_bits_equal(gv.cpu().view(torch.int32 if out_dtype == airkv.F32 else torch.int16).numpy().view(view),
+                          hv.view(view), f"gathered v out={out_dtype} layout={layout}")
 
     # prefill: the newest rows of up to four sequences
     sel = rng.choice(len(lens), size=min(4, len(lens)), replace=False)
