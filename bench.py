@@ -29,6 +29,7 @@ for _p in (ROOT, os.path.join(ROOT, "air.rs_amd")):
         sys.path.insert(0, _p)
 
 PEAK_HBM_GBPS = 8000.0   # MI355X HBM3E spec
+PEAK_F32_TFLOPS = 157.3  # MI355X published fp32 peak
 # rocprofv3 FETCH_SIZE + WRITE_SIZE of the decode call on this workload, scaled
 # by the counters' reading for a 1 GiB copy (the summary lists the commands)
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "paged_decode_c2.md")
@@ -475,10 +476,30 @@ def compress_leg(torch, iters=10):
     ms = timed_loop(torch, lambda: L.air_kv_compress_blocks(*args), iters)
     rows = nb * 16 * 8
     nbytes = rows * (2 * 256 + 16 + 8 + 128 + 8) + 4 * nb
+    res = {"gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "us": round(ms * 1e3, 1), "rows": rows,
+           "blocks": nb, "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+    # QJL (src/kv_compress.rs:908-975) at the reference's QJL_PROJ_DIM = 64: the
+    # sign projection of the same 1M key rows (m dot products of d products
+    # and sums each, contraction off as the reference folds them), then one
+    # query's Hamming scores against every compressed key
+    m = 64
+    proj = torch.randn(m * 128, device="cuda") / 128 ** 0.5
+    qbits, qmag = kc.qjl_compress_blocks(pool, ids, proj, m)
+    ms_q = timed_loop(torch, lambda: kc.qjl_compress_blocks(pool, ids, proj, m), iters)
+    flops = rows * m * 128 * 2
+    res["qjl_compress"] = {"us": round(ms_q * 1e3, 1), "rows": rows, "proj_dim": m,
+                           "tflops_f32": round(flops / (ms_q * 1e-3) / 1e12, 1),
+                           "frac_of_f32_peak": round(flops / (ms_q * 1e-3) / 1e12 / PEAK_F32_TFLOPS, 4),
+                           "gbps": round(rows * (256 + 8 + 4) / (ms_q * 1e-3) / 1e9, 1)}
+    qb = qbits[0].clone()
+    ms_s = timed_loop(torch, lambda: kc.qjl_scores(qbits, qmag, qb, 1.0, m), iters)
+    sbytes = rows * (8 + 4 + 4 + 4)
+    res["qjl_scores"] = {"us": round(ms_s * 1e3, 1), "keys": rows,
+                         "gbps": round(sbytes / (ms_s * 1e-3) / 1e9, 1),
+                         "frac": round(sbytes / (ms_s * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
     assert pool.error_count() == 0
     pool.close()
-    return {"gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "us": round(ms * 1e3, 1), "rows": rows,
-            "blocks": nb, "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+    return res
 
 
 def blocks_leg(torch, iters=20):
