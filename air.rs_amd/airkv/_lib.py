@@ -148,10 +148,6 @@ SIGNATURES = {
                                                ctypes.POINTER(ctypes.c_float), ctypes.POINTER(_P),
                                                ctypes.POINTER(_SZ)]),
     "air_kv_int8_payload_serialise_n": (_int, [_P, ctypes.c_uint16, _P, _P, _SZ, _i32, _P]),
-    "air_kv_stream_record_header": (_int, [ctypes.c_uint64, _u32, _P]),
-    "air_kv_warp_header_serialise": (_int, [ctypes.c_uint64, _u32, _P]),
-    "air_kv_warp_header_deserialise": (_int, [_P, _SZ, ctypes.POINTER(ctypes.c_uint64), _pu32,
-                                              ctypes.POINTER(ctypes.c_uint16)]),
     "air_kv_copy_blocks": (_int, [_P, _P, _P, _P, _i32]),
     "air_kv_read_blocks": (_int, [_P, _P, _pi32, _i32, _P]),
     "air_kv_write_blocks": (_int, [_P, _P, _pi32, _i32, _P]),

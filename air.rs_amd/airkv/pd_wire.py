@@ -1,5 +1,5 @@
 """KvBlock and the disaggregation wire framing (src/pd_disagg.rs:39-104,
-:267-279; src/warp_protocol.rs:25-63) over the C ABI.
+:267-276) over the C ABI.
 
 ``KvBlock`` keeps the reference's fields and methods (serialise /
 deserialise / int8_quantize); ``frames_from_pool`` and
@@ -114,18 +114,3 @@ def int8_payloads_from_pool(pool, ids, layer_idx: int) -> bytes:
                                                            c.shape[1], len(ids), out.ctypes.data),
                "int8_payloads_from_pool")
     return out.tobytes()
-
-
-def warp_header(features: int, body_len: int) -> bytes:
-    out = (ctypes.c_uint8 * 18)()
-    _lib.check(_lib.load().air_kv_warp_header_serialise(features, body_len, out), "warp_header")
-    return bytes(out)
-
-
-def parse_warp_header(buf: bytes):
-    """(features, body_len, version) or raises AirKvError (bad magic / major)."""
-    b = (ctypes.c_uint8 * max(len(buf), 1)).from_buffer_copy(bytes(buf) or b"\x00")
-    f, n, v = ctypes.c_uint64(), ctypes.c_uint32(), ctypes.c_uint16()
-    _lib.check(_lib.load().air_kv_warp_header_deserialise(b, len(buf), ctypes.byref(f), ctypes.byref(n),
-                                                          ctypes.byref(v)), "parse_warp_header")
-    return f.value, n.value, v.value

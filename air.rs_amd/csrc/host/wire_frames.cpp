@@ -1,9 +1,8 @@
 // Host-side framing of KvBlocks for prefill/decode disaggregation: the byte
 // layouts of src/pd_disagg.rs around the wire data that air_kv_pack_blocks /
-// air_kv_pack_blocks_int8 produce on the device, and the W.A.R.P. header of
-// src/warp_protocol.rs.  Every integer is little-endian, as the reference's
-// to_le_bytes writes it; the functions do not depend on the host's byte
-// order.
+// air_kv_pack_blocks_int8 produce on the device.  Every integer is
+// little-endian, as the reference's to_le_bytes writes it; the functions do
+// not depend on the host's byte order.
 #include <cstring>
 
 #include "air_kv.h"
@@ -15,8 +14,6 @@ namespace {
 
 constexpr size_t kFrameHeader = 10;    // [block_id:4][layer_idx:2][data_len:4]
 constexpr size_t kInt8Header = 14;     // [block_id:4][layer_idx:2][scale:4][len:4]
-constexpr uint8_t kWarpMagic[4] = {'W', 'A', 'R', 'P'};
-constexpr uint16_t kWarpVersion = 0x0101;
 
 void put_u16(uint8_t *p, uint16_t v) {
     p[0] = (uint8_t)v;
@@ -25,18 +22,10 @@ void put_u16(uint8_t *p, uint16_t v) {
 void put_u32(uint8_t *p, uint32_t v) {
     for (int i = 0; i < 4; ++i) p[i] = (uint8_t)(v >> (8 * i));
 }
-void put_u64(uint8_t *p, uint64_t v) {
-    for (int i = 0; i < 8; ++i) p[i] = (uint8_t)(v >> (8 * i));
-}
 uint16_t get_u16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 uint32_t get_u32(const uint8_t *p) {
     uint32_t v = 0;
     for (int i = 0; i < 4; ++i) v |= (uint32_t)p[i] << (8 * i);
-    return v;
-}
-uint64_t get_u64(const uint8_t *p) {
-    uint64_t v = 0;
-    for (int i = 0; i < 8; ++i) v |= (uint64_t)p[i] << (8 * i);
     return v;
 }
 
@@ -149,34 +138,6 @@ int air_kv_int8_payload_serialise_n(const uint32_t *block_ids, uint16_t layer_id
     for (int32_t i = 0; i < n; ++i)
         int8_payload(o + (size_t)i * (kInt8Header + codes_per_block), block_ids[i], layer_idx, scales[i],
                      codes + (size_t)i * codes_per_block, (uint32_t)codes_per_block);
-    return AIR_KV_OK;
-}
-
-int air_kv_stream_record_header(uint64_t seq_id, uint32_t payload_len, uint8_t out[12]) {
-    if (!out) return fail(AIR_KV_E_INVALID_ARG, "record header: NULL buffer");
-    put_u64(out, seq_id);
-    put_u32(out + 8, payload_len);
-    return AIR_KV_OK;
-}
-
-int air_kv_warp_header_serialise(uint64_t features, uint32_t body_len, uint8_t out[18]) {
-    if (!out) return fail(AIR_KV_E_INVALID_ARG, "warp header: NULL buffer");
-    std::memcpy(out, kWarpMagic, 4);
-    put_u16(out + 4, kWarpVersion);
-    put_u64(out + 6, features);
-    put_u32(out + 14, body_len);
-    return AIR_KV_OK;
-}
-
-int air_kv_warp_header_deserialise(const uint8_t *buf, size_t len, uint64_t *features, uint32_t *body_len,
-                                   uint16_t *version) {
-    if (!buf || len < 18) return fail(AIR_KV_E_INVALID_ARG, "warp header: %zu bytes, 18 needed", len);
-    if (std::memcmp(buf, kWarpMagic, 4) != 0) return fail(AIR_KV_E_INVALID_ARG, "Invalid WARP magic");
-    const uint16_t v = get_u16(buf + 4);
-    if ((v >> 8) != (kWarpVersion >> 8)) return fail(AIR_KV_E_INVALID_ARG, "Incompatible WARP major version");
-    if (version) *version = v;
-    if (features) *features = get_u64(buf + 6);
-    if (body_len) *body_len = get_u32(buf + 14);
     return AIR_KV_OK;
 }
 

@@ -487,15 +487,6 @@ int air_kv_int8_payload_deserialise(const void *buf, size_t len, uint32_t *block
  * (copied to the host): n * (14 + codes_per_block) bytes. */
 int air_kv_int8_payload_serialise_n(const uint32_t *block_ids, uint16_t layer_idx, const float *scales,
                                     const int8_t *codes, size_t codes_per_block, int32_t n, void *out);
-/* The per-payload record header of the TCP / RDMA streams
- * (src/pd_disagg.rs:277-279, :539-541): [seq_id:8][payload_len:4]. */
-int air_kv_stream_record_header(uint64_t seq_id, uint32_t payload_len, uint8_t out[12]);
-/* WarpHeader::serialise / deserialise (src/warp_protocol.rs:30-63):
- * ["WARP"][version:2 = 0x0101][features:8][body_len:4]; deserialise rejects
- * another magic or major version with AIR_KV_E_INVALID_ARG. */
-int air_kv_warp_header_serialise(uint64_t features, uint32_t body_len, uint8_t out[18]);
-int air_kv_warp_header_deserialise(const uint8_t *buf, size_t len, uint64_t *features, uint32_t *body_len,
-                                   uint16_t *version);
 
 /* ------------------------------------------------------------------------ */
 /* kv_compress warm-tier codecs (src/kv_compress.rs)                          */

@@ -67,7 +67,6 @@ def lib():
                 "orc_kvblock_serialise": (_SZ, [ctypes.c_uint32, ctypes.c_uint16, _P, ctypes.c_uint32, _P]),
                 "orc_kvblock_deserialise": (_i32, [_P, _SZ, _P, _P, _P]),
                 "orc_tcp_int8_payload": (_SZ, [ctypes.c_uint32, ctypes.c_uint16, _P, _SZ, _P]),
-                "orc_warp_header_serialise": (None, [_u64, ctypes.c_uint32, _P]),
                 "orc_kv_append": (_i32, [_i32, _i32, _i32, _i32, _i32, _i64, _P, _P, _P, _i32,
                                          _P, _P, _P, _P]),
                 "orc_kv_gather": (_i32, [_i32, _i32, _i32, _i32, _i32, _i64, _P, _P, _P, _P,
@@ -224,12 +223,6 @@ def tcp_int8_payload(block_id, layer_idx, bf16_bits) -> bytes:
     out = np.empty(14 + len(b), np.uint8)
     n = lib().orc_tcp_int8_payload(block_id, layer_idx, _ptr(b), len(b), _ptr(out))
     return out[:n].tobytes()
-
-
-def warp_header_serialise(features, body_len) -> bytes:
-    out = np.empty(18, np.uint8)
-    lib().orc_warp_header_serialise(features, body_len, _ptr(out))
-    return out.tobytes()
 
 
 # --------------------------------------------------------------------------

@@ -243,15 +243,6 @@ size_t orc_tcp_int8_payload(uint32_t block_id, uint16_t layer_idx, const uint16_
     return o + n;
 }
 
-/* WarpHeader::serialise, src/warp_protocol.rs:30-38: "WARP", version 0x0101,
- * features, body_len, little-endian; 18 bytes. */
-void orc_warp_header_serialise(uint64_t features, uint32_t body_len, uint8_t *out) {
-    out[0] = 'W'; out[1] = 'A'; out[2] = 'R'; out[3] = 'P';
-    out[4] = 0x01; out[5] = 0x01;
-    for (int i = 0; i < 8; ++i) out[6 + i] = (uint8_t)(features >> (8 * i));
-    for (int i = 0; i < 4; ++i) out[14 + i] = (uint8_t)(body_len >> (8 * i));
-}
-
 /* ------------------------------------------------------------------------ */
 /* Paged pool: append and gather                                            */
 /* ------------------------------------------------------------------------ */

@@ -53,7 +53,6 @@ int orc_kvblock_deserialise(const uint8_t *buf, size_t len, uint32_t *block_id, 
                             uint32_t *data_len);
 size_t orc_tcp_int8_payload(uint32_t block_id, uint16_t layer_idx, const uint16_t *bf16, size_t n,
                             uint8_t *out);
-void orc_warp_header_serialise(uint64_t features, uint32_t body_len, uint8_t *out);
 
 /* ---- paged pool operations (definitional) -------------------------------- */
 /* Append n_tokens rows src[t][h][d] (f32) into the pool at slot_mapping[t].

@@ -1,5 +1,5 @@
-"""KvBlock framing on the host (src/pd_disagg.rs:39-104, :267-279;
-src/warp_protocol.rs:25-63): the product's C ABI against the oracle's
+"""KvBlock framing on the host (src/pd_disagg.rs:39-104, :267-276): the
+product's C ABI against the oracle's
 restatement, byte for byte, and the reference's own wire tests restated.
 CPU only (the GPU side -- frames of device-packed pages -- is in
 test_gpu_wire.py)."""
@@ -115,18 +115,3 @@ def test_reference_receiver_misreads_int8_payloads():
     raw = oracle.tcp_int8_payload(9, 1, bits)
     assert oracle.kvblock_deserialise(raw) is None
     assert pd_wire.parse_int8_payload(raw)[0] == 9
-
-
-# --- W.A.R.P. header ---------------------------------------------------------
-
-def test_warp_header_roundtrip_and_checks():
-    f = (1 << 1) | (1 << 3)            # Int8Quantization | AsyncPipelining, as send_blocks sets
-    raw = pd_wire.warp_header(f, 5)
-    assert raw == oracle.warp_header_serialise(f, 5)
-    assert raw[:4] == b"WARP" and raw[4:6] == b"\x01\x01" and len(raw) == 18
-    assert pd_wire.parse_warp_header(raw) == (f, 5, 0x0101)
-    with pytest.raises(airkv.AirKvError):
-        pd_wire.parse_warp_header(b"XARP" + raw[4:])
-    with pytest.raises(airkv.AirKvError):
-        pd_wire.parse_warp_header(raw[:4] + b"\x01\x02" + raw[6:])    # major version 2
-    assert pd_wire.parse_warp_header(raw[:4] + b"\x07\x01" + raw[6:])[2] == 0x0107   # minor differs: accepted
