@@ -185,6 +185,43 @@ __global__ __launch_bounds__(kThreads) void mix21_persist_kernel(const u32x4 *sr
     }
 }
 
+// One-shot forms with other bytes per thread: U 16-byte loads a wave apart
+// (U = 2: 32 B, 8: 128 B, 16: 256 B), then the thread's stores -- U for
+// copy, U / 2 for mix21 -- or U stores alone (write).
+template <bool NTL, bool NTS, int U, int MODE>   // MODE 0 copy, 1 mix21, 2 write
+__global__ __launch_bounds__(kThreads) void wide_kernel(const u32x4 *src, u32x4 *dst, int64_t n16) {
+    const int64_t base = (int64_t)blockIdx.x * kThreads * U + threadIdx.x;
+    if (base + (U - 1) * kThreads >= n16) return;
+    if constexpr (MODE == 2) {
+        const u32x4 v = {0x5bd1e995u, (uint32_t)base, 7u, 11u};
+#pragma unroll
+        for (int i = 0; i < U; ++i) st16<NTS>(dst + base + i * kThreads, v);
+        return;
+    }
+    u32x4 v[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) v[i] = ld16<NTL>(src + base + i * kThreads);
+    if constexpr (MODE == 0) {
+#pragma unroll
+        for (int i = 0; i < U; ++i) st16<NTS>(dst + base + i * kThreads, v[i]);
+    } else {
+        const int64_t obase = (int64_t)blockIdx.x * kThreads * (U / 2) + threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < U / 2; ++i) st16<NTS>(dst + obase + i * kThreads, v[2 * i] ^ v[2 * i + 1]);
+    }
+}
+
+template <int U, int MODE>
+void launch_wide(bool ntl, bool nts, hipStream_t s, const u32x4 *in, u32x4 *out, int64_t n16) {
+    const dim3 g((unsigned)(n16 / (kThreads * U))), b(kThreads);
+#define AIRKV_WIDE(L, S) hipLaunchKernelGGL((wide_kernel<L, S, U, MODE>), g, b, 0, s, in, out, n16)
+    if (ntl && nts) AIRKV_WIDE(true, true);
+    else if (ntl) AIRKV_WIDE(true, false);
+    else if (nts) AIRKV_WIDE(false, true);
+    else AIRKV_WIDE(false, false);
+#undef AIRKV_WIDE
+}
+
 template <int U>
 void launch_persist(bool mix, bool ntl, bool nts, dim3 g, dim3 b, hipStream_t s, const u32x4 *in, u32x4 *out,
                     int64_t n16) {
@@ -214,7 +251,9 @@ extern "C" {
 // the page list), 5 page_copy (as page_read, written to `sink`, which holds
 // 2 * n_pages * 4 KB), 6 page_mix21 (src holds 2 * n_pages * 8 KB of rows,
 // dst = K pool, sink = V pool), 7 / 8 persistent copy with 128 / 256 B in
-// flight per thread, 9 / 10 persistent mix21 likewise.  nt_load / nt_store
+// flight per thread, 9 / 10 persistent mix21 likewise, 11 / 12 / 13 one-shot
+// copy with 32 / 128 / 256 B per thread, 14 one-shot mix21 with 128 B read
+// per thread, 15 / 16 write with 32 / 128 B per thread.  nt_load / nt_store
 // pick the non-temporal variants.
 // Returns 0 or the hipError_t of the launch.
 int air_ceiling_launch(int kind, int nt_load, int nt_store, const void *src, void *dst, int64_t bytes,
@@ -304,6 +343,12 @@ int air_ceiling_launch(int kind, int nt_load, int nt_store, const void *src, voi
         else launch_persist<16>(mix, nt_load, nt_store, gp, b, s, in, out, n16);
         break;
     }
+    case 11: launch_wide<2, 0>(nt_load, nt_store, s, in, out, n16); break;
+    case 12: launch_wide<8, 0>(nt_load, nt_store, s, in, out, n16); break;
+    case 13: launch_wide<16, 0>(nt_load, nt_store, s, in, out, n16); break;
+    case 14: launch_wide<8, 1>(nt_load, nt_store, s, in, out, n16); break;
+    case 15: launch_wide<2, 2>(nt_load, nt_store, s, in, out, n16); break;
+    case 16: launch_wide<8, 2>(nt_load, nt_store, s, in, out, n16); break;
     default:
         return (int)hipErrorInvalidValue;
     }

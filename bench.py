@@ -148,9 +148,11 @@ def ceilings_leg(torch, iters=20):
     (4 KB K and V pages in a shuffled order, one wave per page), and
     page_copy (half of those pages copied to consecutive 4 KB slots: the
     gather's pattern) and page_mix21 (a quarter of them written from 8 KB
-    of contiguous rows each: the append's pattern).  Each
-    pattern runs with plain and non-temporal loads / stores; the faster is
-    kept, with its variant."""
+    of contiguous rows each: the append's pattern).  Copy, mix21 and write
+    also run with 32 to 256 bytes per thread, as persistent grid-stride
+    loops (copy, mix21) and as the runtime's device copy; `*_best` is the
+    fastest form.  Each pattern runs with plain and non-temporal loads /
+    stores; the faster is kept, with its variant."""
     import ctypes
 
     import numpy as np
@@ -184,6 +186,12 @@ def ceilings_leg(torch, iters=20):
         "copy_persist256": (8, 2 * nbytes, (0, 1), (0, 1), 0),
         "mix21_persist128": (9, nbytes + nbytes // 2, (0, 1), (0, 1), 0),
         "mix21_persist256": (10, nbytes + nbytes // 2, (0, 1), (0, 1), 0),
+        "copy_w32": (11, 2 * nbytes, (0, 1), (0, 1), 0),
+        "copy_w128": (12, 2 * nbytes, (0, 1), (0, 1), 0),
+        "copy_w256": (13, 2 * nbytes, (0, 1), (0, 1), 0),
+        "mix21_w128": (14, nbytes + nbytes // 2, (0, 1), (0, 1), 0),
+        "write_w32": (15, nbytes, (0,), (0, 1), 0),
+        "write_w128": (16, nbytes, (0,), (0, 1), 0),
     }
     out = {}
     for name, (kind, moved, lds, sts, npg) in kinds.items():
@@ -224,9 +232,12 @@ def ceilings_leg(torch, iters=20):
     gbps = 2 * nbytes / (ms * 1e-3) / 1e9
     out["memcpy_d2d"] = {"gbps": round(gbps, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4), "variant": "hipMemcpyAsync"}
     # best of each pattern over its one-shot, persistent and runtime forms
-    out["copy_best"] = max((out[k] | {"form": k} for k in ("copy", "copy_persist128", "copy_persist256",
-                                                           "memcpy_d2d")), key=lambda r: r["gbps"])
-    out["mix21_best"] = max((out[k] | {"form": k} for k in ("mix21", "mix21_persist128", "mix21_persist256")),
+    out["copy_best"] = max((out[k] | {"form": k} for k in ("copy", "copy_w32", "copy_w128", "copy_w256",
+                                                           "copy_persist128", "copy_persist256", "memcpy_d2d")),
+                           key=lambda r: r["gbps"])
+    out["mix21_best"] = max((out[k] | {"form": k} for k in ("mix21", "mix21_w128", "mix21_persist128",
+                                                            "mix21_persist256")), key=lambda r: r["gbps"])
+    out["write_best"] = max((out[k] | {"form": k} for k in ("write", "write_w32", "write_w128")),
                             key=lambda r: r["gbps"])
     del a, b, pc_out
     return out
