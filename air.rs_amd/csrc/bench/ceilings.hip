@@ -113,6 +113,27 @@ __global__ __launch_bounds__(kThreads) void page_read_kernel(const u32x4 *k, con
     if (x == 0x9E3779B9u && lane == 7) sink[0] = x;
 }
 
+// 2 KB pages (the int8 decode's per-head run at block size 16): one wave per
+// page, 32 B per lane.  GROUP = 1: pages[] lists 2 KB pages in a shuffled
+// order; GROUP = 8: pages[] lists 16 KB blocks in a shuffled order and eight
+// consecutive waves read the block's eight 2 KB pieces (as the decode's
+// waves read the kv heads of one block).
+template <bool NT, int GROUP>
+__global__ __launch_bounds__(kThreads) void page_read2k_kernel(const u32x4 *k, const u32x4 *v, const int32_t *pages,
+                                                               int64_t n_list, int64_t pool_pages2k, uint32_t *sink) {
+    const int64_t item = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);   // (entry, piece, K|V)
+    if (item >= 2 * GROUP * n_list) return;
+    const int lane = threadIdx.x & 63;
+    const int64_t e = item / (2 * GROUP);
+    const int piece = (int)((item >> 1) % GROUP);
+    const int64_t pg = (int64_t)pages[e] * GROUP + piece;          // 2 KB page index
+    if (pg < 0 || pg >= pool_pages2k) return;
+    const u32x4 *base = ((item & 1) ? v : k) + pg * 128 + lane;
+    const u32x4 a = ld16<NT>(base), b = ld16<NT>(base + 64);
+    const uint32_t x = fold(a, b, a, b) ^ a[0];
+    if (x == 0x9E3779B9u && lane == 7) sink[0] = x;
+}
+
 // The gather's pattern: 4 KB pages read in a shuffled order and written to
 // consecutive 4 KB slots of an output, one wave per page (K pool pages to
 // the first half of `out`, V pool pages to the second half).
@@ -253,8 +274,10 @@ extern "C" {
 // dst = K pool, sink = V pool), 7 / 8 persistent copy with 128 / 256 B in
 // flight per thread, 9 / 10 persistent mix21 likewise, 11 / 12 / 13 one-shot
 // copy with 32 / 128 / 256 B per thread, 14 one-shot mix21 with 128 B read
-// per thread, 15 / 16 write with 32 / 128 B per thread.  nt_load / nt_store
-// pick the non-temporal variants.
+// per thread, 15 / 16 write with 32 / 128 B per thread, 17 page_read of
+// 2 KB pages (pages: a shuffled list of the pools' 2 KB pages), 18 the same
+// pages read eight at a time from shuffled 16 KB blocks (pages: a shuffled
+// list of blocks).  nt_load / nt_store pick the non-temporal variants.
 // Returns 0 or the hipError_t of the launch.
 int air_ceiling_launch(int kind, int nt_load, int nt_store, const void *src, void *dst, int64_t bytes,
                        const int32_t *pages, int64_t n_pages, void *sink, void *stream) {
@@ -341,6 +364,22 @@ int air_ceiling_launch(int kind, int nt_load, int nt_store, const void *src, voi
         const bool mix = kind >= 9;
         if (kind == 7 || kind == 9) launch_persist<8>(mix, nt_load, nt_store, gp, b, s, in, out, n16);
         else launch_persist<16>(mix, nt_load, nt_store, gp, b, s, in, out, n16);
+        break;
+    }
+    case 17:   // 2 KB pages (pages / n_pages: a shuffled list of 2 KB pages)
+    case 18: { // 16 KB blocks (pages / n_pages: a shuffled list of blocks), 8 waves a block
+        const int grp = kind == 17 ? 1 : 8;
+        if (!pages || n_pages <= 0 || n_pages * 2048 * grp > bytes) return (int)hipErrorInvalidValue;
+        const dim3 gp((unsigned)((2 * grp * n_pages + kThreads / 64 - 1) / (kThreads / 64)));
+        const int64_t pool2k = bytes / 2048;
+        const u32x4 *vv = (const u32x4 *)dst;
+        if (kind == 17) {
+            if (nt_load) hipLaunchKernelGGL((page_read2k_kernel<true, 1>), gp, b, 0, s, in, vv, pages, n_pages, pool2k, sk);
+            else hipLaunchKernelGGL((page_read2k_kernel<false, 1>), gp, b, 0, s, in, vv, pages, n_pages, pool2k, sk);
+        } else {
+            if (nt_load) hipLaunchKernelGGL((page_read2k_kernel<true, 8>), gp, b, 0, s, in, vv, pages, n_pages, pool2k, sk);
+            else hipLaunchKernelGGL((page_read2k_kernel<false, 8>), gp, b, 0, s, in, vv, pages, n_pages, pool2k, sk);
+        }
         break;
     }
     case 11: launch_wide<2, 0>(nt_load, nt_store, s, in, out, n16); break;

@@ -148,7 +148,10 @@ def ceilings_leg(torch, iters=20):
     (4 KB K and V pages in a shuffled order, one wave per page), and
     page_copy (half of those pages copied to consecutive 4 KB slots: the
     gather's pattern) and page_mix21 (a quarter of them written from 8 KB
-    of contiguous rows each: the append's pattern).  Copy, mix21 and write
+    of contiguous rows each: the append's pattern), page_read2k (2 KB pages
+    in a shuffled order: the int8 decode's per-head run at block size 16)
+    and block_read2k (the same pages, eight consecutive waves reading the
+    eight pieces of one shuffled 16 KB block).  Copy, mix21 and write
     also run with 32 to 256 bytes per thread, as persistent grid-stride
     loops (copy, mix21) and as the runtime's device copy; `*_best` is the
     fastest form.  Each pattern runs with plain and non-temporal loads /
@@ -171,6 +174,10 @@ def ceilings_leg(torch, iters=20):
     half = pages[: nbytes // 8192].contiguous()
     # page_mix21: a quarter of each pool's pages written from 1 GiB of rows
     quarter = pages[: nbytes // 16384].contiguous()
+    # 2 KB pages (the int8 decode's per-head run at block size 16), and 16 KB
+    # blocks whose eight 2 KB pieces consecutive waves read
+    pages2k = torch.from_numpy(np.random.default_rng(14).permutation(nbytes // 2048).astype(np.int32)).cuda()
+    blocks16k = torch.from_numpy(np.random.default_rng(15).permutation(nbytes // 16384).astype(np.int32)).cuda()
     pc_out = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
@@ -192,6 +199,8 @@ def ceilings_leg(torch, iters=20):
         "mix21_w128": (14, nbytes + nbytes // 2, (0, 1), (0, 1), 0),
         "write_w32": (15, nbytes, (0,), (0, 1), 0),
         "write_w128": (16, nbytes, (0,), (0, 1), 0),
+        "page_read2k": (17, 2 * nbytes, (0, 1), (0,), nbytes // 2048),
+        "block_read2k": (18, 2 * nbytes, (0, 1), (0,), nbytes // 16384),
     }
     out = {}
     for name, (kind, moved, lds, sts, npg) in kinds.items():
@@ -203,6 +212,8 @@ def ceilings_leg(torch, iters=20):
                         args = (P(a), P(b), P(half), P(pc_out))
                     elif kind == 6:    # rows in pc_out -> K / V pools a, b
                         args = (P(pc_out), P(a), P(quarter), P(b))
+                    elif kind in (17, 18):
+                        args = (P(a), P(b), P(pages2k if kind == 17 else blocks16k), P(sink))
                     else:
                         args = (P(a), P(b), P(pages) if npg else None, P(sink))
                     rc = lib.air_ceiling_launch(kind, ntl, nts, args[0], args[1], nbytes, args[2], npg, args[3],
