@@ -14,6 +14,7 @@
 
 #include "../pool.hpp"
 #include "codecs.hpp"
+#include "fastdiv.hpp"
 #include "page_io.hpp"
 
 namespace airkv {
@@ -34,6 +35,11 @@ struct AppendArgs {
     void *k_pages, *v_pages;
     float *k_scales, *v_scales;
     unsigned long long *errors;
+    // a launch's work-items count in 32 bits; its divisions by head_dim / 8
+    // and n_kv_heads are invariant-divisor multiplies, the power-of-two
+    // block size and scale group shifts
+    FastDiv chunks_div, heads_div;
+    int32_t bs_log2, sg_log2;
 };
 
 // F32 / BF16 pages, head_dim 128: each wave covers four consecutive tokens of
@@ -47,9 +53,10 @@ __global__ __launch_bounds__(kThreads) void kv_append_rows_kernel(AppendArgs a) 
     static_assert(DT == AIR_KV_F32 || DT == AIR_KV_BF16, "unquantized pages");
     constexpr int D = 128;
     const int lane = threadIdx.x & 63;
-    const int64_t wave_g = ((int64_t)blockIdx.x * kThreads + threadIdx.x) >> 6;   // (token group of 4, head)
-    const int h = (int)(wave_g % a.n_kv_heads);
-    const int64_t t0 = (wave_g / a.n_kv_heads) * 4;
+    const uint32_t wave_g = (blockIdx.x * kThreads + threadIdx.x) >> 6;   // (token group of 4, head)
+    const uint32_t tg = fast_div(wave_g, a.heads_div);
+    const int h = (int)(wave_g - tg * (uint32_t)a.n_kv_heads);
+    const int64_t t0 = (int64_t)tg * 4;
     f32x4 kx[2], vx[2];
     int64_t dst[2];
     bool ok[2];
@@ -65,8 +72,8 @@ __global__ __launch_bounds__(kThreads) void kv_append_rows_kernel(AppendArgs a) 
         const int64_t src = (active ? t * a.n_kv_heads + h : 0) * D + col;
         kx[half] = active ? __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a.k + src)) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         vx[half] = active ? __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a.v + src)) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        const int64_t blk = ok[half] ? slot / a.block_size : 0;
-        const int64_t off = ok[half] ? slot - blk * a.block_size : 0;
+        const int64_t blk = ok[half] ? slot >> a.bs_log2 : 0;
+        const int64_t off = ok[half] ? slot & (a.block_size - 1) : 0;
         dst[half] = ((blk * a.n_kv_heads + h) * a.block_size + off) * D + col;
     }
 #pragma unroll
@@ -93,14 +100,15 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(AppendArgs a) {
     // 4 * chunks consecutive threads (a wave at head_dim 128) cover four
     // consecutive tokens of one head, whose page rows are one contiguous run
     // when the tokens share a block (prefill chunks)
-    const int chunks = a.head_dim >> 3;
-    const int64_t gid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    const int c = (int)(gid % chunks);
-    const int64_t rest = gid / chunks;
+    const uint32_t chunks = (uint32_t)a.head_dim >> 3;
+    const uint32_t gid = blockIdx.x * kThreads + threadIdx.x;
+    const uint32_t rest = fast_div(gid, a.chunks_div);
+    const int c = (int)(gid - rest * chunks);
     const int tl = (int)(rest & 3);
-    const int64_t rest2 = rest >> 2;
-    const int h = (int)(rest2 % a.n_kv_heads);
-    const int64_t t = (rest2 / a.n_kv_heads) * 4 + tl;
+    const uint32_t rest2 = rest >> 2;
+    const uint32_t tq = fast_div(rest2, a.heads_div);
+    const int h = (int)(rest2 - tq * (uint32_t)a.n_kv_heads);
+    const int64_t t = (int64_t)tq * 4 + tl;
     const bool active = t < a.n_tokens;
     const int64_t row = t * a.n_kv_heads + h;
     const int64_t slot = active ? a.slots[t] : -1;
@@ -125,8 +133,8 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(AppendArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) kx[j] = vx[j] = 0.0f;
     }
-    const int64_t blk = valid ? slot / a.block_size : 0;
-    const int64_t off = valid ? slot - blk * a.block_size : 0;
+    const int64_t blk = valid ? slot >> a.bs_log2 : 0;
+    const int64_t off = valid ? slot & (a.block_size - 1) : 0;
     const int64_t dst_row = (blk * a.n_kv_heads + h) * a.block_size + off;
     const int64_t elem = dst_row * a.head_dim + c * 8;
     int lanes_per_group = 1;
@@ -134,8 +142,8 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(AppendArgs a) {
     bool lead = false;
     if constexpr (DT == AIR_KV_INT8 || DT == AIR_KV_FP8) {
         lanes_per_group = a.scale_group >> 3;
-        scale_idx = dst_row * (a.head_dim / a.scale_group) + (c * 8) / a.scale_group;
-        lead = (c % lanes_per_group) == 0;
+        scale_idx = dst_row * (a.head_dim >> a.sg_log2) + ((c * 8) >> a.sg_log2);
+        lead = (c & (lanes_per_group - 1)) == 0;
     }
     store_row_chunk<DT>(kx, a.k_pages, a.k_scales, elem, scale_idx, lead, lanes_per_group, valid);
     store_row_chunk<DT>(vx, a.v_pages, a.v_scales, elem, scale_idx, lead, lanes_per_group, valid);
@@ -154,6 +162,10 @@ hipError_t launch_append(const air_kv_pool &p, hipStream_t s, const float *k, co
     a.k_pages = p.k_pages; a.v_pages = p.v_pages;
     a.k_scales = p.k_scales; a.v_scales = p.v_scales;
     a.errors = p.errors;
+    a.chunks_div = make_fast_div((uint32_t)p.desc.head_dim / 8);
+    a.heads_div = make_fast_div((uint32_t)p.desc.n_kv_heads);
+    a.bs_log2 = __builtin_ctz((unsigned)p.desc.block_size);              // 16 or 32
+    a.sg_log2 = p.desc.scale_group > 0 ? __builtin_ctz((unsigned)p.desc.scale_group) : 0;   // a power of two
     // a dispatch counts its work-items in 32 bits: long appends take several
     // launches of at most kMaxBlocks workgroups, each a whole number of
     // four-token groups
