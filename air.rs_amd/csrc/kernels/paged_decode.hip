@@ -132,7 +132,11 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     const bool cv = chunk * 8 < d;              // the lane's 8 elements lie inside head_dim
     const int row_in_pass = wave * RPW + lane / LPR;
     const int ng = QUANT ? d / a.scale_group : 1;
-    const int sg = QUANT ? a.scale_group : 1;
+    // block sizes (16, 32) and scale groups are powers of two: the per-row
+    // index arithmetic below shifts and masks instead of dividing
+    const int bs_log2 = __builtin_ctz((unsigned)a.block_size);
+    const int64_t bs_mask = a.block_size - 1;
+    const int sg_log2 = QUANT ? __builtin_ctz((unsigned)a.scale_group) : 0;
     const int32_t *table = a.tables + (int64_t)b * a.max_blocks;
 
     float qr[G][8];                             // this lane's 8 elements of each query row, f32
@@ -187,19 +191,19 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
                 const int r = ps * RPP + row_in_pass;
                 const int64_t t = t0 + r;
                 bool ok = t < end;
-                int32_t blk = ok ? table[t / a.block_size] : 0;
+                int32_t blk = ok ? table[t >> bs_log2] : 0;
                 bool in_pool = true;
                 if (ok && (blk < 0 || blk >= a.num_blocks)) {
                     in_pool = false;
                     ok = oob_zero;
                     if (chunk == 0 && (count == kCountRows ||
-                                       (count == kCountBlocks && (t % a.block_size == 0 || t == start))))
+                                       (count == kCountBlocks && ((t & bs_mask) == 0 || t == start))))
                         atomicAdd(a.errors, 1ull);
                 }
                 Raw8<DT> kraw;
                 if (ok && cv && in_pool) {
-                    const int64_t row = ((int64_t)blk * a.n_kv_heads + kh) * a.block_size + t % a.block_size;
-                    const int64_t sidx = row * ng + (chunk * 8) / sg;
+                    const int64_t row = ((int64_t)blk * a.n_kv_heads + kh) * a.block_size + (t & bs_mask);
+                    const int64_t sidx = row * ng + ((chunk * 8) >> sg_log2);
                     load_raw<DT>(a.k_pages, a.k_scales, row * d + chunk * 8, sidx, kraw);
                     load_raw<DT>(a.v_pages, a.v_scales, row * d + chunk * 8, sidx, vraw[ps]);
                 } else {
