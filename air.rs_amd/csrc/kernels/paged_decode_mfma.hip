@@ -87,7 +87,7 @@ constexpr int kMinChunk = 4;               // tiles per slice at least
 #define AIRKV_DECODE_K16 1                 // 1-byte pages: K as 16-byte loads re-paired across lanes (else 8-byte loads)
 #endif
 #ifndef AIRKV_DECODE_QNT_LOADS
-#define AIRKV_DECODE_QNT_LOADS 0           // 1-byte pages: every K/V/scale load nt (else the per-stream policy below)
+#define AIRKV_DECODE_QNT_LOADS 1           // 1-byte pages: every K/V/scale load nt (else the per-stream policy below)
 #endif
 
 // Buffer descriptor word 3 for raw (untyped) buffer access on gfx9-class
@@ -98,10 +98,12 @@ constexpr int kMinChunk = 4;               // tiles per slice at least
 constexpr int kBufferWord3 = 0x00020000;
 constexpr int kLoadAux = AIRKV_DECODE_NT_LOADS ? 2 : 0;
 
-// 1-byte pages pick the policy per stream (whole c3 / c4 call, three runs
-// each, one box): nt scale loads 124.0 -> 120.6 us (c3) and 371.2 -> 360.7 us
-// (c4); nt int8 K loads on top 119.4 us for c3, while nt fp8 K loads gave
-// c4 367.7 us; nt V loads were slower on both (125.0 and 413 us).
+// 1-byte pages: every code and scale load is nt now that each load
+// instruction reads whole rows.  With instructions that read half of every
+// row, the policy had to be chosen per stream (nt scale loads 124.0 -> 120.6
+// us at c3, 371.2 -> 360.7 us at c4; nt fp8 K loads gave c4 367.7 us, nt V
+// loads 125.0 and 413 us), and a probe reading scattered 2 KB pages that way
+// ran at 5.1-5.3 TB/s with nt against 6.0 without.
 template <int DT> constexpr int k_code_aux() { return (AIRKV_DECODE_QNT_LOADS || DT == AIR_KV_INT8) ? 2 : 0; }
 constexpr int kVCodeAux = AIRKV_DECODE_QNT_LOADS ? 2 : 0;
 constexpr int kScaleAux = 2;
@@ -166,6 +168,29 @@ __device__ __forceinline__ float sum_x16(float x) {
 __device__ __forceinline__ float sum_x32(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Register-pair transposes: afterwards x_b in lane l holds what x_c held in
+// lane l', where c is lane l's bit 3 (bit 5) and l' is l with that bit set
+// to b.  Bit 3: DPP row_ror:8 (lane l ^ 8 within each row of 16), written
+// only to the lanes whose bit 3 differs from the register index (bank masks
+// 0xC: lanes 8..15 of each row, 0x3: lanes 0..7).  Bit 5: the lane swap
+// across the wave's halves.
+__device__ __forceinline__ void swap_lane_bit3(u32x4 &x0, u32x4 &x1) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int a = (int)x0[j], b = (int)x1[j];
+        x0[j] = (uint32_t)__builtin_amdgcn_update_dpp(a, b, 0x128, 0xF, 0xC, false);
+        x1[j] = (uint32_t)__builtin_amdgcn_update_dpp(b, a, 0x128, 0xF, 0x3, false);
+    }
+}
+__device__ __forceinline__ void swap_lane_bit5(u32x4 &x0, u32x4 &x1) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const auto r = __builtin_amdgcn_permlane32_swap(x0[j], x1[j], false, false);
+        x0[j] = r[0];
+        x1[j] = r[1];
+    }
 }
 
 __device__ __forceinline__ void store_out(const DecodeArgs &a, int64_t idx, float v) {
@@ -276,7 +301,8 @@ __device__ __forceinline__ int seq_of_tile(const int32_t *pre, int B, int t) {
 // Q8_0 codes, fp8): K in the same layout (8 codes per step: k-step ks is
 // head_dim 32*ks .. +32, one scale group), the lane's own K row scale (row
 // r16, head_dim 32*g4), and 32 contiguous codes -- one scale group -- of one
-// V row with its scale.
+// V row with its scale.  (1-byte k16 and v hold the whole-row load order
+// until compute_tile transposes them into this layout.)
 template <int DT> struct Tile {
     u32x2 k[4];          // 8-byte K loads: step ks
     u32x4 k16[2];        // 16-byte K loads: head_dim 64*m + 16*g4 .. +16
@@ -529,12 +555,23 @@ void decode_mfma_kernel(DecodeArgs a) {
     const char *vp = (const char *)a.v_pages;
     uint16_t *sv = s_v + wave * VTILE;
     // Lane offsets inside a tile (loop invariant).  bf16: K as the A operand,
-    // V as 16-byte chunks of rows lane / 16 + 4 * v.  1-byte: K row r16 and V
-    // row lane / 4, 32 codes from column 32 * g4 (K) or 32 * (lane % 4) (V).
+    // V as 16-byte chunks of rows lane / 16 + 4 * v.  1-byte: compute_tile
+    // works on K row r16 and V row lane / 4, 32 codes from column 32 * g4
+    // (K) or 32 * (lane % 4) (V), but each 16-byte load instruction reads
+    // eight whole 128-byte rows: K load m gives lane l row 8m + (l & 7),
+    // 16-byte chunk 4 bit3(l) + 2 bit5(l) + bit4(l); V load i row
+    // 8i + ((l >> 2) & 7), chunk 4 bit1(l) + 2 bit0(l) + bit5(l).  One
+    // transpose of lane bit 3 (K) or 5 (V) with the load index turns that
+    // into the layout above.  (Loads reading half of every row they touch
+    // ran scattered 2 KB pages at 5.1-5.3 TB/s with the non-temporal bit,
+    // against 6.7-6.9 for whole rows.)
     const int vrow = QUANT ? lane >> 2 : lane >> 4;
     const int vcol = QUANT ? 32 * (lane & 3) : 8 * (lane & 15);
-    const int k_boff = (QUANT && AIRKV_DECODE_K16) ? r16 * D + 16 * g4 : (r16 * D + 8 * g4) * EB;
-    const int v_boff = (vrow * D + vcol) * EB;
+    const int k_boff = (QUANT && AIRKV_DECODE_K16)
+                           ? (lane & 7) * D + 16 * (4 * ((lane >> 3) & 1) + 2 * ((lane >> 5) & 1) + ((lane >> 4) & 1))
+                           : (r16 * D + 8 * g4) * EB;
+    const int v_boff = QUANT ? ((lane >> 2) & 7) * D + 16 * (4 * ((lane >> 1) & 1) + 2 * (lane & 1) + ((lane >> 5) & 1))
+                             : (vrow * D + vcol) * EB;
     const int n_sc = QUANT ? D / a.scale_group : 0;              // scales per row
     const int k_soff = QUANT ? (r16 * n_sc + (32 * g4) / a.scale_group) * 4 : 0;
     const int v_soff = QUANT ? (vrow * n_sc + vcol / a.scale_group) * 4 : 0;
@@ -603,7 +640,7 @@ void decode_mfma_kernel(DecodeArgs a) {
             if constexpr (AIRKV_DECODE_K16) {
 #pragma unroll
                 for (int m = 0; m < 2; ++m)
-                    t.k16[m] = __builtin_amdgcn_raw_buffer_load_b128(rk, k_boff + 64 * m, 0, k_code_aux<DT>());
+                    t.k16[m] = __builtin_amdgcn_raw_buffer_load_b128(rk, k_boff + 8 * D * m, 0, k_code_aux<DT>());
             } else {
 #pragma unroll
                 for (int ks = 0; ks < KSTEPS; ++ks)
@@ -611,7 +648,7 @@ void decode_mfma_kernel(DecodeArgs a) {
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i)
-                t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, v_boff + 16 * i, 0, kVCodeAux);
+                t.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, v_boff + 8 * D * i, 0, kVCodeAux);
             const int64_t srow = row0 * n_sc;
             const __amdgpu_buffer_rsrc_t rks = __builtin_amdgcn_make_buffer_rsrc(
                 (void *)(a.k_scales + srow), (short)0, 16 * n_sc * 4, kBufferWord3);
@@ -687,6 +724,12 @@ void decode_mfma_kernel(DecodeArgs a) {
         // consumed on all paths and the loads in flight never need draining.
         if (!ok && lane == 0) atomicAdd(a.errors, 1ull);
         const int nv = ok ? __builtin_amdgcn_readlane(nv_l, idx) : 0;   // valid tokens
+        if constexpr (QUANT) {
+            // the whole-row load order into the Tile layout (V here only for
+            // the fused append, which replaces a row first; else at its use)
+            if constexpr (AIRKV_DECODE_K16) swap_lane_bit3(t.k16[0], t.k16[1]);
+            if constexpr (APPEND) swap_lane_bit5(t.v[0], t.v[1]);
+        }
         if constexpr (APPEND && QUANT) {
             // Fused append, 1-byte pages: the new token's codes and scales,
             // quantized and written to the page by load_tile, move by lane
@@ -859,6 +902,7 @@ void decode_mfma_kernel(DecodeArgs a) {
         // V tile -> LDS as bf16 (token rows beyond the sequence are zeroed: p = 0
         // there, but stale page bytes may hold non-finite values)
         if constexpr (QUANT) {
+            if constexpr (!APPEND) swap_lane_bit5(t.v[0], t.v[1]);
             const float vsc = __uint_as_float(t.vs);
             const bool live = full || vrow < nv;
             u32x2 *dst = reinterpret_cast<u32x2 *>(sv + vrow * PITCH);
