@@ -94,7 +94,25 @@ __global__ __launch_bounds__(kThreads) void kv_append_rows_kernel(AppendArgs a) 
     }
 }
 
-template <int DT>
+// The whole-line form of the source loads below (head_dim 128: a wave is
+// four tokens of one head, lane 16 tl + c owning elements 8c .. 8c + 7 of
+// token tl): load i gives lane l 16-byte piece 2 (l & 15) + (l >> 5) of token
+// 2i + ((l >> 4) & 1)'s row, so each load instruction reads two whole
+// 512-byte rows; exchanging lane bit 5 with the load index (the lane swap
+// across the wave's halves) then leaves lane 16 tl + c holding pieces 2c and
+// 2c + 1 of token tl, the layout the quantizer works on.  With each lane
+// loading its own two pieces, every load instruction read half of every line
+// it touched.
+__device__ __forceinline__ void swap_halves(f32x4 &x0, f32x4 &x1) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x0[j]), __float_as_uint(x1[j]), false, false);
+        x0[j] = __uint_as_float(r[0]);
+        x1[j] = __uint_as_float(r[1]);
+    }
+}
+
+template <int DT, bool LINES>
 __global__ __launch_bounds__(kThreads) void kv_append_kernel(AppendArgs a) {
     // thread -> (chunk c, token t % 4, kv head h, token t / 4), chunk fastest:
     // 4 * chunks consecutive threads (a wave at head_dim 128) cover four
@@ -119,7 +137,30 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(AppendArgs a) {
     // token's row exists), so their loads overlap the slot load instead of
     // waiting for it
     float kx[8], vx[8];
-    if (active) {
+    if constexpr (LINES) {
+        // head_dim 128, whole-line loads (above); a lane loads for token
+        // 2i + ((lane >> 4) & 1) of its wave's four, which may differ from
+        // its own
+        const int lane = threadIdx.x & 63;
+        const int64_t tw = t - tl;                           // the wave's first token
+        f32x4 kr[2], vr[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int64_t ts = tw + 2 * i + ((lane >> 4) & 1);
+            const int64_t src = (ts * a.n_kv_heads + h) * 128 + 4 * (2 * (lane & 15) + (lane >> 5));
+            kr[i] = ts < a.n_tokens ? __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a.k + src))
+                                    : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            vr[i] = ts < a.n_tokens ? __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a.v + src))
+                                    : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        swap_halves(kr[0], kr[1]);
+        swap_halves(vr[0], vr[1]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            kx[j] = valid ? kr[0][j] : 0.0f; kx[4 + j] = valid ? kr[1][j] : 0.0f;
+            vx[j] = valid ? vr[0][j] : 0.0f; vx[4 + j] = valid ? vr[1][j] : 0.0f;
+        }
+    } else if (active) {
         const f32x4 *ks = reinterpret_cast<const f32x4 *>(a.k + row * a.head_dim + c * 8);
         const f32x4 *vs = reinterpret_cast<const f32x4 *>(a.v + row * a.head_dim + c * 8);
         const f32x4 k0 = __builtin_nontemporal_load(ks), k1 = __builtin_nontemporal_load(ks + 1);
@@ -185,14 +226,20 @@ hipError_t launch_append(const air_kv_pool &p, hipStream_t s, const float *k, co
         switch (p.desc.dtype) {
         case AIR_KV_F32:
             if (rows128) hipLaunchKernelGGL(kv_append_rows_kernel<AIR_KV_F32>, grid, dim3(kThreads), 0, s, c);
-            else hipLaunchKernelGGL(kv_append_kernel<AIR_KV_F32>, grid, dim3(kThreads), 0, s, c);
+            else hipLaunchKernelGGL((kv_append_kernel<AIR_KV_F32, false>), grid, dim3(kThreads), 0, s, c);
             break;
         case AIR_KV_BF16:
             if (rows128) hipLaunchKernelGGL(kv_append_rows_kernel<AIR_KV_BF16>, grid, dim3(kThreads), 0, s, c);
-            else hipLaunchKernelGGL(kv_append_kernel<AIR_KV_BF16>, grid, dim3(kThreads), 0, s, c);
+            else hipLaunchKernelGGL((kv_append_kernel<AIR_KV_BF16, false>), grid, dim3(kThreads), 0, s, c);
             break;
-        case AIR_KV_INT8: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_INT8>, grid, dim3(kThreads), 0, s, c); break;
-        default: hipLaunchKernelGGL(kv_append_kernel<AIR_KV_FP8>, grid, dim3(kThreads), 0, s, c); break;
+        case AIR_KV_INT8:
+            if (rows128) hipLaunchKernelGGL((kv_append_kernel<AIR_KV_INT8, true>), grid, dim3(kThreads), 0, s, c);
+            else hipLaunchKernelGGL((kv_append_kernel<AIR_KV_INT8, false>), grid, dim3(kThreads), 0, s, c);
+            break;
+        default:
+            if (rows128) hipLaunchKernelGGL((kv_append_kernel<AIR_KV_FP8, true>), grid, dim3(kThreads), 0, s, c);
+            else hipLaunchKernelGGL((kv_append_kernel<AIR_KV_FP8, false>), grid, dim3(kThreads), 0, s, c);
+            break;
         }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
