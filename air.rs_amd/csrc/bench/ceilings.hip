@@ -117,8 +117,12 @@ __global__ __launch_bounds__(kThreads) void page_read_kernel(const u32x4 *k, con
 // page, 32 B per lane.  GROUP = 1: pages[] lists 2 KB pages in a shuffled
 // order; GROUP = 8: pages[] lists 16 KB blocks in a shuffled order and eight
 // consecutive waves read the block's eight 2 KB pieces (as the decode's
-// waves read the kv heads of one block).
-template <bool NT, int GROUP>
+// waves read the kv heads of one block).  HALF: each load instruction reads
+// half of every 128-byte line it touches (lane (r, g) = (lane & 15, lane >> 4)
+// reads row r's bytes 16 g and 64 + 16 g), as a 1-byte decode tile whose
+// lane holds the MFMA operand layout directly would; else lane l reads bytes
+// 16 l and 1024 + 16 l (whole lines per instruction).
+template <bool NT, int GROUP, bool HALF = false>
 __global__ __launch_bounds__(kThreads) void page_read2k_kernel(const u32x4 *k, const u32x4 *v, const int32_t *pages,
                                                                int64_t n_list, int64_t pool_pages2k, uint32_t *sink) {
     const int64_t item = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);   // (entry, piece, K|V)
@@ -128,8 +132,8 @@ __global__ __launch_bounds__(kThreads) void page_read2k_kernel(const u32x4 *k, c
     const int piece = (int)((item >> 1) % GROUP);
     const int64_t pg = (int64_t)pages[e] * GROUP + piece;          // 2 KB page index
     if (pg < 0 || pg >= pool_pages2k) return;
-    const u32x4 *base = ((item & 1) ? v : k) + pg * 128 + lane;
-    const u32x4 a = ld16<NT>(base), b = ld16<NT>(base + 64);
+    const u32x4 *base = ((item & 1) ? v : k) + pg * 128 + (HALF ? (lane & 15) * 8 + (lane >> 4) : lane);
+    const u32x4 a = ld16<NT>(base), b = ld16<NT>(base + (HALF ? 4 : 64));
     const uint32_t x = fold(a, b, a, b) ^ a[0];
     if (x == 0x9E3779B9u && lane == 7) sink[0] = x;
 }
@@ -277,7 +281,8 @@ extern "C" {
 // per thread, 15 / 16 write with 32 / 128 B per thread, 17 page_read of
 // 2 KB pages (pages: a shuffled list of the pools' 2 KB pages), 18 the same
 // pages read eight at a time from shuffled 16 KB blocks (pages: a shuffled
-// list of blocks).  nt_load / nt_store pick the non-temporal variants.
+// list of blocks), 19 kind 17 with each load instruction reading half of
+// every line it touches.  nt_load / nt_store pick the non-temporal variants.
 // Returns 0 or the hipError_t of the launch.
 int air_ceiling_launch(int kind, int nt_load, int nt_store, const void *src, void *dst, int64_t bytes,
                        const int32_t *pages, int64_t n_pages, void *sink, void *stream) {
@@ -367,8 +372,9 @@ int air_ceiling_launch(int kind, int nt_load, int nt_store, const void *src, voi
         break;
     }
     case 17:   // 2 KB pages (pages / n_pages: a shuffled list of 2 KB pages)
-    case 18: { // 16 KB blocks (pages / n_pages: a shuffled list of blocks), 8 waves a block
-        const int grp = kind == 17 ? 1 : 8;
+    case 18:   // 16 KB blocks (pages / n_pages: a shuffled list of blocks), 8 waves a block
+    case 19: { // kind 17 with half of every line per load instruction
+        const int grp = kind == 18 ? 8 : 1;
         if (!pages || n_pages <= 0 || n_pages * 2048 * grp > bytes) return (int)hipErrorInvalidValue;
         const dim3 gp((unsigned)((2 * grp * n_pages + kThreads / 64 - 1) / (kThreads / 64)));
         const int64_t pool2k = bytes / 2048;
@@ -376,6 +382,11 @@ int air_ceiling_launch(int kind, int nt_load, int nt_store, const void *src, voi
         if (kind == 17) {
             if (nt_load) hipLaunchKernelGGL((page_read2k_kernel<true, 1>), gp, b, 0, s, in, vv, pages, n_pages, pool2k, sk);
             else hipLaunchKernelGGL((page_read2k_kernel<false, 1>), gp, b, 0, s, in, vv, pages, n_pages, pool2k, sk);
+        } else if (kind == 19) {
+            if (nt_load)
+                hipLaunchKernelGGL((page_read2k_kernel<true, 1, true>), gp, b, 0, s, in, vv, pages, n_pages, pool2k, sk);
+            else
+                hipLaunchKernelGGL((page_read2k_kernel<false, 1, true>), gp, b, 0, s, in, vv, pages, n_pages, pool2k, sk);
         } else {
             if (nt_load) hipLaunchKernelGGL((page_read2k_kernel<true, 8>), gp, b, 0, s, in, vv, pages, n_pages, pool2k, sk);
             else hipLaunchKernelGGL((page_read2k_kernel<false, 8>), gp, b, 0, s, in, vv, pages, n_pages, pool2k, sk);

@@ -151,7 +151,10 @@ def ceilings_leg(torch, iters=20):
     of contiguous rows each: the append's pattern), page_read2k (2 KB pages
     in a shuffled order: the int8 decode's per-head run at block size 16)
     and block_read2k (the same pages, eight consecutive waves reading the
-    eight pieces of one shuffled 16 KB block).  Copy, mix21 and write
+    eight pieces of one shuffled 16 KB block), page_read2k_halflines
+    (page_read2k with each load instruction reading half of every line it
+    touches, as the 1-byte decode's MFMA operand layout would if loaded
+    directly; the variant field says which cache policy was faster).  Copy, mix21 and write
     also run with 32 to 256 bytes per thread, as persistent grid-stride
     loops (copy, mix21) and as the runtime's device copy; `*_best` is the
     fastest form.  Each pattern runs with plain and non-temporal loads /
@@ -201,6 +204,7 @@ def ceilings_leg(torch, iters=20):
         "write_w128": (16, nbytes, (0,), (0, 1), 0),
         "page_read2k": (17, 2 * nbytes, (0, 1), (0,), nbytes // 2048),
         "block_read2k": (18, 2 * nbytes, (0, 1), (0,), nbytes // 16384),
+        "page_read2k_halflines": (19, 2 * nbytes, (0, 1), (0,), nbytes // 2048),
     }
     out = {}
     for name, (kind, moved, lds, sts, npg) in kinds.items():
@@ -212,8 +216,8 @@ def ceilings_leg(torch, iters=20):
                         args = (P(a), P(b), P(half), P(pc_out))
                     elif kind == 6:    # rows in pc_out -> K / V pools a, b
                         args = (P(pc_out), P(a), P(quarter), P(b))
-                    elif kind in (17, 18):
-                        args = (P(a), P(b), P(pages2k if kind == 17 else blocks16k), P(sink))
+                    elif kind in (17, 18, 19):
+                        args = (P(a), P(b), P(blocks16k if kind == 18 else pages2k), P(sink))
                     else:
                         args = (P(a), P(b), P(pages) if npg else None, P(sink))
                     rc = lib.air_ceiling_launch(kind, ntl, nts, args[0], args[1], nbytes, args[2], npg, args[3],
