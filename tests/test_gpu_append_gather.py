@@ -430,3 +430,35 @@ def test_bound_launchers_keep_their_tensors_alive():
     assert torch.equal(gv.view(torch.int16), want_v.view(torch.int16))
     assert torch.equal(out, want_o) and torch.equal(outp, want_p)
     assert pa.error_count() == 0 and pb.error_count() == 0
+
+
+@pytest.mark.parametrize("dtype", [airkv.INT8, airkv.FP8])
+def test_quantized_append_head_dim_128_partial_waves_and_invalid_slots(dtype):
+    """head_dim 128 quantized appends load each wave's four tokens as whole
+    source lines and hand them between lanes: token counts that leave a
+    wave partly filled, several kv heads, a skipped slot (-1) and an
+    out-of-range one must still give the oracle's pages and scales bit for
+    bit and count the out-of-range slot once."""
+    torch = torch_mod()
+    nb, bs, nkv, d = 8, 16, 3, 128
+    pool = airkv.KvPool(nb, bs, nkv, d, dtype)
+    host = oracle.HostPool(nb, bs, nkv, d, dtype, pool.scale_group)
+    pool.error_count(reset=True)
+    rng = np.random.default_rng(77 + dtype)
+    for n in (1, 2, 3, 5, 7, 13):
+        log(f"quantized append dtype={dtype} tokens={n}")
+        slots = rng.choice(nb * bs, size=n, replace=False).astype(np.int64)
+        if n >= 5:
+            slots[1] = -1
+            slots[3] = nb * bs + 5                              # outside the pool
+        k = (rng.standard_normal((n, nkv, d)) * rng.uniform(0.1, 30.0)).astype(np.float32)
+        v = (rng.standard_normal((n, nkv, d)) * rng.uniform(0.1, 30.0)).astype(np.float32)
+        pool.append(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(), torch.from_numpy(slots).cuda())
+        want_bad = host.append(k, v, slots)
+        assert pool.error_count(reset=True) == want_bad == (1 if n >= 5 else 0)
+    torch.cuda.synchronize()
+    pk, pv, ks, vs = pool.snapshot()
+    assert_bits_equal(pk, host.k, "k codes")
+    assert_bits_equal(pv, host.v, "v codes")
+    assert_bits_equal(ks.view(np.uint32), host.k_scales.view(np.uint32), "k scales")
+    assert_bits_equal(vs.view(np.uint32), host.v_scales.view(np.uint32), "v scales")
